@@ -1,0 +1,253 @@
+/*
+ * voxcpm_amd -- the C ABI of an MI355X-native (gfx950, CDNA4, wave64)
+ * implementation of VoxCPM2's per-patch DiT hot path: Q8_0-weight x
+ * bfloat16-activation products and the local diffusion transformer they
+ * drive through the Euler/CFG sampler.
+ *
+ * Conventions (all entry points):
+ *  - Every data pointer is a device pointer unless documented otherwise;
+ *    `stream` is a hipStream_t passed as void* (NULL = the null stream).
+ *    Work is enqueued on `stream` and nothing synchronizes internally
+ *    unless documented.
+ *  - The caller owns activations, outputs and weights, as the reference's
+ *    callers do (device.hpp:33-77); handles own only their scratch.
+ *  - No exception crosses the ABI. Each call returns a vx_status:
+ *    VX_UNSUPPORTED corresponds to the reference launchers returning false
+ *    ("nothing launched", kernels/wmma_products.hpp:87-89), VX_BAD_ARG to
+ *    the reference's std::invalid_argument/WeightError paths, VX_HIP_ERROR
+ *    to its GpuError (device.hpp:16-30). vx_last_error() returns the message
+ *    of the calling thread's last failure.
+ *  - bf16 values are raw bfloat16 bits (uint16_t), as in the reference
+ *    (kernels/wmma_products.hpp:26-27).
+ */
+#ifndef VOXCPM_AMD_H_
+#define VOXCPM_AMD_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef enum vx_status {
+  VX_OK = 0,
+  VX_UNSUPPORTED = 1,
+  VX_BAD_ARG = 2,
+  VX_HIP_ERROR = 3,
+} vx_status;
+
+/* The calling thread's last failure message ("" after success). */
+const char* vx_last_error(void);
+/* The hipError_t of the calling thread's last VX_HIP_ERROR (0 if none). */
+int vx_last_hip_error(void);
+/* Library version string. */
+const char* vx_version(void);
+
+/* ------------------------------------------------------------------------
+ * Q8_0 weights in the gfx950 panel layout.
+ *
+ * GGML Q8_0 stores a [n][k] matrix as blocks of 34 bytes (float16 scale,
+ * then 32 int8 values) along k. The panel layout keeps every value and
+ * scale exactly and orders them for 64-lane MFMA operands: 16 weight rows
+ * x 64 columns (two blocks) per 1088-byte unit, 16 bytes per lane, then the
+ * 16 rows' pairs of float16 scales; units run along k, then down the rows.
+ * Rows are padded to 16 and columns to 64 with zero values and scales.
+ * ---------------------------------------------------------------------- */
+
+/* Bytes of a packed [n][k] matrix (k a multiple of 32).
+ * Replaces kernels::Q8TilesBytes (kernels/wmma_products.hpp:34-38). */
+size_t vx_q8_packed_bytes(size_t n, size_t k);
+
+/* GGML Q8_0 blocks [n][k/32] (34 bytes each) -> panels.
+ * Replaces kernels::Q8_0ToTiles (kernels/wmma_products.hpp:45-49). */
+int vx_q8_pack(const uint8_t* blocks, size_t n, size_t k, void* packed,
+               void* stream);
+
+/* Panels -> GGML Q8_0 blocks, the exact inverse of vx_q8_pack. No
+ * reference counterpart: it lets the packed form be checked and exported. */
+int vx_q8_unpack_blocks(const void* packed, size_t n, size_t k,
+                        uint8_t* blocks, void* stream);
+
+/* Panels -> bfloat16 [n][k]: bf16_rne(f32(f16 scale) * q), the conversion
+ * the reference applies before products of more than 128 rows.
+ * Replaces kernels::Q8TilesToBf16 (kernels/wmma_products.hpp:55-58). */
+int vx_q8_unpack_bf16(const void* packed, size_t n, size_t k, uint16_t* out,
+                      void* stream);
+
+/* ------------------------------------------------------------------------
+ * Products y[m][n] (+)= x[m][k] . W[n][k]^T, x bf16 row-major, W panels,
+ * y float32 row-major.
+ *
+ * m <= 128 (the reference's kChunkedRows, gemm.cpp:48-49) keeps the Q8_0
+ * arithmetic exact: int8 -> bf16 exactly, a float32 sum per 32-column
+ * block, acc = fmaf(f16 scale, sum, acc), partial sums added in a fixed
+ * order (deterministic run to run). m > 128 follows the reference's
+ * expansion (gemm.cpp:305-312): W as bf16(scale * q), one float32 sum over
+ * k on the matrix cores.
+ * ---------------------------------------------------------------------- */
+
+/* Split-reduction scratch of the products: partial sums and counters that
+ * are zero between products (the products leave them so), like
+ * Bf16Gemm::State's partials/counters (gemm.cpp:95-98). One scratch serves
+ * one stream at a time. */
+typedef struct vx_scratch vx_scratch;
+int vx_scratch_create(vx_scratch** scratch, size_t max_m, size_t max_n);
+void vx_scratch_destroy(vx_scratch* scratch);
+
+/* Replaces kernels::WmmaQ8 and Bf16Gemm::Linear on Q8_0 weights
+ * (kernels/wmma_products.hpp:87-93; gemm.hpp:56-58). `scratch` may be NULL,
+ * in which case no split reduction across workgroups is used. */
+int vx_q8_linear(const uint16_t* x, const void* packed, float* y, size_t m,
+                 size_t k, size_t n, int accumulate, vx_scratch* scratch,
+                 void* stream);
+
+/* The same product with a bf16 (round to nearest even) output instead of
+ * float32 and no accumulation. No reference counterpart (the reference's
+ * products write float32); it is the bf16 epilogue of a standalone product. */
+int vx_q8_linear_bf16(const uint16_t* x, const void* packed, uint16_t* y,
+                      size_t m, size_t k, size_t n, vx_scratch* scratch,
+                      void* stream);
+
+/* ------------------------------------------------------------------------
+ * Generator kernels: one entry per reference launcher on the path
+ * (kernels/generator_kernels.hpp), same argument meaning, any head_dim that
+ * is a multiple of 2 up to 256.
+ * ---------------------------------------------------------------------- */
+
+/* kernels::RmsNorm (generator_kernels.hpp:32-36). */
+int vx_rms_norm(const float* input, const uint16_t* weight, uint16_t* output,
+                float* output_f32, size_t rows, size_t width, float epsilon,
+                void* stream);
+/* kernels::QkvRope (generator_kernels.hpp:38-47); cos_sin may be NULL. */
+int vx_qkv_rope(const float* qkv, const float* cos_sin,
+                const int32_t* positions, const int32_t* cache_rows, float* q,
+                float* k_cache, float* v_cache, size_t rows, size_t heads,
+                size_t kv_heads, size_t head_dim, size_t capacity,
+                void* stream);
+/* kernels::Attention (generator_kernels.hpp:49-58). */
+int vx_attention(const float* q, const float* k_cache, const float* v_cache,
+                 uint16_t* output, size_t rows, size_t rows_per_sequence,
+                 size_t keys_per_sequence, size_t past, int causal,
+                 size_t heads, size_t kv_heads, size_t head_dim,
+                 size_t capacity, void* stream);
+/* kernels::SwiGlu (generator_kernels.hpp:60-62). */
+int vx_swiglu(const float* gate_up, uint16_t* output, size_t rows,
+              size_t width, void* stream);
+/* kernels::AddBias (generator_kernels.hpp:64-66). */
+int vx_add_bias(float* data, const uint16_t* bias, size_t rows, size_t width,
+                void* stream);
+/* kernels::ToBf16 (generator_kernels.hpp:68-70). */
+int vx_to_bf16(const float* input, uint16_t* output, size_t count, int silu,
+               void* stream);
+/* kernels::GatherRows (generator_kernels.hpp:28-30). */
+int vx_gather_rows(const float* input, const int32_t* indices, float* output,
+                   size_t rows, size_t width, void* stream);
+/* kernels::AssembleDit (generator_kernels.hpp:94-99). */
+int vx_assemble_dit(const float* mu, const float* time, const float* cond,
+                    const float* x, float* output, size_t patch_size,
+                    size_t width, void* stream);
+/* kernels::GuidedEuler (generator_kernels.hpp:101-106). zero_star = 1 is the
+ * reference's CFG-Zero* scale s = <c,u>/(|u|^2 + 1e-8); zero_star = 0 takes
+ * s = 1 (plain CFG: x -= dt (u + cfg (c - u))). */
+int vx_guided_euler(const float* velocity, float* x, size_t count, float cfg,
+                    float dt, int zero_star, void* stream);
+
+/* ------------------------------------------------------------------------
+ * The local DiT and its sampler (generator.cpp:297-324, 424-463, 515-538;
+ * transformer.cpp:55-100).
+ * ---------------------------------------------------------------------- */
+
+typedef struct vx_dit_shape {
+  uint32_t hidden;    /* 1024 */
+  uint32_t heads;     /* query heads */
+  uint32_t kv_heads;  /* heads % kv_heads == 0 */
+  uint32_t head_dim;  /* even, <= 256 */
+  uint32_t ffn;       /* intermediate size */
+  uint32_t layers;
+  uint32_t patch;     /* latent frames per patch (4) */
+  uint32_t feat;      /* latent channels (64) */
+  uint32_t time_in;   /* width of the sinusoidal time embedding */
+  uint32_t has_delta; /* add delta_time_mlp(sinusoid(0)) to the time vector */
+  float eps;          /* RMSNorm epsilon */
+} vx_dit_shape;
+
+typedef struct vx_dit_projection {
+  const void* weight;   /* Q8_0 panels [out][in] */
+  const uint16_t* bias; /* bf16 [out], or NULL */
+} vx_dit_projection;
+
+typedef struct vx_dit_layer {
+  const uint16_t* input_norm; /* bf16 [hidden] */
+  const void* qkv;            /* panels [(heads + 2 kv_heads) head_dim][hidden]:
+                                 q rows, then k rows, then v rows */
+  const void* o;              /* panels [hidden][heads head_dim] */
+  const uint16_t* post_norm;  /* bf16 [hidden] */
+  const void* gate_up;        /* panels [2 ffn][hidden]: gate rows, up rows */
+  const void* down;           /* panels [hidden][ffn] */
+} vx_dit_layer;
+
+typedef struct vx_dit_weights {
+  const vx_dit_layer* layers; /* host array of `layers` entries */
+  const uint16_t* norm;       /* final norm, bf16 [hidden] */
+  const float* rope;          /* [>= 3 + 2 patch][head_dim] cos|sin table, or
+                                 NULL for no rotation */
+  vx_dit_projection in_proj;  /* feat -> hidden */
+  vx_dit_projection cond_proj;
+  vx_dit_projection out_proj; /* hidden -> feat */
+  vx_dit_projection time_1;   /* time_in -> hidden */
+  vx_dit_projection time_2;   /* hidden -> hidden */
+  vx_dit_projection delta_1;  /* time_in -> hidden (has_delta) */
+  vx_dit_projection delta_2;  /* hidden -> hidden (has_delta) */
+} vx_dit_weights;
+
+typedef struct vx_dit vx_dit;
+
+/* Creates a DiT over caller-owned device weights (the handle keeps the
+ * pointers, not copies). Allocates the handle's scratch. */
+int vx_dit_create(vx_dit** dit, const vx_dit_shape* shape,
+                  const vx_dit_weights* weights);
+void vx_dit_destroy(vx_dit* dit);
+
+/* time_mlp(sinusoid(t)) (+ delta_time_mlp(sinusoid(0))) -> [hidden]
+ * (generator.cpp:212-237). */
+int vx_dit_time_vector(vx_dit* dit, float t, float* vector, void* stream);
+/* cond_proj(bf16(cond_latent [patch][feat])) -> [patch][hidden]
+ * (generator.cpp:448-451). */
+int vx_dit_cond_rows(vx_dit* dit, const float* cond_latent, float* cond_rows,
+                     void* stream);
+/* One CFG-pair evaluation (EvaluateDit, generator.cpp:297-324):
+ * mu [2 hidden], cond_rows [patch][hidden], x [patch][feat],
+ * time_vector [hidden] -> velocity [2][patch][feat] (conditional first). */
+int vx_dit_eval(vx_dit* dit, const float* mu, const float* cond_rows,
+                const float* x, const float* time_vector, float* velocity,
+                void* stream);
+/* Generator::Velocity (generator.cpp:515-538) on device data. */
+int vx_dit_velocity(vx_dit* dit, const float* mu, const float* cond_latent,
+                    const float* x, float t, float* velocity, void* stream);
+/* The sampler of Generator::Step (generator.cpp:448-463): x [patch][feat]
+ * is updated in place over `steps` Euler steps; t, dt, evaluate are HOST
+ * arrays (EulerStep, generator.hpp:38-44). The whole patch after its first
+ * call with the same arguments replays as one HIP graph. */
+int vx_dit_patch(vx_dit* dit, const float* mu, const float* cond_latent,
+                 float* x, const float* t, const float* dt,
+                 const int32_t* evaluate, size_t steps, float cfg,
+                 int zero_star, void* stream);
+
+/* EulerSchedule (generator.cpp:63-80, generator.hpp:34-44) on the host:
+ * writes `timesteps` entries. skip = 1 marks CFG-Zero*'s zero-velocity
+ * first steps as not evaluated; sway = 0 gives the uniform schedule. */
+int vx_euler_schedule(size_t timesteps, float sway, int skip, float* t,
+                      float* dt, int32_t* evaluate);
+
+/* The rotary table of MiniCPM's LongRoPE on the host, float32 as the
+ * reference computes it (transformer.cpp:20-45): [positions][dim], cos in
+ * the first half, sin in the second. factors: dim/2 values or NULL. */
+int vx_rope_table(double theta, size_t dim, const double* factors,
+                  float scaling, size_t positions, float* table);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* VOXCPM_AMD_H_ */

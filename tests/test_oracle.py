@@ -1,0 +1,458 @@
+"""Pins the CPU oracle (oracle/oracle.c) against what fixes it independently:
+library conversions (numpy float16, torch bfloat16), torch.linspace (which
+the reference's Linspace mirrors, generator.cpp:21-22), closed forms and
+invariants, brute force in float64 on small inputs, and a float64 torch
+formulation of the whole DiT. Each check is chosen so that a plausible slip
+(a dropped term, a swapped operand, a wrong index, a wrong rounding) fails.
+"""
+import ctypes
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from voxcpm_amd import synth
+
+
+def f32(x):
+    return np.ascontiguousarray(x, dtype=np.float32)
+
+
+# ---- conversions ------------------------------------------------------------
+
+def test_bf16_rounding_matches_torch(oracle):
+    rng = synth.Rng(1, 1)
+    bits = rng.bits(200000).astype(np.uint32)
+    values = bits.view(np.float32)
+    values = values[np.isfinite(values)]
+    # ties: the low 16 bits exactly 0x8000, odd and even upper halves
+    ties = (np.arange(0, 2000, dtype=np.uint32) << 16 | 0x8000).view(np.float32)
+    values = f32(np.concatenate([values, ties, [0.0, -0.0, 1e-45, 3.4e38, -3.4e38]]))
+    out = np.zeros(values.size, dtype=np.uint16)
+    oracle.lib().vo_bf16_round_array(oracle.ptr(values), oracle.ptr(out), values.size)
+    expected = torch.from_numpy(values).to(torch.bfloat16).view(torch.int16).numpy()
+    assert np.array_equal(out, expected.view(np.uint16))
+    # NaNs stay quiet NaNs with the payload's upper half.
+    nan = np.array([0x7F800001, 0xFF812345, 0x7FC00000], dtype=np.uint32).view(np.float32)
+    for value, bits_in in zip(nan, [0x7F800001, 0xFF812345, 0x7FC00000]):
+        assert oracle.lib().vo_bf16_bits(float(value)) == ((bits_in >> 16) | 0x40)
+
+
+def test_half_decode_exhaustive(oracle):
+    bits = np.arange(65536, dtype=np.uint16)
+    expected = bits.view(np.float16).astype(np.float32)
+    got = np.array([oracle.lib().vo_half_value(int(b)) for b in bits], dtype=np.float32)
+    finite = np.isfinite(expected)
+    assert np.array_equal(got[finite].view(np.uint32), expected[finite].view(np.uint32))
+    assert np.array_equal(np.isnan(got), np.isnan(expected))
+    assert np.array_equal(np.isinf(got), np.isinf(expected))
+
+
+def test_half_encode_matches_numpy(oracle):
+    rng = synth.Rng(2, 2)
+    values = f32(np.concatenate([rng.normal(20000, 1e-3), rng.normal(20000, 1e-6),
+                                 rng.normal(2000, 1e4), [65519.0, 65520.0, 6e-8, 3e-8]]))
+    got = np.array([oracle.lib().vo_half_bits(float(v)) for v in values], dtype=np.uint16)
+    assert np.array_equal(got, values.astype(np.float16).view(np.uint16))
+
+
+# ---- Q8_0 -----------------------------------------------------------------------
+
+def test_q8_dequant_closed_form(oracle):
+    rng = synth.Rng(3, 3)
+    n, k = 48, 128
+    blocks = synth.q8_blocks(rng, n, k)
+    blocks.reshape(-1, 34)[::5, 2] = 0x80  # q = -128
+    got = oracle.q8_dequant_bf16(blocks, n, k)
+    scale = blocks[:, :, :2].copy().view(np.uint16).view(np.float16).astype(np.float32)
+    q = blocks[:, :, 2:].view(np.int8).astype(np.float32)
+    exact = (scale * q).reshape(n, k)  # exact in float32 (19 significant bits)
+    expected = torch.from_numpy(exact).to(torch.bfloat16).view(torch.int16).numpy()
+    assert np.array_equal(got, expected.view(np.uint16))
+    values = oracle.q8_values(blocks, n, k)
+    assert np.array_equal(values, exact.astype(np.float64))
+
+
+def test_q8_linear_exact_on_integers(oracle):
+    """Unit scales and small integer activations: every float32 sum is exact,
+    so the product equals the integer matrix product bit for bit."""
+    rng = synth.Rng(4, 4)
+    m, k, n = 5, 256, 40
+    blocks = synth.q8_blocks(rng, n, k)
+    flat = blocks.reshape(-1, 34)
+    flat[:, 0] = 0x00
+    flat[:, 1] = 0x3C  # 1.0
+    xi = ((rng.bits(m * k) % np.uint64(9)).astype(np.int64) - 4).reshape(m, k)
+    x = synth.bf16_bits(xi.astype(np.float32))
+    y = oracle.q8_linear(x, blocks, n, threads=3)
+    q = blocks[:, :, 2:].view(np.int8).astype(np.int64).reshape(n, k)
+    assert np.array_equal(y, (xi @ q.T).astype(np.float32))
+
+
+def test_q8_linear_block_scales_and_accumulate(oracle):
+    """Against a float64 product of the dequantized values (independent of the
+    oracle's loops) and the accumulate path: y = before + x W^T."""
+    rng = synth.Rng(5, 5)
+    m, k, n = 7, 320, 33
+    blocks = synth.q8_blocks(rng, n, k)
+    x = synth.activations(rng, m, k)
+    w = oracle.q8_values(blocks, n, k)
+    xf = synth.bf16_values(x).astype(np.float64)
+    exact = xf @ w.T
+    magnitude = np.abs(xf) @ np.abs(w).T
+    y = oracle.q8_linear(x, blocks, n, threads=4)
+    assert np.max(np.abs(y - exact) / magnitude) < 2e-6
+    before = f32(rng.normal(m * n).reshape(m, n))
+    y2 = oracle.q8_linear(x, blocks, n, before=before, threads=1)
+    assert np.max(np.abs(y2 - (exact + before)) / (magnitude + np.abs(before))) < 2e-6
+    # The checker agrees, and catches a planted error of 1e-4 |x w|.
+    assert oracle.q8_check(y, x, blocks) < 2e-6
+    bad = y.copy()
+    bad[3, 7] += 1e-4 * magnitude[3, 7]
+    assert oracle.q8_check(bad, x, blocks) > 5e-5
+    # Thread count does not change a bit.
+    assert np.array_equal(y, oracle.q8_linear(x, blocks, n, threads=1))
+
+
+def test_q8_linear_scales_after_block_sums(oracle):
+    """The scale multiplies each block's float32 sum (fmaf), not each value:
+    a block whose exact sum is zero contributes exactly zero even with a
+    scale whose products with q are inexact in bf16."""
+    k, n = 64, 1
+    blocks = np.zeros((n, k // 32, 34), dtype=np.uint8)
+    blocks[0, :, 0:2] = np.frombuffer(np.float16(0.0123).tobytes(), np.uint8)
+    q = np.zeros(32, dtype=np.int8)
+    q[0], q[1] = 77, -77
+    blocks[0, 0, 2:] = q.view(np.uint8)
+    blocks[0, 1, 2:] = q.view(np.uint8)
+    x = synth.bf16_bits(f32(np.ones((1, k))))
+    y = oracle.q8_linear(x, blocks, n)
+    assert y[0, 0] == 0.0
+
+
+# ---- generator kernels -------------------------------------------------------
+
+def test_rms_norm(oracle):
+    rng = synth.Rng(6, 6)
+    rows, width, eps = 3, 1024, 1e-5
+    x = f32(rng.normal(rows * width, 3.0).reshape(rows, width))
+    x[2] = 0.5  # constant row: closed form gamma * c / sqrt(c^2 + eps)
+    gamma = synth.bf16_vector(rng, width, 1.0, 0.02)
+    out = np.zeros((rows, width), dtype=np.uint16)
+    out32 = np.zeros((rows, width), dtype=np.float32)
+    oracle.lib().vo_rms_norm(oracle.ptr(x), oracle.ptr(gamma), oracle.ptr(out),
+                             oracle.ptr(out32), rows, width, eps)
+    g = synth.bf16_values(gamma).astype(np.float64)
+    xd = x.astype(np.float64)
+    expected = xd / np.sqrt((xd ** 2).mean(axis=1, keepdims=True) + eps) * g
+    assert np.max(np.abs(out32 - expected)) < 1e-5 * np.abs(expected).max()
+    assert np.allclose(out32[2], g * 0.5 / math.sqrt(0.25 + eps), rtol=1e-6)
+    assert np.array_equal(out, synth.bf16_bits(out32))
+
+
+def test_rope_table_and_rotation(oracle):
+    dim, positions = 128, 11
+    factors = np.array(synth.VOXCPM2_SHORT_FACTORS)
+    table = oracle.rope_table(10000.0, dim, factors, 1.0, positions)
+    half = dim // 2
+    i = np.arange(half)
+    angle = np.arange(positions)[:, None] / factors[None, :] * 10000.0 ** (-2.0 * i / dim)
+    assert np.max(np.abs(table[:, :half] - np.cos(angle))) < 2e-5
+    assert np.max(np.abs(table[:, half:] - np.sin(angle))) < 2e-5
+    assert np.array_equal(table[0, :half], np.ones(half, np.float32))
+    assert np.array_equal(table[0, half:], np.zeros(half, np.float32))
+    # QkvRope: rotation of pairs (i, i + half); position 0 is the identity,
+    # norms of the pairs are kept, and <R(p) q, R(p') k> depends on p - p'.
+    rng = synth.Rng(7, 7)
+    heads, kv_heads, rows = 2, 1, 4
+    width = (heads + 2 * kv_heads) * dim
+    base = f32(rng.normal(width))
+    qkv = f32(np.tile(base, (rows, 1)))
+    positions_arr = np.array([0, 3, 5, 8], dtype=np.int32)
+    cache_rows = np.array([0, 1, 2, 3], dtype=np.int32)
+    q = np.zeros((rows, heads, dim), np.float32)
+    kc = np.zeros((kv_heads, rows, dim), np.float32)
+    vc = np.zeros((kv_heads, rows, dim), np.float32)
+    oracle.lib().vo_qkv_rope(oracle.ptr(qkv), oracle.ptr(table), oracle.ptr(positions_arr),
+                             oracle.ptr(cache_rows), oracle.ptr(q), oracle.ptr(kc),
+                             oracle.ptr(vc), rows, heads, kv_heads, dim, rows)
+    assert np.array_equal(q[0].ravel(), base[:heads * dim])
+    assert np.array_equal(vc[0, 2], base[(heads + kv_heads) * dim:])
+    for r in range(rows):
+        a, b = q[r, 1, :half].astype(np.float64), q[r, 1, half:].astype(np.float64)
+        a0, b0 = base[dim:dim + half].astype(np.float64), base[dim + half:2 * dim].astype(np.float64)
+        assert np.allclose(a * a + b * b, a0 * a0 + b0 * b0, rtol=1e-5)
+    # q at position 8 against k at 5 equals q at 3 against k at 0.
+    d1 = float(np.dot(q[3, 0].astype(np.float64), kc[0, 2].astype(np.float64)))
+    d2 = float(np.dot(q[1, 0].astype(np.float64), kc[0, 0].astype(np.float64)))
+    assert abs(d1 - d2) < 1e-4 * max(1.0, abs(d1))
+
+
+@pytest.mark.parametrize("head_dim,heads,kv_heads", [(64, 4, 4), (128, 4, 2), (32, 3, 1)])
+def test_attention_against_torch(oracle, head_dim, heads, kv_heads):
+    rng = synth.Rng(8, head_dim)
+    length, rows = 11, 22
+    q = f32(rng.normal(rows * heads * head_dim).reshape(rows, heads, head_dim))
+    kc = f32(rng.normal(kv_heads * rows * head_dim).reshape(kv_heads, rows, head_dim))
+    vc = f32(rng.normal(kv_heads * rows * head_dim).reshape(kv_heads, rows, head_dim))
+    out = np.zeros((rows, heads, head_dim), np.uint16)
+    oracle.lib().vo_attention(oracle.ptr(q), oracle.ptr(kc), oracle.ptr(vc), oracle.ptr(out),
+                              rows, length, length, 0, 0, heads, kv_heads, head_dim, rows)
+    got = synth.bf16_values(out).astype(np.float64)
+    group = heads // kv_heads
+    for s in range(2):
+        rs = slice(s * length, (s + 1) * length)
+        qt = torch.from_numpy(q[rs].astype(np.float64)).permute(1, 0, 2)
+        kt = torch.from_numpy(kc[:, rs].astype(np.float64)).repeat_interleave(group, 0)
+        vt = torch.from_numpy(vc[:, rs].astype(np.float64)).repeat_interleave(group, 0)
+        ref = torch.nn.functional.scaled_dot_product_attention(qt, kt, vt).permute(1, 0, 2).numpy()
+        assert np.max(np.abs(got[rs] - ref)) < 1e-2 * np.abs(ref).max()
+    # causal with one key: the output is that key's value
+    out1 = np.zeros((1, heads, head_dim), np.uint16)
+    oracle.lib().vo_attention(oracle.ptr(q), oracle.ptr(kc), oracle.ptr(vc), oracle.ptr(out1),
+                              1, 1, 1, 0, 1, heads, kv_heads, head_dim, rows)
+    for h in range(heads):
+        assert np.array_equal(out1[0, h], synth.bf16_bits(vc[h // group, 0]))
+
+
+def test_swiglu_bias_to_bf16(oracle):
+    rng = synth.Rng(9, 9)
+    rows, width = 3, 256
+    gu = f32(rng.normal(rows * 2 * width, 3.0).reshape(rows, 2 * width))
+    out = np.zeros((rows, width), np.uint16)
+    oracle.lib().vo_swiglu(oracle.ptr(gu), oracle.ptr(out), rows, width)
+    g = torch.from_numpy(gu[:, :width].astype(np.float64))
+    u = torch.from_numpy(gu[:, width:].astype(np.float64))
+    ref = (torch.nn.functional.silu(g) * u).numpy()
+    got = synth.bf16_values(out)
+    assert np.all(np.abs(got - ref) <= np.abs(ref) * 2 ** -8 + 1e-30)
+    bias = synth.bf16_vector(rng, width, 0.0, 0.5)
+    data = f32(rng.normal(rows * width).reshape(rows, width))
+    before = data.copy()
+    oracle.lib().vo_add_bias(oracle.ptr(data), oracle.ptr(bias), rows, width)
+    assert np.array_equal(data, before + synth.bf16_values(bias)[None, :])
+    silu = np.zeros(rows * width, np.uint16)
+    oracle.lib().vo_to_bf16(oracle.ptr(before), oracle.ptr(silu), rows * width, 1)
+    ref = torch.nn.functional.silu(torch.from_numpy(before.astype(np.float64))).numpy().ravel()
+    assert np.all(np.abs(synth.bf16_values(silu) - ref) <= np.abs(ref) * 2 ** -8 + 1e-30)
+
+
+def test_assemble_and_gather(oracle):
+    patch, width = 4, 8
+    mu = f32(np.arange(2 * width) + 100)
+    time = f32(np.arange(width) + 200)
+    cond = f32(np.arange(patch * width).reshape(patch, width) + 300)
+    x = f32(np.arange(patch * width).reshape(patch, width) + 400)
+    out = np.zeros((2, 11, width), np.float32)
+    oracle.lib().vo_assemble_dit(oracle.ptr(mu), oracle.ptr(time), oracle.ptr(cond),
+                                 oracle.ptr(x), oracle.ptr(out), patch, width)
+    assert np.array_equal(out[0, 0:2].ravel(), mu)
+    assert np.array_equal(out[1, 0:2], np.zeros((2, width)))
+    for s in range(2):
+        assert np.array_equal(out[s, 2], time)
+        assert np.array_equal(out[s, 3:7], cond)
+        assert np.array_equal(out[s, 7:11], x)
+    idx = np.array([7, 8, 9, 10, 18, 19, 20, 21], dtype=np.int32)
+    gathered = np.zeros((8, width), np.float32)
+    oracle.lib().vo_gather_rows(oracle.ptr(out.reshape(22, width)), oracle.ptr(idx),
+                                oracle.ptr(gathered), 8, width)
+    assert np.array_equal(gathered, np.concatenate([x, x]))
+
+
+def test_guided_euler_closed_forms(oracle):
+    rng = synth.Rng(10, 10)
+    count = 256
+    c = f32(rng.normal(count))
+    u = f32(rng.normal(count))
+    v = f32(np.concatenate([c, u]))
+    x0 = f32(rng.normal(count))
+    # plain CFG (s = 1): x -= dt (u + cfg (c - u))
+    x = x0.copy()
+    oracle.lib().vo_guided_euler(oracle.ptr(v), oracle.ptr(x), count, 2.0, 0.1, 0)
+    ref = x0.astype(np.float64) - 0.1 * (u + 2.0 * (c.astype(np.float64) - u))
+    assert np.allclose(x, ref, atol=1e-6)
+    # cfg = 1, s = 1: x -= dt c
+    x = x0.copy()
+    oracle.lib().vo_guided_euler(oracle.ptr(v), oracle.ptr(x), count, 1.0, 0.25, 0)
+    assert np.allclose(x, x0 - 0.25 * c, atol=1e-6)
+    # CFG-Zero*: s = <c,u>/(|u|^2 + 1e-8); with c = u, v = u for any cfg
+    x = x0.copy()
+    same = f32(np.concatenate([u, u]))
+    oracle.lib().vo_guided_euler(oracle.ptr(same), oracle.ptr(x), count, 2.0, 0.5, 1)
+    assert np.allclose(x, x0 - 0.5 * u, atol=1e-5)
+    x = x0.copy()
+    oracle.lib().vo_guided_euler(oracle.ptr(v), oracle.ptr(x), count, 2.0, 0.1, 1)
+    s = np.dot(c.astype(np.float64), u) / (np.dot(u.astype(np.float64), u) + 1e-8)
+    ref = x0 - 0.1 * (u * s + 2.0 * (c - u * s))
+    assert np.allclose(x, ref, atol=1e-5)
+
+
+# ---- sampler ---------------------------------------------------------------------
+
+@pytest.mark.parametrize("steps", [1, 2, 3, 10, 11, 25, 101])
+def test_linspace_matches_torch(oracle, steps):
+    out = np.zeros(steps, np.float32)
+    oracle.lib().vo_linspace(1.0, 0.0, steps, oracle.ptr(out))
+    expected = torch.linspace(1.0, 0.0, steps, dtype=torch.float32).numpy()
+    assert np.array_equal(out, expected)
+
+
+def test_euler_schedule(oracle):
+    # Uniform (sway 0), no skip: t = 1 - i/10 from torch.linspace, dt = 0.1.
+    t, dt, ev = oracle.euler_schedule(10, 0.0, False)
+    lin = torch.linspace(1.0, 0.0, 11, dtype=torch.float32).numpy()
+    assert np.array_equal(t[0:1], lin[0:1])
+    assert np.allclose(t, lin[:10], atol=1e-6)
+    assert np.allclose(dt, 0.1, atol=1e-6)
+    assert ev.tolist() == [1] * 10
+    # The chained t stays within float32 rounding of the span and the dt
+    # sum to 1 (the end point 0).
+    assert abs(float(np.sum(dt.astype(np.float64))) - 1.0) < 1e-6
+    # Sway 1 and CFG-Zero*'s skip: t = s + (cos(pi s / 2) - 1 + s); the
+    # first max(1, int(0.04 * 11)) = 1 step is not evaluated.
+    t, dt, ev = oracle.euler_schedule(10, 1.0, True)
+    span = lin.astype(np.float64)
+    warped = span + (np.cos(np.pi / 2 * span) - 1 + span)
+    assert np.allclose(t, warped[:10], atol=2e-6)
+    assert np.allclose(dt, warped[:10] - warped[1:], atol=2e-6)
+    assert ev.tolist() == [0] + [1] * 9
+    # t of the reference's 10-step schedule (restated from generator.cpp)
+    table = [1.0, 0.9564344, 0.9090170, 0.8539906, 0.7877852, 0.7071068,
+             0.6090170, 0.4910066, 0.3510565, 0.1876884]
+    assert np.allclose(t, table, atol=1e-6)
+    # 25 steps skip int(0.04 * 26) = 1; 50 steps skip int(2.04) = 2
+    assert oracle.euler_schedule(50, 1.0, True)[2][:3].tolist() == [0, 0, 1]
+
+
+def test_sinusoid(oracle):
+    for t, width in [(0.0, 256), (0.63, 1024), (1.0, 256), (0.1876884, 1024)]:
+        out = np.zeros(width, np.float32)
+        oracle.lib().vo_sinusoid(t, width, oracle.ptr(out))
+        half = width // 2
+        freq = np.exp(-np.arange(half) * math.log(10000.0) / (half - 1))
+        angle = 1000.0 * t * freq
+        assert np.max(np.abs(out[:half] - np.sin(angle))) < 2e-4
+        assert np.max(np.abs(out[half:] - np.cos(angle))) < 2e-4
+    zero = np.zeros(64, np.float32)
+    oracle.lib().vo_sinusoid(0.0, 64, oracle.ptr(zero))
+    assert np.array_equal(zero, np.concatenate([np.zeros(32), np.ones(32)]).astype(np.float32))
+
+
+# ---- the DiT against a float64 torch formulation --------------------------------
+
+def torch_dit_velocity(weights, oracle, mu, cond_latent, x, t):
+    """The local DiT in float64 torch from its description (no bf16 rounding,
+    torch's attention), for comparison at tolerance."""
+    c = weights.config
+    td = torch.float64
+
+    def W(blocks):
+        n, kb, _ = blocks.shape
+        return torch.from_numpy(oracle.q8_values(np.ascontiguousarray(blocks), n, kb * 32))
+
+    def vec(bits):
+        return torch.from_numpy(synth.bf16_values(bits).astype(np.float64))
+
+    def proj(name, inp):
+        blocks, bias = weights.projections[name]
+        return inp @ W(blocks).T + vec(bias)
+
+    def rms(h, g):
+        return h / torch.sqrt((h * h).mean(-1, keepdim=True) + c.eps) * vec(g)
+
+    def sinus(tt, width):
+        half = width // 2
+        freq = torch.exp(-torch.arange(half, dtype=td) * math.log(10000.0) / (half - 1))
+        a = 1000.0 * tt * freq
+        return torch.cat([torch.sin(a), torch.cos(a)])
+
+    silu = torch.nn.functional.silu
+    time = proj("time_2", silu(proj("time_1", sinus(t, c.time_in))))
+    if c.has_delta:
+        time = time + proj("delta_2", silu(proj("delta_1", sinus(0.0, c.time_in))))
+    cond_rows = proj("cond_proj", torch.from_numpy(cond_latent.astype(np.float64)))
+    x_rows = proj("in_proj", torch.from_numpy(x.astype(np.float64)))
+    mu_t = torch.from_numpy(mu.astype(np.float64)).reshape(2, c.hidden)
+    seq = []
+    for branch in range(2):
+        head = mu_t if branch == 0 else torch.zeros_like(mu_t)
+        seq.append(torch.cat([head, time[None], cond_rows, x_rows]))
+    h = torch.stack(seq)  # [2][11][hidden]
+    length = 3 + 2 * c.patch
+    pos = torch.arange(length, dtype=td)
+    half = c.head_dim // 2
+    factors = torch.tensor(c.rope_factors if c.rope_factors else [1.0] * half, dtype=td)
+    inv = c.rope_theta ** (-2.0 * torch.arange(half, dtype=td) / c.head_dim)
+    ang = pos[:, None] / factors[None, :] * inv[None, :]
+    cos, sin = torch.cos(ang) * c.rope_scaling, torch.sin(ang) * c.rope_scaling
+
+    def rope(v):  # [2][heads][length][hd]
+        a, b = v[..., :half], v[..., half:]
+        return torch.cat([a * cos - b * sin, b * cos + a * sin], -1)
+
+    for layer in weights.layers:
+        n1 = rms(h, layer["input_norm"])
+        qkv = n1 @ W(layer["qkv"]).T
+        qw, kw = c.q_width, c.kv_heads * c.head_dim
+        q = qkv[..., :qw].reshape(2, length, c.heads, c.head_dim).transpose(1, 2)
+        k = qkv[..., qw:qw + kw].reshape(2, length, c.kv_heads, c.head_dim).transpose(1, 2)
+        v = qkv[..., qw + kw:].reshape(2, length, c.kv_heads, c.head_dim).transpose(1, 2)
+        q, k = rope(q), rope(k)
+        g = c.heads // c.kv_heads
+        k, v = k.repeat_interleave(g, 1), v.repeat_interleave(g, 1)
+        a = torch.nn.functional.scaled_dot_product_attention(q, k, v)
+        a = a.transpose(1, 2).reshape(2, length, qw)
+        h = h + a @ W(layer["o"]).T
+        n2 = rms(h, layer["post_norm"])
+        gu = n2 @ W(layer["gate_up"]).T
+        act = silu(gu[..., :c.ffn]) * gu[..., c.ffn:]
+        h = h + act @ W(layer["down"]).T
+    out = rms(h, weights.norm)[:, 3 + c.patch:]  # [2][patch][hidden]
+    return proj("out_proj", out).numpy()
+
+
+@pytest.mark.parametrize("config", [
+    synth.DitConfig(hidden=256, heads=4, kv_heads=4, head_dim=64, ffn=512,
+                    layers=2, time_in=128),
+    synth.DitConfig(hidden=256, heads=4, kv_heads=2, head_dim=128, ffn=512,
+                    layers=2, time_in=256, has_delta=True, eps=1e-5,
+                    rope_factors=synth.VOXCPM2_SHORT_FACTORS),
+], ids=["mha-hd64", "gqa-hd128-delta"])
+def test_dit_velocity_against_float64_torch(oracle, config):
+    rope = oracle.rope_table(config.rope_theta, config.head_dim, config.rope_factors,
+                             config.rope_scaling, 3 + 2 * config.patch)
+    weights = synth.dit_weights(config, 11, rope)
+    inputs = synth.patch_inputs(config, 12)
+    dit = oracle.OracleDit(weights)
+    got = dit.velocity(inputs.mu, inputs.cond_latent, inputs.noise, 0.63)
+    ref = torch_dit_velocity(weights, oracle, inputs.mu, inputs.cond_latent,
+                             inputs.noise, 0.63)
+    error = np.linalg.norm(got - ref) / np.linalg.norm(ref)
+    assert error < 1e-2, error  # bf16 activations against float64
+    # A planted slip in the oracle's composition (swapping the CFG branches)
+    # fails the same bound.
+    assert np.linalg.norm(got[::-1] - ref) / np.linalg.norm(ref) > 5e-2
+
+
+def test_dit_patch_composes_evaluations(oracle):
+    """The sampler equals its steps: cond rows and time vectors, then
+    eval + guided Euler per evaluated step."""
+    config = synth.DitConfig(hidden=128, heads=2, kv_heads=1, head_dim=64, ffn=256,
+                             layers=1, time_in=128, has_delta=True)
+    rope = oracle.rope_table(10000.0, 64, None, 1.0, 11)
+    weights = synth.dit_weights(config, 13, rope)
+    inputs = synth.patch_inputs(config, 14)
+    dit = oracle.OracleDit(weights, threads=2)
+    t, dt, ev = oracle.euler_schedule(5, 1.0, True)
+    got = dit.patch(inputs.mu, inputs.cond_latent, inputs.noise, t, dt, ev, 2.0, True)
+    x = inputs.noise.copy()
+    cond = dit.cond_rows(inputs.cond_latent)
+    for step in range(5):
+        if not ev[step]:
+            continue
+        v = dit.eval(inputs.mu, cond, x, dit.time_vector(float(t[step])))
+        flat = np.ascontiguousarray(v.reshape(-1))
+        oracle.lib().vo_guided_euler(oracle.ptr(flat), oracle.ptr(x), x.size, 2.0,
+                                     float(dt[step]), 1)
+    assert np.array_equal(got, x)

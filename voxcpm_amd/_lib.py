@@ -1,0 +1,124 @@
+"""ctypes binding of libvoxcpm_amd.so, the C ABI of include/voxcpm_amd.h.
+
+The library must have been built (voxcpm_amd.build); loading fails loudly
+otherwise -- there is no fallback implementation.
+"""
+from __future__ import annotations
+
+import ctypes
+import pathlib
+
+LIBRARY = pathlib.Path(__file__).resolve().parent / "libvoxcpm_amd.so"
+
+VX_OK = 0
+VX_UNSUPPORTED = 1
+VX_BAD_ARG = 2
+VX_HIP_ERROR = 3
+
+c_size = ctypes.c_size_t
+c_int = ctypes.c_int
+c_float = ctypes.c_float
+c_void_p = ctypes.c_void_p
+
+
+class VxError(RuntimeError):
+    """A failed voxcpm_amd call: `status` is the vx_status."""
+
+    def __init__(self, status: int, message: str):
+        super().__init__(f"voxcpm_amd status {status}: {message}")
+        self.status = status
+
+
+class DitShape(ctypes.Structure):
+    _fields_ = [(name, ctypes.c_uint32) for name in (
+        "hidden", "heads", "kv_heads", "head_dim", "ffn", "layers", "patch",
+        "feat", "time_in", "has_delta")] + [("eps", ctypes.c_float)]
+
+
+class DitProjection(ctypes.Structure):
+    _fields_ = [("weight", c_void_p), ("bias", c_void_p)]
+
+
+class DitLayer(ctypes.Structure):
+    _fields_ = [("input_norm", c_void_p), ("qkv", c_void_p), ("o", c_void_p),
+                ("post_norm", c_void_p), ("gate_up", c_void_p),
+                ("down", c_void_p)]
+
+
+class DitWeights(ctypes.Structure):
+    _fields_ = [("layers", ctypes.POINTER(DitLayer)), ("norm", c_void_p),
+                ("rope", c_void_p), ("in_proj", DitProjection),
+                ("cond_proj", DitProjection), ("out_proj", DitProjection),
+                ("time_1", DitProjection), ("time_2", DitProjection),
+                ("delta_1", DitProjection), ("delta_2", DitProjection)]
+
+
+_SIGNATURES = {
+    "vx_last_error": ([], ctypes.c_char_p),
+    "vx_last_hip_error": ([], c_int),
+    "vx_version": ([], ctypes.c_char_p),
+    "vx_q8_packed_bytes": ([c_size, c_size], c_size),
+    "vx_q8_pack": ([c_void_p, c_size, c_size, c_void_p, c_void_p], c_int),
+    "vx_q8_unpack_blocks": ([c_void_p, c_size, c_size, c_void_p, c_void_p], c_int),
+    "vx_q8_unpack_bf16": ([c_void_p, c_size, c_size, c_void_p, c_void_p], c_int),
+    "vx_scratch_create": ([ctypes.POINTER(c_void_p), c_size, c_size], c_int),
+    "vx_scratch_destroy": ([c_void_p], None),
+    "vx_q8_linear": ([c_void_p, c_void_p, c_void_p, c_size, c_size, c_size,
+                      c_int, c_void_p, c_void_p], c_int),
+    "vx_q8_linear_bf16": ([c_void_p, c_void_p, c_void_p, c_size, c_size,
+                           c_size, c_void_p, c_void_p], c_int),
+    "vx_q8_linear_planned": ([c_void_p, c_void_p, c_void_p, c_size, c_size,
+                              c_size, c_int, c_void_p, c_int, c_int, c_int,
+                              c_void_p], c_int),
+    "vx_q8_plan": ([c_size, c_size, c_size, c_void_p, c_void_p], c_int),
+    "vx_rms_norm": ([c_void_p, c_void_p, c_void_p, c_void_p, c_size, c_size,
+                     c_float, c_void_p], c_int),
+    "vx_qkv_rope": ([c_void_p] * 7 + [c_size] * 5 + [c_void_p], c_int),
+    "vx_attention": ([c_void_p] * 4 + [c_size] * 4 + [c_int] + [c_size] * 4
+                     + [c_void_p], c_int),
+    "vx_swiglu": ([c_void_p, c_void_p, c_size, c_size, c_void_p], c_int),
+    "vx_add_bias": ([c_void_p, c_void_p, c_size, c_size, c_void_p], c_int),
+    "vx_to_bf16": ([c_void_p, c_void_p, c_size, c_int, c_void_p], c_int),
+    "vx_gather_rows": ([c_void_p, c_void_p, c_void_p, c_size, c_size,
+                        c_void_p], c_int),
+    "vx_assemble_dit": ([c_void_p] * 5 + [c_size, c_size, c_void_p], c_int),
+    "vx_guided_euler": ([c_void_p, c_void_p, c_size, c_float, c_float, c_int,
+                         c_void_p], c_int),
+    "vx_dit_create": ([ctypes.POINTER(c_void_p), ctypes.POINTER(DitShape),
+                       ctypes.POINTER(DitWeights)], c_int),
+    "vx_dit_destroy": ([c_void_p], None),
+    "vx_dit_time_vector": ([c_void_p, c_float, c_void_p, c_void_p], c_int),
+    "vx_dit_cond_rows": ([c_void_p, c_void_p, c_void_p, c_void_p], c_int),
+    "vx_dit_eval": ([c_void_p] * 6 + [c_void_p], c_int),
+    "vx_dit_velocity": ([c_void_p] * 4 + [c_float, c_void_p, c_void_p], c_int),
+    "vx_dit_patch": ([c_void_p] * 7 + [c_size, c_float, c_int, c_void_p], c_int),
+    "vx_euler_schedule": ([c_size, c_float, c_int, c_void_p, c_void_p,
+                           c_void_p], c_int),
+    "vx_rope_table": ([ctypes.c_double, c_size, c_void_p, c_float, c_size,
+                       c_void_p], c_int),
+}
+
+_lib: ctypes.CDLL | None = None
+
+
+def lib() -> ctypes.CDLL:
+    """The loaded library (raises if it has not been built)."""
+    global _lib
+    if _lib is None:
+        if not LIBRARY.exists():
+            raise RuntimeError(
+                f"{LIBRARY} is missing: build it with `python -m voxcpm_amd.build`"
+                " (there is no fallback path)")
+        handle = ctypes.CDLL(str(LIBRARY))
+        for name, (args, result) in _SIGNATURES.items():
+            function = getattr(handle, name)
+            function.argtypes = args
+            function.restype = result
+        _lib = handle
+    return _lib
+
+
+def check(status: int) -> None:
+    """Raises VxError for a failed status."""
+    if status != VX_OK:
+        raise VxError(status, lib().vx_last_error().decode())

@@ -1,0 +1,188 @@
+// The C ABI's error state, the product scratch and the product entry points.
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+#include <string>
+
+#include "common.hpp"
+#include "products.hpp"
+#include "q8.hpp"
+
+namespace vx {
+namespace {
+
+thread_local std::string last_error;
+thread_local int last_hip_error = 0;
+
+}  // namespace
+
+int Fail(int status, const std::string& message) {
+  last_error = message;
+  return status;
+}
+
+int FailHip(hipError_t error, const char* what) {
+  last_hip_error = static_cast<int>(error);
+  last_error = std::string(what) + ": " + hipGetErrorString(error);
+  return VX_HIP_ERROR;
+}
+
+int Succeed() {
+  last_error.clear();
+  last_hip_error = 0;
+  return VX_OK;
+}
+
+int LaunchStatus(const char* what) {
+  const hipError_t error = hipGetLastError();
+  if (error != hipSuccess)
+    return FailHip(error, what);
+  return Succeed();
+}
+
+}  // namespace vx
+
+struct vx_scratch {
+  float* partials = nullptr;
+  std::size_t partial_floats = 0;
+  unsigned* counters = nullptr;
+  std::size_t counter_count = 0;
+};
+
+namespace {
+
+bool Aligned(const void* pointer, std::size_t bytes) {
+  return reinterpret_cast<std::uintptr_t>(pointer) % bytes == 0;
+}
+
+int CheckProduct(const void* x, const void* w, const void* y, std::size_t m,
+                 std::size_t k, std::size_t n, const char* what) {
+  if (x == nullptr || w == nullptr || y == nullptr)
+    return vx::Fail(VX_BAD_ARG, std::string(what) + ": null pointer");
+  if (m == 0 || n == 0 || k == 0 || k % 32 != 0)
+    return vx::Fail(VX_BAD_ARG, std::string(what) +
+                                    ": m, n must be positive and k a positive "
+                                    "multiple of 32");
+  if (m > (1U << 24) || n > (1U << 24) || k > (1U << 24))
+    return vx::Fail(VX_BAD_ARG, std::string(what) + ": shape too large");
+  if (!Aligned(x, 16) || !Aligned(w, 16))
+    return vx::Fail(VX_BAD_ARG,
+                    std::string(what) + ": x and the panels must be 16-byte "
+                                        "aligned");
+  return VX_OK;
+}
+
+int Product(const uint16_t* x, const void* packed, float* y, uint16_t* y_bf16,
+            size_t m, size_t k, size_t n, int accumulate, vx_scratch* scratch,
+            int rg, int waves, int splits, void* stream) {
+  if (m > vx::kExactRows)
+    return vx::RunPrefill(x, packed, y, y_bf16, m, k, n, accumulate != 0,
+                          vx::Stream(stream));
+  const vx::ProductPlan plan = vx::PlanSkinny(
+      m, k, n, scratch != nullptr ? scratch->partial_floats : 0,
+      scratch != nullptr ? scratch->counter_count : 0, rg, waves, splits);
+  return vx::RunSkinny(x, packed, y, y_bf16, m, k, n, accumulate != 0, plan,
+                       scratch != nullptr ? scratch->partials : nullptr,
+                       scratch != nullptr ? scratch->counters : nullptr,
+                       vx::Stream(stream));
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* vx_last_error(void) { return vx::last_error.c_str(); }
+
+int vx_last_hip_error(void) { return vx::last_hip_error; }
+
+const char* vx_version(void) { return "voxcpm_amd 0.1.0 gfx950"; }
+
+int vx_scratch_create(vx_scratch** scratch, size_t max_m, size_t max_n) {
+  if (scratch == nullptr)
+    return vx::Fail(VX_BAD_ARG, "vx_scratch_create: null handle pointer");
+  *scratch = nullptr;
+  if (max_m == 0 || max_n == 0 || max_m > vx::kExactRows || max_n > (1U << 24))
+    return vx::Fail(VX_BAD_ARG,
+                    "vx_scratch_create: max_m must be in 1..128 and max_n "
+                    "positive");
+  auto* created = new vx_scratch();
+  // Up to 16 splits of the largest product; one counter per row group.
+  created->partial_floats = 16 * max_m * max_n;
+  created->counter_count = vx::q8::Groups(max_n);
+  hipError_t error = hipMalloc(reinterpret_cast<void**>(&created->partials),
+                               created->partial_floats * sizeof(float));
+  if (error == hipSuccess)
+    error = hipMalloc(reinterpret_cast<void**>(&created->counters),
+                      created->counter_count * sizeof(unsigned));
+  if (error == hipSuccess)
+    error = hipMemset(created->counters, 0,
+                      created->counter_count * sizeof(unsigned));
+  if (error != hipSuccess) {
+    vx_scratch_destroy(created);
+    return vx::FailHip(error, "vx_scratch_create");
+  }
+  *scratch = created;
+  return vx::Succeed();
+}
+
+void vx_scratch_destroy(vx_scratch* scratch) {
+  if (scratch == nullptr)
+    return;
+  if (scratch->partials != nullptr)
+    (void)hipFree(scratch->partials);
+  if (scratch->counters != nullptr)
+    (void)hipFree(scratch->counters);
+  delete scratch;
+}
+
+int vx_q8_linear(const uint16_t* x, const void* packed, float* y, size_t m,
+                 size_t k, size_t n, int accumulate, vx_scratch* scratch,
+                 void* stream) {
+  VX_TRY(CheckProduct(x, packed, y, m, k, n, "vx_q8_linear"));
+  return Product(x, packed, y, nullptr, m, k, n, accumulate, scratch, 0, 0, 0,
+                 stream);
+}
+
+int vx_q8_linear_bf16(const uint16_t* x, const void* packed, uint16_t* y,
+                      size_t m, size_t k, size_t n, vx_scratch* scratch,
+                      void* stream) {
+  VX_TRY(CheckProduct(x, packed, y, m, k, n, "vx_q8_linear_bf16"));
+  return Product(x, packed, nullptr, y, m, k, n, 0, scratch, 0, 0, 0, stream);
+}
+
+/* Testing and tuning entry (declared in voxcpm_amd_internal.h): the product
+ * with a forced split plan, as PlanWmma's target_waves argument lets the
+ * reference's tests force splits (kernels/wmma_products.hpp:82-85). */
+int vx_q8_linear_planned(const uint16_t* x, const void* packed, float* y,
+                         size_t m, size_t k, size_t n, int accumulate,
+                         vx_scratch* scratch, int row_groups, int waves,
+                         int splits, void* stream) {
+  VX_TRY(CheckProduct(x, packed, y, m, k, n, "vx_q8_linear_planned"));
+  if (m > vx::kExactRows)
+    return vx::Fail(VX_BAD_ARG,
+                    "vx_q8_linear_planned: plans apply to m <= 128");
+  return Product(x, packed, y, nullptr, m, k, n, accumulate, scratch,
+                 row_groups, waves, splits, stream);
+}
+
+/* The plan vx_q8_linear would use: {mt, rg, waves, tiles, splits,
+ * pairs_per_split, pairs_per_wave}. */
+int vx_q8_plan(size_t m, size_t k, size_t n, vx_scratch* scratch,
+               int32_t* out7) {
+  if (out7 == nullptr || m == 0 || m > vx::kExactRows || k % 32 != 0 ||
+      k == 0 || n == 0)
+    return vx::Fail(VX_BAD_ARG, "vx_q8_plan: bad arguments");
+  const vx::ProductPlan plan = vx::PlanSkinny(
+      m, k, n, scratch != nullptr ? scratch->partial_floats : 0,
+      scratch != nullptr ? scratch->counter_count : 0);
+  out7[0] = plan.mt;
+  out7[1] = plan.rg;
+  out7[2] = plan.waves;
+  out7[3] = plan.tiles;
+  out7[4] = plan.splits;
+  out7[5] = plan.pairs_per_split;
+  out7[6] = plan.pairs_per_wave;
+  return vx::Succeed();
+}
+
+}  // extern "C"

@@ -1,0 +1,107 @@
+// Shared helpers of the voxcpm_amd library: error reporting across the C
+// ABI, bfloat16/float16 conversions and the wave64 reductions.
+#ifndef VOXCPM_AMD_COMMON_HPP_
+#define VOXCPM_AMD_COMMON_HPP_
+
+#include <hip/hip_runtime.h>
+
+#include <cstddef>
+#include <cstdint>
+#include <string>
+
+#include "voxcpm_amd.h"
+
+namespace vx {
+
+using Bf16 = std::uint16_t;
+
+// ---- error reporting --------------------------------------------------
+
+/// Records `message` as the calling thread's last error and returns `status`.
+int Fail(int status, const std::string& message);
+/// Records a HIP failure of `what`.
+int FailHip(hipError_t error, const char* what);
+/// Clears the calling thread's last error; returns VX_OK.
+int Succeed();
+
+/// Returns from the enclosing function when `status` is a failure.
+#define VX_TRY(expression)                 \
+  do {                                     \
+    const int vx_status_ = (expression);   \
+    if (vx_status_ != VX_OK)               \
+      return vx_status_;                   \
+  } while (0)
+
+/// Returns VX_HIP_ERROR from the enclosing function on a HIP failure.
+#define VX_HIP(expression, what)                 \
+  do {                                           \
+    const hipError_t vx_error_ = (expression);   \
+    if (vx_error_ != hipSuccess)                 \
+      return ::vx::FailHip(vx_error_, what);     \
+  } while (0)
+
+/// The status of the launches just enqueued.
+int LaunchStatus(const char* what);
+
+inline hipStream_t Stream(void* stream) {
+  return static_cast<hipStream_t>(stream);
+}
+
+// ---- conversions ---------------------------------------------------------
+
+/// float32 -> bfloat16 bits, nearest even; NaNs stay quiet NaNs.
+__host__ __device__ inline Bf16 Bf16Bits(float value) {
+  const std::uint32_t bits = __builtin_bit_cast(std::uint32_t, value);
+  if ((bits & 0x7F800000U) == 0x7F800000U && (bits & 0x007FFFFFU) != 0)
+    return static_cast<Bf16>((bits >> 16U) | 0x40U);
+  return static_cast<Bf16>((bits + 0x7FFFU + ((bits >> 16U) & 1U)) >> 16U);
+}
+
+__host__ __device__ inline float Bf16Value(Bf16 bits) {
+  return __builtin_bit_cast(float, static_cast<std::uint32_t>(bits) << 16U);
+}
+
+/// float16 bits -> float32 (subnormals included; the hardware conversion
+/// keeps them).
+__device__ inline float HalfValue(std::uint16_t bits) {
+  return static_cast<float>(__builtin_bit_cast(_Float16, bits));
+}
+
+// ---- wave64 reductions -----------------------------------------------------
+
+constexpr int kWave = 64;
+
+__device__ inline float WaveSum(float value) {
+#pragma unroll
+  for (int offset = kWave / 2; offset > 0; offset /= 2)
+    value += __shfl_xor(value, offset, kWave);
+  return value;
+}
+
+__device__ inline float WaveMax(float value) {
+#pragma unroll
+  for (int offset = kWave / 2; offset > 0; offset /= 2)
+    value = fmaxf(value, __shfl_xor(value, offset, kWave));
+  return value;
+}
+
+/// Sum over a block of up to 1024 threads; `scratch` holds one float per
+/// wave. Every thread receives the total, added in wave order.
+__device__ inline float BlockSum(float value, float* scratch) {
+  const int lane = threadIdx.x % kWave;
+  const int wave = threadIdx.x / kWave;
+  const int waves = (blockDim.x + kWave - 1) / kWave;
+  value = WaveSum(value);
+  __syncthreads();
+  if (lane == 0)
+    scratch[wave] = value;
+  __syncthreads();
+  float total = scratch[0];
+  for (int w = 1; w < waves; ++w)
+    total += scratch[w];
+  return total;
+}
+
+}  // namespace vx
+
+#endif  // VOXCPM_AMD_COMMON_HPP_

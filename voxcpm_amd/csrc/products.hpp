@@ -1,0 +1,54 @@
+// Internal interface of the Q8_0 product kernels (q8_products.hip,
+// q8_prefill.hip) for the C ABI and the DiT.
+#ifndef VOXCPM_AMD_PRODUCTS_HPP_
+#define VOXCPM_AMD_PRODUCTS_HPP_
+
+#include <hip/hip_runtime.h>
+
+#include <cstddef>
+
+#include "common.hpp"
+
+namespace vx {
+
+/// Rows up to which products keep the exact per-block Q8_0 arithmetic; more
+/// rows take the reference's expansion to bf16(scale * q) (gemm.cpp:48-49,
+/// 272, 305-312).
+constexpr std::size_t kExactRows = 128;
+
+/// How a skinny product is split: `rg` row groups per workgroup, `waves`
+/// waves per workgroup splitting its pairs, `splits` workgroups along k.
+struct ProductPlan {
+  int mt = 1;
+  int rg = 1;
+  int waves = 4;
+  int tiles = 1;
+  int splits = 1;
+  int pairs_per_split = 0;
+  int pairs_per_wave = 0;
+};
+
+/// Largest row-group count per workgroup the kernels have for `mt` tiles.
+int MaxRowGroups(int mt);
+
+/// The plan of an m x k x n product (m <= 128). Positive `rg`, `waves` and
+/// `splits` force those values; the split falls back to 1 when the scratch
+/// cannot hold its partials.
+ProductPlan PlanSkinny(std::size_t m, std::size_t k, std::size_t n,
+                       std::size_t scratch_floats, std::size_t scratch_counters,
+                       int rg = 0, int waves = 0, int splits = 0);
+
+/// Launches the exact product (m <= 128) with `plan`.
+int RunSkinny(const Bf16* x, const void* w, float* y, Bf16* y_bf16,
+              std::size_t m, std::size_t k, std::size_t n, bool accumulate,
+              const ProductPlan& plan, float* partials, unsigned* counters,
+              hipStream_t stream);
+
+/// Launches the expanded product (any m; meant for m > 128).
+int RunPrefill(const Bf16* x, const void* w, float* y, Bf16* y_bf16,
+               std::size_t m, std::size_t k, std::size_t n, bool accumulate,
+               hipStream_t stream);
+
+}  // namespace vx
+
+#endif  // VOXCPM_AMD_PRODUCTS_HPP_

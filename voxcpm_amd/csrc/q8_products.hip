@@ -1,0 +1,377 @@
+// Q8_0 x bfloat16 products on gfx950's matrix cores.
+//
+// Up to 128 activation rows ("skinny", the memory-bound case: the DiT's 22
+// rows, decoding's 1) the Q8_0 arithmetic stays exact: each weight pair of
+// blocks is converted int8 -> bf16 exactly in registers, each 32-column
+// block is one v_mfma_f32_16x16x32_bf16 from zero (a float32 block sum), and
+// acc = fmaf(f16 scale, block sum, acc) applies the block's scale; the
+// arithmetic of kernels/wmma_products.hip:192-215 on wave64 MFMA.
+//
+// Work split: a workgroup owns `rg` row groups (16 weight rows each) and a
+// range of column pairs; its waves split that range and every wave
+// streams all `rg` row groups, so an activation fragment, loaded once from
+// L2, feeds rg x 2 MFMAs. The waves' partial sums meet in LDS and are added
+// in wave order; a product split over several workgroups along k stores
+// per-split partials and the last workgroup of a tile (an atomic counter)
+// adds them in split order and resets the counter. No float atomics: the
+// result is the same on every run.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cstdint>
+
+#include "common.hpp"
+#include "products.hpp"
+#include "q8.hpp"
+
+namespace vx {
+namespace {
+
+using q8::AsBf16x8;
+using q8::Bf16x8;
+using q8::F32x4;
+using q8::Int8x8ToBf16;
+using q8::kUnitBytes;
+using q8::kValueBytes;
+using q8::Mfma16x16x32;
+
+constexpr int kMaxThreads = 512;
+
+struct SkinnyArgs {
+  const Bf16* x;
+  const std::uint8_t* w;
+  float* y;
+  Bf16* y_bf16;  // non-null: bf16 output (no accumulation)
+  float* partials;
+  unsigned* counters;
+  int m, k, n;
+  int pairs;
+  int pairs_per_split;
+  int pairs_per_wave;
+  int splits;
+  int accumulate;
+};
+
+template<int MT, int RG>
+struct Stage {
+  uint4 w[RG];
+  std::uint32_t scales[RG];
+  uint4 a[MT][2];
+};
+
+template<int MT, int RG>
+__global__ __launch_bounds__(kMaxThreads) void SkinnyKernel(SkinnyArgs args) {
+  extern __shared__ float reduce[];  // [waves][RG * MT][4][64]
+  const int lane = threadIdx.x % kWave;
+  const int wave = threadIdx.x / kWave;
+  const int waves = blockDim.x / kWave;
+  const int groups = (args.n + 15) / 16;
+  const int first_group = static_cast<int>(blockIdx.x) * RG;
+  const int split = static_cast<int>(blockIdx.y);
+  const int split_begin = split * args.pairs_per_split;
+  const int split_end = min(split_begin + args.pairs_per_split, args.pairs);
+  const int begin = split_begin + wave * args.pairs_per_wave;
+  const int end = min(begin + args.pairs_per_wave, split_end);
+  const int r16 = lane % 16;
+  const int octet = lane / 16;
+  const int k_blocks = args.k / 32;
+
+  // The lane's bytes in the units of its row groups (groups past the
+  // matrix re-read the last one; their results are dropped).
+  const std::uint8_t* unit[RG];
+#pragma unroll
+  for (int r = 0; r < RG; ++r)
+    unit[r] = args.w +
+              static_cast<std::size_t>(min(first_group + r, groups - 1)) *
+                  args.pairs * kUnitBytes;
+  const Bf16* x_row[MT];
+  bool row_ok[MT];
+#pragma unroll
+  for (int t = 0; t < MT; ++t) {
+    const int row = 16 * t + r16;
+    row_ok[t] = row < args.m;
+    x_row[t] = args.x + static_cast<std::size_t>(row_ok[t] ? row : 0) * args.k +
+               8 * octet;
+  }
+
+  F32x4 acc[RG][MT];
+#pragma unroll
+  for (int r = 0; r < RG; ++r)
+#pragma unroll
+    for (int t = 0; t < MT; ++t)
+      acc[r][t] = F32x4{0.0F, 0.0F, 0.0F, 0.0F};
+
+  const auto load = [&](int pair, Stage<MT, RG>& s) {
+#pragma unroll
+    for (int r = 0; r < RG; ++r) {
+      const std::uint8_t* u = unit[r] + static_cast<std::size_t>(pair) * kUnitBytes;
+      s.w[r] = *reinterpret_cast<const uint4*>(u + 16 * lane);
+      s.scales[r] =
+          *reinterpret_cast<const std::uint32_t*>(u + kValueBytes + 4 * r16);
+    }
+#pragma unroll
+    for (int t = 0; t < MT; ++t)
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        if (row_ok[t] && 2 * pair + h < k_blocks)
+          s.a[t][h] = *reinterpret_cast<const uint4*>(x_row[t] + 64 * pair + 32 * h);
+        else
+          s.a[t][h] = uint4{0U, 0U, 0U, 0U};
+      }
+  };
+  const auto compute = [&](const Stage<MT, RG>& s) {
+    const F32x4 zero{0.0F, 0.0F, 0.0F, 0.0F};
+#pragma unroll
+    for (int r = 0; r < RG; ++r) {
+      const Bf16x8 b0 = Int8x8ToBf16(s.w[r].x, s.w[r].y);
+      const Bf16x8 b1 = Int8x8ToBf16(s.w[r].z, s.w[r].w);
+      const float s0 = HalfValue(static_cast<std::uint16_t>(s.scales[r] & 0xFFFFU));
+      const float s1 = HalfValue(static_cast<std::uint16_t>(s.scales[r] >> 16));
+#pragma unroll
+      for (int t = 0; t < MT; ++t) {
+        const F32x4 sum0 = Mfma16x16x32(AsBf16x8(s.a[t][0]), b0, zero);
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          acc[r][t][i] = fmaf(s0, sum0[i], acc[r][t][i]);
+        const F32x4 sum1 = Mfma16x16x32(AsBf16x8(s.a[t][1]), b1, zero);
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          acc[r][t][i] = fmaf(s1, sum1[i], acc[r][t][i]);
+      }
+    }
+  };
+
+  // Two pairs in flight: the next pair's loads are issued before this
+  // pair's products.
+  Stage<MT, RG> even, odd;
+  if (begin < end)
+    load(begin, even);
+  for (int pair = begin; pair < end; pair += 2) {
+    if (pair + 1 < end)
+      load(pair + 1, odd);
+    compute(even);
+    if (pair + 1 >= end)
+      break;
+    if (pair + 2 < end)
+      load(pair + 2, even);
+    compute(odd);
+  }
+
+  // Writes one finished 16 x 16 fragment (rows 16 t + 4 (lane / 16) + i,
+  // column 16 g + lane % 16).
+  const auto emit = [&](int r, int t, const float* v) {
+    const int column = 16 * (first_group + r) + r16;
+    if (first_group + r >= groups || column >= args.n)
+      return;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int row = 16 * t + 4 * octet + i;
+      if (row >= args.m)
+        continue;
+      const std::size_t at = static_cast<std::size_t>(row) * args.n + column;
+      if (args.splits > 1)
+        args.partials[static_cast<std::size_t>(split) * args.m * args.n + at] =
+            v[i];
+      else if (args.y_bf16 != nullptr)
+        args.y_bf16[at] = Bf16Bits(v[i]);
+      else
+        args.y[at] = args.accumulate ? args.y[at] + v[i] : v[i];
+    }
+  };
+
+  if (waves == 1) {
+#pragma unroll
+    for (int r = 0; r < RG; ++r)
+#pragma unroll
+      for (int t = 0; t < MT; ++t) {
+        float v[4] = {acc[r][t][0], acc[r][t][1], acc[r][t][2], acc[r][t][3]};
+        emit(r, t, v);
+      }
+  } else {
+    constexpr int kFragments = RG * MT;
+    float* mine = reduce + static_cast<std::size_t>(wave) * kFragments * 4 * kWave;
+#pragma unroll
+    for (int r = 0; r < RG; ++r)
+#pragma unroll
+      for (int t = 0; t < MT; ++t)
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          mine[((r * MT + t) * 4 + i) * kWave + lane] = acc[r][t][i];
+    __syncthreads();
+    for (int f = wave; f < kFragments; f += waves) {
+      float v[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        float total = reduce[(f * 4 + i) * kWave + lane];
+        for (int w = 1; w < waves; ++w)
+          total += reduce[((static_cast<std::size_t>(w) * kFragments + f) * 4 + i) *
+                              kWave + lane];
+        v[i] = total;
+      }
+      emit(f / MT, f % MT, v);
+    }
+  }
+  if (args.splits == 1)
+    return;
+
+  // Split along k: the last workgroup of this tile adds the partials.
+  __shared__ unsigned last;
+  __threadfence();
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    const unsigned previous = __hip_atomic_fetch_add(
+        args.counters + blockIdx.x, 1U, __ATOMIC_ACQ_REL,
+        __HIP_MEMORY_SCOPE_AGENT);
+    last = previous + 1 == static_cast<unsigned>(args.splits) ? 1U : 0U;
+  }
+  __syncthreads();
+  if (last == 0)
+    return;
+  __threadfence();
+  const int columns = 16 * RG;
+  const int elements = columns * 16 * MT;
+  for (int e = threadIdx.x; e < elements; e += blockDim.x) {
+    const int column = 16 * first_group + e % columns;
+    const int row = e / columns;
+    if (column >= args.n || row >= args.m)
+      continue;
+    const std::size_t at = static_cast<std::size_t>(row) * args.n + column;
+    const std::size_t stride = static_cast<std::size_t>(args.m) * args.n;
+    float total = __hip_atomic_load(args.partials + at, __ATOMIC_RELAXED,
+                                    __HIP_MEMORY_SCOPE_AGENT);
+    for (int s = 1; s < args.splits; ++s)
+      total += __hip_atomic_load(args.partials + s * stride + at,
+                                 __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (args.y_bf16 != nullptr)
+      args.y_bf16[at] = Bf16Bits(total);
+    else
+      args.y[at] = args.accumulate ? args.y[at] + total : total;
+  }
+  if (threadIdx.x == 0)
+    __hip_atomic_store(args.counters + blockIdx.x, 0U, __ATOMIC_RELAXED,
+                       __HIP_MEMORY_SCOPE_AGENT);
+}
+
+template<int MT, int RG>
+void LaunchSkinny(const SkinnyArgs& args, const ProductPlan& plan,
+                  hipStream_t stream) {
+  const dim3 grid(static_cast<unsigned>(plan.tiles),
+                  static_cast<unsigned>(plan.splits));
+  const std::size_t shared =
+      plan.waves > 1 ? static_cast<std::size_t>(plan.waves) * RG * MT * 4 *
+                           kWave * sizeof(float)
+                     : 0;
+  SkinnyKernel<MT, RG><<<grid, plan.waves * kWave, shared, stream>>>(args);
+}
+
+using Launcher = void (*)(const SkinnyArgs&, const ProductPlan&, hipStream_t);
+
+template<int MT>
+Launcher PickRg(int rg) {
+  if constexpr (MT * 4 <= 8) {
+    if (rg == 4)
+      return LaunchSkinny<MT, 4>;
+  }
+  if constexpr (MT * 2 <= 8) {
+    if (rg == 2)
+      return LaunchSkinny<MT, 2>;
+  }
+  if (rg == 1)
+    return LaunchSkinny<MT, 1>;
+  return nullptr;
+}
+
+Launcher PickLauncher(int mt, int rg) {
+  switch (mt) {
+    case 1: return PickRg<1>(rg);
+    case 2: return PickRg<2>(rg);
+    case 3: return PickRg<3>(rg);
+    case 4: return PickRg<4>(rg);
+    case 5: return PickRg<5>(rg);
+    case 6: return PickRg<6>(rg);
+    case 7: return PickRg<7>(rg);
+    case 8: return PickRg<8>(rg);
+    default: return nullptr;
+  }
+}
+
+}  // namespace
+
+int MaxRowGroups(int mt) {
+  if (mt * 4 <= 8)
+    return 4;
+  if (mt * 2 <= 8)
+    return 2;
+  return 1;
+}
+
+ProductPlan PlanSkinny(std::size_t m, std::size_t k, std::size_t n,
+                       std::size_t scratch_floats,
+                       std::size_t scratch_counters, int rg, int waves,
+                       int splits) {
+  ProductPlan plan;
+  plan.mt = static_cast<int>((m + 15) / 16);
+  const int groups = static_cast<int>(q8::Groups(n));
+  const int pairs = static_cast<int>(q8::Pairs(k));
+  if (rg <= 0) {
+    // Wide products reuse each activation fragment for two row groups.
+    rg = groups >= 1024 ? 2 : 1;
+  }
+  rg = std::min(rg, MaxRowGroups(plan.mt));
+  if (waves <= 0) {
+    waves = 4;
+    while (waves > 1 && pairs < 2 * waves)
+      waves /= 2;
+  }
+  waves = std::max(1, std::min(waves, kMaxThreads / kWave));
+  plan.rg = rg;
+  plan.waves = waves;
+  plan.tiles = (groups + rg - 1) / rg;
+  if (splits <= 0) {
+    // Fewer tiles than compute units: split k over workgroups, keeping at
+    // least two pairs per wave.
+    splits = 1;
+    while (plan.tiles * splits < 256 &&
+           pairs >= 4 * waves * splits)
+      splits *= 2;
+  }
+  splits = std::max(1, std::min(splits, pairs));
+  plan.pairs_per_split = (pairs + splits - 1) / splits;
+  plan.splits = (pairs + plan.pairs_per_split - 1) / plan.pairs_per_split;
+  if (plan.splits > 1 &&
+      (scratch_floats < static_cast<std::size_t>(plan.splits) * m * n ||
+       scratch_counters < static_cast<std::size_t>(plan.tiles))) {
+    plan.splits = 1;
+    plan.pairs_per_split = pairs;
+  }
+  plan.pairs_per_wave = (plan.pairs_per_split + waves - 1) / waves;
+  return plan;
+}
+
+int RunSkinny(const Bf16* x, const void* w, float* y, Bf16* y_bf16,
+              std::size_t m, std::size_t k, std::size_t n, bool accumulate,
+              const ProductPlan& plan, float* partials, unsigned* counters,
+              hipStream_t stream) {
+  const Launcher launch = PickLauncher(plan.mt, plan.rg);
+  if (launch == nullptr)
+    return Fail(VX_UNSUPPORTED, "no product kernel for this plan");
+  SkinnyArgs args;
+  args.x = x;
+  args.w = static_cast<const std::uint8_t*>(w);
+  args.y = y;
+  args.y_bf16 = y_bf16;
+  args.partials = partials;
+  args.counters = counters;
+  args.m = static_cast<int>(m);
+  args.k = static_cast<int>(k);
+  args.n = static_cast<int>(n);
+  args.pairs = static_cast<int>(q8::Pairs(k));
+  args.pairs_per_split = plan.pairs_per_split;
+  args.pairs_per_wave = plan.pairs_per_wave;
+  args.splits = plan.splits;
+  args.accumulate = accumulate ? 1 : 0;
+  launch(args, plan, stream);
+  return LaunchStatus("q8 product");
+}
+
+}  // namespace vx

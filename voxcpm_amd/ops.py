@@ -1,0 +1,259 @@
+"""Python entry points over the C ABI, with torch tensors as device memory.
+
+Every function calls libvoxcpm_amd.so; torch only allocates device memory
+and supplies the stream. bf16 tensors are torch.bfloat16 (the same bits as
+the ABI's uint16 bfloat16).
+"""
+from __future__ import annotations
+
+import ctypes
+
+import numpy as np
+import torch
+
+from . import synth
+from ._lib import DitLayer, DitProjection, DitShape, DitWeights, check, lib
+
+__all__ = [
+    "Scratch", "Dit", "q8_pack", "q8_unpack_blocks", "q8_unpack_bf16",
+    "q8_linear", "q8_linear_bf16", "q8_plan", "euler_schedule", "rope_table",
+]
+
+
+def _ptr(tensor: torch.Tensor | None) -> ctypes.c_void_p | None:
+    return None if tensor is None else ctypes.c_void_p(tensor.data_ptr())
+
+
+def _stream(stream: torch.cuda.Stream | None) -> ctypes.c_void_p:
+    stream = stream or torch.cuda.current_stream()
+    return ctypes.c_void_p(stream.cuda_stream)
+
+
+def _device(device) -> torch.device:
+    return torch.device(device if device is not None else "cuda")
+
+
+# ---- Q8_0 panels -----------------------------------------------------------
+
+def q8_pack(blocks: torch.Tensor, n: int, k: int, stream=None) -> torch.Tensor:
+    """GGML Q8_0 blocks (uint8 [n][k/32][34] on the device) -> panels."""
+    packed = torch.empty(lib().vx_q8_packed_bytes(n, k), dtype=torch.uint8,
+                         device=blocks.device)
+    check(lib().vx_q8_pack(_ptr(blocks), n, k, _ptr(packed), _stream(stream)))
+    return packed
+
+
+def q8_unpack_blocks(packed: torch.Tensor, n: int, k: int,
+                     stream=None) -> torch.Tensor:
+    blocks = torch.empty((n, k // 32, 34), dtype=torch.uint8,
+                         device=packed.device)
+    check(lib().vx_q8_unpack_blocks(_ptr(packed), n, k, _ptr(blocks),
+                                    _stream(stream)))
+    return blocks
+
+
+def q8_unpack_bf16(packed: torch.Tensor, n: int, k: int,
+                   stream=None) -> torch.Tensor:
+    out = torch.empty((n, k), dtype=torch.bfloat16, device=packed.device)
+    check(lib().vx_q8_unpack_bf16(_ptr(packed), n, k, _ptr(out),
+                                  _stream(stream)))
+    return out
+
+
+class Scratch:
+    """vx_scratch: split-reduction scratch of the products."""
+
+    def __init__(self, max_m: int, max_n: int):
+        handle = ctypes.c_void_p()
+        check(lib().vx_scratch_create(ctypes.byref(handle), max_m, max_n))
+        self.handle = handle
+
+    def close(self) -> None:
+        if self.handle:
+            lib().vx_scratch_destroy(self.handle)
+            self.handle = ctypes.c_void_p()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+def q8_linear(x: torch.Tensor, packed: torch.Tensor, n: int,
+              y: torch.Tensor | None = None, accumulate: bool = False,
+              scratch: Scratch | None = None, plan: tuple | None = None,
+              stream=None) -> torch.Tensor:
+    """y[m][n] (+)= x[m][k] W^T; x bf16 [m][k], y float32 [m][n].
+
+    `plan` = (row_groups, waves, splits) forces the split (m <= 128)."""
+    m, k = x.shape
+    if y is None:
+        y = torch.empty((m, n), dtype=torch.float32, device=x.device)
+    handle = scratch.handle if scratch is not None else None
+    if plan is None:
+        status = lib().vx_q8_linear(_ptr(x), _ptr(packed), _ptr(y), m, k, n,
+                                    int(accumulate), handle, _stream(stream))
+    else:
+        status = lib().vx_q8_linear_planned(
+            _ptr(x), _ptr(packed), _ptr(y), m, k, n, int(accumulate), handle,
+            plan[0], plan[1], plan[2], _stream(stream))
+    check(status)
+    return y
+
+
+def q8_linear_bf16(x: torch.Tensor, packed: torch.Tensor, n: int,
+                   y: torch.Tensor | None = None,
+                   scratch: Scratch | None = None, stream=None) -> torch.Tensor:
+    m, k = x.shape
+    if y is None:
+        y = torch.empty((m, n), dtype=torch.bfloat16, device=x.device)
+    handle = scratch.handle if scratch is not None else None
+    check(lib().vx_q8_linear_bf16(_ptr(x), _ptr(packed), _ptr(y), m, k, n,
+                                  handle, _stream(stream)))
+    return y
+
+
+def q8_plan(m: int, k: int, n: int, scratch: Scratch | None = None) -> dict:
+    out = (ctypes.c_int32 * 7)()
+    check(lib().vx_q8_plan(m, k, n, scratch.handle if scratch else None, out))
+    names = ("mt", "rg", "waves", "tiles", "splits", "pairs_per_split",
+             "pairs_per_wave")
+    return dict(zip(names, list(out)))
+
+
+# ---- host-side schedule and tables -----------------------------------------
+
+def euler_schedule(timesteps: int, sway: float = 1.0, skip: bool = True):
+    """(t, dt, evaluate) numpy arrays of EulerSchedule."""
+    t = np.zeros(timesteps, dtype=np.float32)
+    dt = np.zeros(timesteps, dtype=np.float32)
+    evaluate = np.zeros(timesteps, dtype=np.int32)
+    check(lib().vx_euler_schedule(timesteps, sway, int(skip),
+                                  t.ctypes.data, dt.ctypes.data,
+                                  evaluate.ctypes.data))
+    return t, dt, evaluate
+
+
+def rope_table(theta: float, dim: int, factors, scaling: float,
+               positions: int) -> np.ndarray:
+    table = np.zeros((positions, dim), dtype=np.float32)
+    f = None
+    if factors is not None:
+        f = np.ascontiguousarray(factors, dtype=np.float64)
+    check(lib().vx_rope_table(theta, dim, None if f is None else f.ctypes.data,
+                              scaling, positions, table.ctypes.data))
+    return table
+
+
+# ---- the DiT -----------------------------------------------------------------
+
+class Dit:
+    """vx_dit over device copies of synthetic (or given) host weights."""
+
+    def __init__(self, weights: synth.DitWeightsHost, device=None,
+                 stream=None):
+        self.config = config = weights.config
+        device = _device(device)
+        self._keep = []
+
+        def upload_q8(blocks: np.ndarray) -> torch.Tensor:
+            n, kb, _ = blocks.shape
+            raw = torch.from_numpy(np.ascontiguousarray(blocks)).to(device)
+            packed = q8_pack(raw, n, kb * 32, stream)
+            self._keep.append(packed)
+            return packed
+
+        def upload_bf16(bits: np.ndarray) -> torch.Tensor:
+            tensor = torch.from_numpy(bits.view(np.int16).copy()).to(device)
+            self._keep.append(tensor)
+            return tensor
+
+        layer_array = (DitLayer * config.layers)()
+        for index, layer in enumerate(weights.layers):
+            layer_array[index] = DitLayer(
+                upload_bf16(layer["input_norm"]).data_ptr(),
+                upload_q8(layer["qkv"]).data_ptr(),
+                upload_q8(layer["o"]).data_ptr(),
+                upload_bf16(layer["post_norm"]).data_ptr(),
+                upload_q8(layer["gate_up"]).data_ptr(),
+                upload_q8(layer["down"]).data_ptr())
+        projections = {}
+        for name in synth.PROJECTIONS:
+            if name in weights.projections:
+                blocks, bias = weights.projections[name]
+                projections[name] = DitProjection(
+                    upload_q8(blocks).data_ptr(), upload_bf16(bias).data_ptr())
+            else:
+                projections[name] = DitProjection(None, None)
+        rope_ptr = None
+        if weights.rope is not None:
+            rope = torch.from_numpy(np.ascontiguousarray(
+                weights.rope, dtype=np.float32)).to(device)
+            self._keep.append(rope)
+            rope_ptr = rope.data_ptr()
+        self._layers = layer_array
+        self._weights = DitWeights(
+            layer_array, upload_bf16(weights.norm).data_ptr(), rope_ptr,
+            **projections)
+        self._shape = DitShape(
+            config.hidden, config.heads, config.kv_heads, config.head_dim,
+            config.ffn, config.layers, config.patch, config.feat,
+            config.time_in, int(config.has_delta), config.eps)
+        torch.cuda.synchronize(device)
+        handle = ctypes.c_void_p()
+        check(lib().vx_dit_create(ctypes.byref(handle),
+                                  ctypes.byref(self._shape),
+                                  ctypes.byref(self._weights)))
+        self.handle = handle
+        self.device = device
+
+    def close(self) -> None:
+        if getattr(self, "handle", None):
+            lib().vx_dit_destroy(self.handle)
+            self.handle = ctypes.c_void_p()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def _f32(self, *shape) -> torch.Tensor:
+        return torch.empty(shape, dtype=torch.float32, device=self.device)
+
+    def time_vector(self, t: float, stream=None) -> torch.Tensor:
+        out = self._f32(self.config.hidden)
+        check(lib().vx_dit_time_vector(self.handle, t, _ptr(out),
+                                       _stream(stream)))
+        return out
+
+    def cond_rows(self, cond_latent: torch.Tensor, stream=None) -> torch.Tensor:
+        out = self._f32(self.config.patch, self.config.hidden)
+        check(lib().vx_dit_cond_rows(self.handle, _ptr(cond_latent), _ptr(out),
+                                     _stream(stream)))
+        return out
+
+    def eval(self, mu, cond_rows, x, time_vector, stream=None) -> torch.Tensor:
+        out = self._f32(2, self.config.patch, self.config.feat)
+        check(lib().vx_dit_eval(self.handle, _ptr(mu), _ptr(cond_rows), _ptr(x),
+                                _ptr(time_vector), _ptr(out), _stream(stream)))
+        return out
+
+    def velocity(self, mu, cond_latent, x, t: float, stream=None) -> torch.Tensor:
+        out = self._f32(2, self.config.patch, self.config.feat)
+        check(lib().vx_dit_velocity(self.handle, _ptr(mu), _ptr(cond_latent),
+                                    _ptr(x), t, _ptr(out), _stream(stream)))
+        return out
+
+    def patch(self, mu, cond_latent, x, t, dt, evaluate, cfg: float,
+              zero_star: bool, stream=None) -> torch.Tensor:
+        """Runs the sampler in place on x; returns x."""
+        t = np.ascontiguousarray(t, dtype=np.float32)
+        dt = np.ascontiguousarray(dt, dtype=np.float32)
+        evaluate = np.ascontiguousarray(evaluate, dtype=np.int32)
+        check(lib().vx_dit_patch(
+            self.handle, _ptr(mu), _ptr(cond_latent), _ptr(x), t.ctypes.data,
+            dt.ctypes.data, evaluate.ctypes.data, len(t), cfg, int(zero_star),
+            _stream(stream)))
+        return x
