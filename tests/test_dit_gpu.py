@@ -1,0 +1,276 @@
+"""The DiT's kernels, one evaluation and the whole sampler on the GPU
+against the CPU oracle, on identical seeded inputs.
+
+Tolerances (fp32 accumulation, bf16 activations): elementwise kernels whose
+outputs are float32 agree to 1e-5 relative; bf16 outputs to one bf16 ulp
+(a rounding boundary may fall differently after float32 reassociation).
+DiT velocities and patch latents: max |gpu - oracle| / max |oracle| <= 1e-2
+and cosine >= 0.9999 per patch -- the bound the workload states -- while
+the measured errors are reported far below it.
+"""
+import numpy as np
+import pytest
+import torch
+
+from voxcpm_amd import synth
+
+pytestmark = pytest.mark.gpu
+
+
+def dev(array, cuda):
+    array = np.ascontiguousarray(array)
+    if array.dtype == np.uint16:
+        return torch.from_numpy(array.view(np.int16).copy()).to(cuda).view(torch.bfloat16)
+    return torch.from_numpy(array.copy()).to(cuda)
+
+
+def host_bf16(t):
+    return t.view(torch.int16).cpu().numpy().view(np.uint16)
+
+
+def ulp_diff(a_bits, b_bits):
+    a = a_bits.astype(np.int32)
+    b = b_bits.astype(np.int32)
+    # map sign-magnitude to a monotone integer line
+    a = np.where(a & 0x8000, 0x8000 - a, a)
+    b = np.where(b & 0x8000, 0x8000 - b, b)
+    return np.abs(a - b)
+
+
+def rel_max(a, b):
+    return float(np.max(np.abs(a - b)) / max(np.max(np.abs(b)), 1e-30))
+
+
+def cosine(a, b):
+    a = a.ravel().astype(np.float64)
+    b = b.ravel().astype(np.float64)
+    return float(a @ b / (np.linalg.norm(a) * np.linalg.norm(b)))
+
+
+def vxlib():
+    from voxcpm_amd._lib import check, lib
+    return lib(), check
+
+
+_HELD = []
+
+
+@pytest.fixture(autouse=True)
+def _release_held():
+    yield
+    torch.cuda.synchronize()
+    _HELD.clear()
+
+
+def ptr(t):
+    return t.data_ptr()
+
+
+def hold(t):
+    """data_ptr of a tensor kept alive until the test ends (a temporary's
+    memory would return to torch's allocator before the kernel runs)."""
+    _HELD.append(t)
+    return t.data_ptr()
+
+
+def stream_ptr():
+    return torch.cuda.current_stream().cuda_stream
+
+
+# ---- kernels -----------------------------------------------------------------
+
+@pytest.mark.parametrize("rows,width,eps", [(22, 1024, 1e-6), (8, 1024, 1e-5), (3, 256, 1e-5)])
+def test_rms_norm(vx, oracle, cuda, stream, rows, width, eps):
+    L, check = vxlib()
+    rng = synth.Rng(20, rows)
+    x = rng.normal(rows * width, 2.0).astype(np.float32).reshape(rows, width)
+    gamma = synth.bf16_vector(rng, width, 1.0, 0.02)
+    out = torch.empty((rows, width), dtype=torch.bfloat16, device=cuda)
+    out32 = torch.empty((rows, width), dtype=torch.float32, device=cuda)
+    check(L.vx_rms_norm(hold(dev(x, cuda)), hold(dev(gamma, cuda)), ptr(out), ptr(out32),
+                        rows, width, eps, stream_ptr()))
+    ref = np.zeros((rows, width), np.uint16)
+    ref32 = np.zeros((rows, width), np.float32)
+    oracle.lib().vo_rms_norm(oracle.ptr(x), oracle.ptr(gamma), oracle.ptr(ref),
+                             oracle.ptr(ref32), rows, width, eps)
+    torch.cuda.synchronize()
+    assert rel_max(out32.cpu().numpy(), ref32) < 1e-5
+    assert ulp_diff(host_bf16(out), ref).max() <= 1
+
+
+@pytest.mark.parametrize("heads,kv_heads,head_dim,rope", [
+    (16, 16, 64, True), (16, 2, 128, True), (4, 1, 32, False)])
+def test_qkv_rope_and_attention(vx, oracle, cuda, stream, heads, kv_heads, head_dim, rope):
+    L, check = vxlib()
+    rng = synth.Rng(21, head_dim)
+    length, rows = 11, 22
+    width = (heads + 2 * kv_heads) * head_dim
+    qkv = rng.normal(rows * width).astype(np.float32).reshape(rows, width)
+    table = oracle.rope_table(10000.0, head_dim, synth.VOXCPM2_SHORT_FACTORS
+                              if head_dim == 128 else None, 1.0, length) if rope else None
+    positions = (np.arange(rows) % length).astype(np.int32)
+    cache_rows = np.arange(rows, dtype=np.int32)
+    q = torch.zeros((rows, heads, head_dim), dtype=torch.float32, device=cuda)
+    kc = torch.zeros((kv_heads, rows, head_dim), dtype=torch.float32, device=cuda)
+    vc = torch.zeros((kv_heads, rows, head_dim), dtype=torch.float32, device=cuda)
+    table_d = dev(table, cuda) if rope else None
+    check(L.vx_qkv_rope(hold(dev(qkv, cuda)), ptr(table_d) if rope else None,
+                        hold(dev(positions, cuda)), hold(dev(cache_rows, cuda)), ptr(q),
+                        ptr(kc), ptr(vc), rows, heads, kv_heads, head_dim, rows,
+                        stream_ptr()))
+    rq = np.zeros((rows, heads, head_dim), np.float32)
+    rk = np.zeros((kv_heads, rows, head_dim), np.float32)
+    rv = np.zeros((kv_heads, rows, head_dim), np.float32)
+    oracle.lib().vo_qkv_rope(oracle.ptr(qkv), oracle.ptr(table), oracle.ptr(positions),
+                             oracle.ptr(cache_rows), oracle.ptr(rq), oracle.ptr(rk),
+                             oracle.ptr(rv), rows, heads, kv_heads, head_dim, rows)
+    torch.cuda.synchronize()
+    assert rel_max(q.cpu().numpy(), rq) < 1e-6
+    assert rel_max(kc.cpu().numpy(), rk) < 1e-6
+    assert np.array_equal(vc.cpu().numpy(), rv)
+    out = torch.empty((rows, heads, head_dim), dtype=torch.bfloat16, device=cuda)
+    for causal in (0, 1):
+        check(L.vx_attention(ptr(q), ptr(kc), ptr(vc), ptr(out), rows, length, length,
+                             0, causal, heads, kv_heads, head_dim, rows, stream_ptr()))
+        ref = np.zeros((rows, heads, head_dim), np.uint16)
+        oracle.lib().vo_attention(oracle.ptr(rq), oracle.ptr(rk), oracle.ptr(rv),
+                                  oracle.ptr(ref), rows, length, length, 0, causal,
+                                  heads, kv_heads, head_dim, rows)
+        torch.cuda.synchronize()
+        assert ulp_diff(host_bf16(out), ref).max() <= 2
+
+
+def test_elementwise_kernels(vx, oracle, cuda, stream):
+    L, check = vxlib()
+    rng = synth.Rng(22, 0)
+    rows, width = 22, 4096
+    gu = rng.normal(rows * 2 * width, 2.0).astype(np.float32).reshape(rows, 2 * width)
+    out = torch.empty((rows, width), dtype=torch.bfloat16, device=cuda)
+    check(L.vx_swiglu(hold(dev(gu, cuda)), ptr(out), rows, width, stream_ptr()))
+    ref = np.zeros((rows, width), np.uint16)
+    oracle.lib().vo_swiglu(oracle.ptr(gu), oracle.ptr(ref), rows, width)
+    torch.cuda.synchronize()
+    assert ulp_diff(host_bf16(out), ref).max() <= 1
+    data = rng.normal(rows * 1024).astype(np.float32).reshape(rows, 1024)
+    bias = synth.bf16_vector(rng, 1024, 0.0, 0.02)
+    d = dev(data, cuda)
+    check(L.vx_add_bias(ptr(d), hold(dev(bias, cuda)), rows, 1024, stream_ptr()))
+    ref = data.copy()
+    oracle.lib().vo_add_bias(oracle.ptr(ref), oracle.ptr(bias), rows, 1024)
+    torch.cuda.synchronize()
+    assert np.array_equal(d.cpu().numpy(), ref)
+    for silu in (0, 1):
+        o = torch.empty(data.size, dtype=torch.bfloat16, device=cuda)
+        check(L.vx_to_bf16(hold(dev(data, cuda)), ptr(o), data.size, silu, stream_ptr()))
+        r = np.zeros(data.size, np.uint16)
+        oracle.lib().vo_to_bf16(oracle.ptr(data), oracle.ptr(r), data.size, silu)
+        torch.cuda.synchronize()
+        assert ulp_diff(host_bf16(o), r).max() <= (1 if silu else 0)
+    # assemble + gather: exact indexing
+    patch, w = 4, 1024
+    mu = rng.normal(2 * w).astype(np.float32)
+    time = rng.normal(w).astype(np.float32)
+    cond = rng.normal(patch * w).astype(np.float32)
+    x = rng.normal(patch * w).astype(np.float32)
+    out = torch.empty((22, w), dtype=torch.float32, device=cuda)
+    check(L.vx_assemble_dit(*(hold(dev(a, cuda)) for a in (mu, time, cond, x)), ptr(out),
+                            patch, w, stream_ptr()))
+    ref = np.zeros((22, w), np.float32)
+    oracle.lib().vo_assemble_dit(oracle.ptr(mu), oracle.ptr(time), oracle.ptr(cond),
+                                 oracle.ptr(x), oracle.ptr(ref), patch, w)
+    idx = np.array([7, 8, 9, 10, 18, 19, 20, 21], np.int32)
+    g = torch.empty((8, w), dtype=torch.float32, device=cuda)
+    check(L.vx_gather_rows(ptr(out), hold(dev(idx, cuda)), ptr(g), 8, w, stream_ptr()))
+    torch.cuda.synchronize()
+    assert np.array_equal(out.cpu().numpy(), ref)
+    assert np.array_equal(g.cpu().numpy(), ref[idx])
+
+
+@pytest.mark.parametrize("zero_star", [0, 1])
+def test_guided_euler(vx, oracle, cuda, stream, zero_star):
+    L, check = vxlib()
+    rng = synth.Rng(23, zero_star)
+    count = 256
+    v = rng.normal(2 * count).astype(np.float32)
+    x = rng.normal(count).astype(np.float32)
+    xd = dev(x, cuda)
+    check(L.vx_guided_euler(hold(dev(v, cuda)), ptr(xd), count, 2.0, 0.0980898, zero_star,
+                            stream_ptr()))
+    ref = x.copy()
+    oracle.lib().vo_guided_euler(oracle.ptr(v), oracle.ptr(ref), count, 2.0, 0.0980898,
+                                 zero_star)
+    torch.cuda.synchronize()
+    assert rel_max(xd.cpu().numpy(), ref) < 1e-5
+
+
+# ---- the DiT ---------------------------------------------------------------------
+
+def make_dit(config, seed, vx, oracle, cuda):
+    length = 3 + 2 * config.patch
+    rope = oracle.rope_table(config.rope_theta, config.head_dim, config.rope_factors,
+                             config.rope_scaling, length)
+    weights = synth.dit_weights(config, seed, rope)
+    return weights, vx.Dit(weights, cuda), oracle.OracleDit(weights, threads=16)
+
+
+SMALL = synth.DitConfig(layers=2)
+SMALL_REAL = synth.dataclasses.replace(synth.VOXCPM2_DIT, layers=2)
+
+
+@pytest.mark.parametrize("config", [SMALL, SMALL_REAL], ids=["synthetic", "voxcpm2"])
+def test_time_and_cond(vx, oracle, cuda, stream, config):
+    weights, dit, odit = make_dit(config, 30, vx, oracle, cuda)
+    inputs = synth.patch_inputs(config, 31)
+    for t in (1.0, 0.63, 0.1876884):
+        got = dit.time_vector(t).cpu().numpy()
+        ref = odit.time_vector(t)
+        assert rel_max(got, ref) < 1e-4, t
+    got = dit.cond_rows(dev(inputs.cond_latent, cuda)).cpu().numpy()
+    assert rel_max(got, odit.cond_rows(inputs.cond_latent)) < 1e-5
+
+
+@pytest.mark.parametrize("config", [
+    synth.DitConfig(layers=1),  # one block of the synthetic DiT
+    SMALL_REAL,
+], ids=["synthetic-block", "voxcpm2-2layers"])
+def test_dit_velocity(vx, oracle, cuda, stream, config):
+    weights, dit, odit = make_dit(config, 32, vx, oracle, cuda)
+    inputs = synth.patch_inputs(config, 33)
+    mu, cond, x = (dev(a, cuda) for a in (inputs.mu, inputs.cond_latent, inputs.noise))
+    got = dit.velocity(mu, cond, x, 0.63).cpu().numpy()
+    ref = odit.velocity(inputs.mu, inputs.cond_latent, inputs.noise, 0.63)
+    error, cos = rel_max(got, ref), cosine(got, ref)
+    print(f"velocity rel-max {error:.2e} cosine {cos:.8f}")
+    assert error <= 1e-2 and cos >= 0.9999
+    # Bitwise run-to-run determinism.
+    again = dit.velocity(mu, cond, x, 0.63).cpu().numpy()
+    assert np.array_equal(got, again)
+
+
+@pytest.mark.parametrize("config", [synth.SYNTHETIC_DIT, synth.VOXCPM2_DIT],
+                         ids=["synthetic-12x10", "voxcpm2-12x10"])
+def test_dit_patch_full(vx, oracle, cuda, stream, config):
+    """The full sampler: 12 blocks, 10 Euler steps (the synthetic workload:
+    uniform, plain CFG 2.0; the released model: sway schedule, CFG-Zero*),
+    replayed as a HIP graph twice (same result both times)."""
+    weights, dit, odit = make_dit(config, 34, vx, oracle, cuda)
+    inputs = synth.patch_inputs(config, 35)
+    from voxcpm_amd import ops
+    t, dt, ev = ops.euler_schedule(config.steps, config.sway, config.skip)
+    mu, cond = dev(inputs.mu, cuda), dev(inputs.cond_latent, cuda)
+    x = dev(inputs.noise, cuda)
+    dit.patch(mu, cond, x, t, dt, ev, config.cfg, config.zero_star)
+    got = x.cpu().numpy()
+    x.copy_(dev(inputs.noise, cuda))
+    dit.patch(mu, cond, x, t, dt, ev, config.cfg, config.zero_star)  # graph replay
+    replay = x.cpu().numpy()
+    x2 = dev(inputs.noise, cuda)  # another buffer: a new graph
+    dit.patch(mu, cond, x2, t, dt, ev, config.cfg, config.zero_star)
+    torch.cuda.synchronize()
+    assert np.array_equal(replay, got)
+    assert np.array_equal(x2.cpu().numpy(), got)
+    ref = odit.patch(inputs.mu, inputs.cond_latent, inputs.noise, t, dt, ev,
+                     config.cfg, config.zero_star)
+    error, cos = rel_max(got, ref), cosine(got, ref)
+    print(f"patch rel-max {error:.2e} cosine {cos:.8f}")
+    assert error <= 1e-2 and cos >= 0.9999

@@ -30,6 +30,8 @@ struct ProductPlan {
 
 /// Largest row-group count per workgroup the kernels have for `mt` tiles.
 int MaxRowGroups(int mt);
+/// Largest wave count per workgroup of the kernel for (`mt`, `rg`).
+int MaxWaves(int mt, int rg);
 
 /// The plan of an m x k x n product (m <= 128). Positive `rg`, `waves` and
 /// `splits` force those values; the split falls back to 1 when the scratch

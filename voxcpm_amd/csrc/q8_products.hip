@@ -35,7 +35,11 @@ using q8::kUnitBytes;
 using q8::kValueBytes;
 using q8::Mfma16x16x32;
 
-constexpr int kMaxThreads = 512;
+// Workgroups of up to 16 waves (1024 threads) split a tile's pairs for the
+// smaller register footprints; the others take up to 8 waves.
+constexpr int kMaxThreads = 1024;
+
+constexpr int ThreadsFor(int mt, int rg) { return mt * rg <= 2 ? 1024 : 512; }
 
 struct SkinnyArgs {
   const Bf16* x;
@@ -59,8 +63,8 @@ struct Stage {
   uint4 a[MT][2];
 };
 
-template<int MT, int RG>
-__global__ __launch_bounds__(kMaxThreads) void SkinnyKernel(SkinnyArgs args) {
+template<int MT, int RG, int kThreads>
+__global__ __launch_bounds__(kThreads) void SkinnyKernel(SkinnyArgs args) {
   extern __shared__ float reduce[];  // [waves][RG * MT][4][64]
   const int lane = threadIdx.x % kWave;
   const int wave = threadIdx.x / kWave;
@@ -214,20 +218,24 @@ __global__ __launch_bounds__(kMaxThreads) void SkinnyKernel(SkinnyArgs args) {
   if (args.splits == 1)
     return;
 
-  // Split along k: the last workgroup of this tile adds the partials.
+  // Split along k: the last workgroup of this tile adds the partials. The
+  // barrier orders every wave's partial stores before thread 0's release
+  // (one L2 write-back per workgroup); only the last workgroup acquires
+  // (one L2 invalidation per tile), and its barrier orders the acquire
+  // before every wave's loads.
   __shared__ unsigned last;
-  __threadfence();
   __syncthreads();
   if (threadIdx.x == 0) {
     const unsigned previous = __hip_atomic_fetch_add(
-        args.counters + blockIdx.x, 1U, __ATOMIC_ACQ_REL,
+        args.counters + blockIdx.x, 1U, __ATOMIC_RELEASE,
         __HIP_MEMORY_SCOPE_AGENT);
     last = previous + 1 == static_cast<unsigned>(args.splits) ? 1U : 0U;
+    if (last != 0)
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
   }
   __syncthreads();
   if (last == 0)
     return;
-  __threadfence();
   const int columns = 16 * RG;
   const int elements = columns * 16 * MT;
   for (int e = threadIdx.x; e < elements; e += blockDim.x) {
@@ -237,11 +245,9 @@ __global__ __launch_bounds__(kMaxThreads) void SkinnyKernel(SkinnyArgs args) {
       continue;
     const std::size_t at = static_cast<std::size_t>(row) * args.n + column;
     const std::size_t stride = static_cast<std::size_t>(args.m) * args.n;
-    float total = __hip_atomic_load(args.partials + at, __ATOMIC_RELAXED,
-                                    __HIP_MEMORY_SCOPE_AGENT);
+    float total = args.partials[at];
     for (int s = 1; s < args.splits; ++s)
-      total += __hip_atomic_load(args.partials + s * stride + at,
-                                 __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      total += args.partials[s * stride + at];
     if (args.y_bf16 != nullptr)
       args.y_bf16[at] = Bf16Bits(total);
     else
@@ -261,7 +267,8 @@ void LaunchSkinny(const SkinnyArgs& args, const ProductPlan& plan,
       plan.waves > 1 ? static_cast<std::size_t>(plan.waves) * RG * MT * 4 *
                            kWave * sizeof(float)
                      : 0;
-  SkinnyKernel<MT, RG><<<grid, plan.waves * kWave, shared, stream>>>(args);
+  SkinnyKernel<MT, RG, ThreadsFor(MT, RG)>
+      <<<grid, plan.waves * kWave, shared, stream>>>(args);
 }
 
 using Launcher = void (*)(const SkinnyArgs&, const ProductPlan&, hipStream_t);
@@ -297,6 +304,8 @@ Launcher PickLauncher(int mt, int rg) {
 
 }  // namespace
 
+int MaxWaves(int mt, int rg) { return ThreadsFor(mt, rg) / kWave; }
+
 int MaxRowGroups(int mt) {
   if (mt * 4 <= 8)
     return 4;
@@ -318,21 +327,25 @@ ProductPlan PlanSkinny(std::size_t m, std::size_t k, std::size_t n,
     rg = groups >= 1024 ? 2 : 1;
   }
   rg = std::min(rg, MaxRowGroups(plan.mt));
+  const int tiles = (groups + rg - 1) / rg;
+  const int max_waves = MaxWaves(plan.mt, rg);
   if (waves <= 0) {
+    // About 2048 waves over the chip with at least two pairs each; a tile's
+    // waves split its pairs and meet in LDS.
     waves = 4;
+    while (waves < max_waves && tiles * waves < 2048 && pairs >= 4 * waves)
+      waves *= 2;
     while (waves > 1 && pairs < 2 * waves)
       waves /= 2;
   }
-  waves = std::max(1, std::min(waves, kMaxThreads / kWave));
+  waves = std::max(1, std::min(waves, max_waves));
   plan.rg = rg;
   plan.waves = waves;
-  plan.tiles = (groups + rg - 1) / rg;
+  plan.tiles = tiles;
   if (splits <= 0) {
-    // Fewer tiles than compute units: split k over workgroups, keeping at
-    // least two pairs per wave.
+    // Still fewer tiles than compute units: split k over workgroups too.
     splits = 1;
-    while (plan.tiles * splits < 256 &&
-           pairs >= 4 * waves * splits)
+    while (plan.tiles * splits < 128 && pairs >= 4 * waves * splits)
       splits *= 2;
   }
   splits = std::max(1, std::min(splits, pairs));
