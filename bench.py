@@ -1,0 +1,357 @@
+"""Benchmark of the MI355X DiT hot path: Q8_0 x bf16 products at M = 22
+and the 10-step CFG DiT patch.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
+
+A step is one pass over the product sweep's four weight shapes
+(K, N) in {(1024, 3072), (1024, 8192), (2048, 2048), (2048, 16384)} with
+22 bf16 activation rows: four launches, each on the next of the rotating
+weight copies that keep at least 1 GiB per shape in HBM (beyond the 256 MB
+Infinity Cache), the launches replayed from one HIP graph. `value` is the
+weight bytes (N K 34 / 32 per product, read once) of the K timed steps over
+their wall time. Beside it the line reports every (M, K, N) of the sweep,
+a plain-read probe, the whole 12-block 10-step CFG patch (MALL-warm and
+MALL-cold), and the CPU oracle on the host's cores.
+
+Prints progress to stderr and one JSON line to stdout.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0
+SWEEP_SHAPES = [(1024, 3072), (1024, 8192), (2048, 2048), (2048, 16384)]
+SWEEP_ROWS = [1, 2, 22, 44, 128]
+ROWS = 22
+ROTATION_BYTES = 1.1e9
+METRIC = "Q8_0 GEMM GB/s (% HBM peak) at M=22; us per 10-step CFG DiT patch"
+
+
+def log(message: str) -> None:
+    print(f"[bench] {message}", file=sys.stderr, flush=True)
+
+
+def q8_bytes(k: int, n: int) -> int:
+    return n * k * 34 // 32
+
+
+class Product:
+    """One sweep shape on the GPU: a pool of rotating weight copies."""
+
+    def __init__(self, ops, synth, torch, device, k: int, n: int, seed: int):
+        self.k, self.n = k, n
+        rng = synth.Rng(seed, k * 31 + n)
+        blocks = torch.from_numpy(synth.q8_blocks(rng, n, k)).to(device)
+        packed = ops.q8_pack(blocks, n, k)
+        self.bytes = packed.numel()
+        assert self.bytes == q8_bytes(k, n)
+        self.copies = max(8, int(np.ceil(ROTATION_BYTES / self.bytes)))
+        self.pool = packed.repeat(self.copies).view(self.copies, -1)
+        self.inputs = {}
+        for m in SWEEP_ROWS:
+            x = synth.activations(rng, m, k)
+            self.inputs[m] = (
+                torch.from_numpy(x.view(np.int16)).to(device).view(torch.bfloat16),
+                torch.empty((m, n), dtype=torch.float32, device=device))
+        self.launches = 0
+
+    def launch(self, ops, scratch, m: int) -> None:
+        x, y = self.inputs[m]
+        ops.q8_linear(x, self.pool[self.launches % self.copies], self.n, y=y,
+                      scratch=scratch)
+        self.launches += 1
+
+
+def graph_of(torch, stream, body, count: int):
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=stream):
+        for i in range(count):
+            body(i)
+    return graph
+
+
+def time_graph(torch, stream, graph) -> float:
+    """Seconds of one replay, events on the replay stream."""
+    start = torch.cuda.Event(enable_timing=True)
+    stop = torch.cuda.Event(enable_timing=True)
+    stream.synchronize()
+    start.record(stream)
+    graph.replay()
+    stop.record(stream)
+    stop.synchronize()
+    return start.elapsed_time(stop) / 1e3
+
+
+def read_probe(torch, device, stream) -> float:
+    """GB/s of torch's sum over 2 GiB of int64 (a read-bound pass)."""
+    data = torch.ones(1 << 28, dtype=torch.int64, device=device)
+    for _ in range(2):
+        data.sum()
+    start = torch.cuda.Event(enable_timing=True)
+    stop = torch.cuda.Event(enable_timing=True)
+    start.record(stream)
+    for _ in range(5):
+        data.sum()
+    stop.record(stream)
+    stop.synchronize()
+    seconds = start.elapsed_time(stop) / 1e3 / 5
+    return data.numel() * 8 / seconds / 1e9
+
+
+def gpu_products(args, torch, ops, synth, device, stream):
+    scratch = ops.Scratch(128, 16384)
+    log("building weight pools")
+    products = [Product(ops, synth, torch, device, k, n, seed=0) for k, n in SWEEP_SHAPES]
+
+    def step(_):
+        for p in products:
+            p.launch(ops, scratch, ROWS)
+
+    for _ in range(args.warmup):
+        step(0)
+    stream.synchronize()
+    timed = graph_of(torch, stream, step, args.steps)
+    warm = graph_of(torch, stream, step, max(1, args.warmup))
+    warm.replay()
+    torch.cuda.synchronize()
+    seconds = time_graph(torch, stream, timed)
+    torch.cuda.synchronize()
+    step_bytes = sum(p.bytes for p in products)
+    value = step_bytes * args.steps / seconds / 1e9
+    log(f"M=22 sweep: {value:.0f} GB/s over {args.steps} steps, "
+        f"{seconds / args.steps * 1e6:.2f} us per step")
+
+    sweep = []
+    for p in products:
+        for m in SWEEP_ROWS:
+            count = max(p.copies, 64)
+            g = graph_of(torch, stream, lambda _i, p=p, m=m: p.launch(ops, scratch, m), count)
+            g.replay()
+            s = time_graph(torch, stream, g)
+            us = s / count * 1e6
+            sweep.append({"m": m, "k": p.k, "n": p.n, "us": round(us, 3),
+                          "gbs": round(p.bytes / us / 1e3, 1),
+                          "hbm_frac": round(p.bytes / us / 1e3 / HBM_PEAK_GBS, 4),
+                          "tflops": round(2 * m * p.k * p.n / us / 1e6, 2)})
+            del g
+    for row in sweep:
+        if row["m"] == ROWS:
+            log(f"  M=22 K={row['k']} N={row['n']}: {row['us']} us, {row['gbs']} GB/s")
+    launches = 4 * args.steps
+    result = {
+        "value": value,
+        "seconds": seconds,
+        "step_bytes": step_bytes,
+        "launch_bytes": step_bytes / 4,
+        "launch_us": seconds / launches * 1e6,
+        "sweep": sweep,
+    }
+    del products
+    torch.cuda.empty_cache()
+    return result
+
+
+def gpu_patch(args, torch, ops, synth, device, stream):
+    config = synth.SYNTHETIC_DIT
+    log("building the synthetic DiT (12 blocks, 214 MB of Q8_0)")
+    rope = ops.rope_table(config.rope_theta, config.head_dim, config.rope_factors,
+                          config.rope_scaling, 3 + 2 * config.patch)
+    weights = synth.dit_weights(config, 3, rope)
+    dit = ops.Dit(weights, device, stream)
+    inputs = synth.patch_inputs(config, 4)
+    t, dt, evaluate = ops.euler_schedule(config.steps, config.sway, config.skip)
+    mu = torch.from_numpy(inputs.mu).to(device)
+    cond = torch.from_numpy(inputs.cond_latent).to(device)
+    x = torch.from_numpy(inputs.noise).to(device)
+    for _ in range(max(2, args.warmup)):
+        dit.patch(mu, cond, x, t, dt, evaluate, config.cfg, config.zero_star)
+    torch.cuda.synchronize()
+    patches = max(5, args.steps)
+    start = torch.cuda.Event(enable_timing=True)
+    stop = torch.cuda.Event(enable_timing=True)
+    start.record(stream)
+    for _ in range(patches):
+        dit.patch(mu, cond, x, t, dt, evaluate, config.cfg, config.zero_star)
+    stop.record(stream)
+    stop.synchronize()
+    warm_us = start.elapsed_time(stop) * 1e3 / patches
+    # MALL-cold: a 1 GiB read between patches evicts the weights.
+    flush = torch.ones(1 << 27, dtype=torch.int64, device=device)
+    cold = []
+    for _ in range(5):
+        flush.sum()
+        start.record(stream)
+        dit.patch(mu, cond, x, t, dt, evaluate, config.cfg, config.zero_star)
+        stop.record(stream)
+        stop.synchronize()
+        cold.append(start.elapsed_time(stop) * 1e3)
+    cold_us = float(np.median(cold))
+    # Algorithmic bytes of a patch: 10 evaluations x 12 blocks of weights,
+    # in/out projections per evaluation and cond_proj once; the time MLP is
+    # cached per t and not counted.
+    block = (q8_bytes(config.hidden, config.qkv_width) + q8_bytes(config.q_width, config.hidden)
+             + q8_bytes(config.hidden, 2 * config.ffn) + q8_bytes(config.ffn, config.hidden))
+    io = q8_bytes(config.feat, config.hidden) + q8_bytes(config.hidden, config.feat)
+    evaluations = int(np.sum(evaluate))
+    patch_bytes = evaluations * (config.layers * block + io) + q8_bytes(config.feat, config.hidden)
+    log(f"patch: {warm_us:.1f} us warm, {cold_us:.1f} us cold "
+        f"({patch_bytes / 1e6:.1f} MB of weights per patch)")
+    dit.close()
+    gpu_patch.weights = weights
+    return {"us_warm": round(warm_us, 2), "us_cold": round(cold_us, 2),
+            "patches_timed": patches, "evaluations": evaluations,
+            "bytes": patch_bytes,
+            "gbs_warm": round(patch_bytes / warm_us / 1e3, 1),
+            "gbs_cold": round(patch_bytes / cold_us / 1e3, 1),
+            "roofline_us": round(patch_bytes / HBM_PEAK_GBS / 1e3, 1),
+            "hbm_frac_cold": round(patch_bytes / cold_us / 1e3 / HBM_PEAK_GBS, 4),
+            "workload": "12 blocks hidden 1024, 16 heads x 64, SwiGLU 4096, "
+                        "22 rows (CFG pair x 11), 10 uniform Euler steps, CFG 2.0"}
+
+
+def cpu_baseline(synth):
+    """The oracle's scalar products on the host's cores: a bounded sample
+    (about 10 s) of the same M=22 workload."""
+    sys.path.insert(0, os.path.join(ROOT, "tests"))
+    import oracle_lib
+    threads = max(1, min(16, os.cpu_count() or 1))
+    total_bytes = 0
+    total_seconds = 0.0
+    repeats = {}
+    for k, n in SWEEP_SHAPES:
+        rng = synth.Rng(0, k * 31 + n)
+        blocks = synth.q8_blocks(rng, n, k)
+        x = synth.activations(rng, ROWS, k)
+        count = 0
+        start = time.perf_counter()
+        while True:
+            oracle_lib.q8_linear(x, blocks, n, threads=threads)
+            count += 1
+            elapsed = time.perf_counter() - start
+            if elapsed > 2.5 or count >= 50:
+                break
+        total_seconds += elapsed
+        total_bytes += count * q8_bytes(k, n)
+        repeats[f"{k}x{n}"] = count
+    value = total_bytes / total_seconds / 1e9
+    log(f"CPU oracle: {value:.2f} GB/s on {threads} threads")
+    return {"value": round(value, 3), "unit": "GB/s", "cores": threads,
+            "kind": "port",
+            "sample": "oracle Q8_0 x bf16 products, M=22, the four sweep shapes, "
+                      f"repeats {repeats}, {total_seconds:.1f} s"}
+
+
+def cpu_patch(synth):
+    """One DiT evaluation of the oracle (the synthetic 12-block DiT) on the
+    host's cores, scaled to the 10 evaluations of a patch."""
+    import oracle_lib
+    config = synth.SYNTHETIC_DIT
+    threads = max(1, min(16, os.cpu_count() or 1))
+    weights = getattr(gpu_patch, "weights", None)
+    if weights is None:
+        rope = oracle_lib.rope_table(config.rope_theta, config.head_dim, None, 1.0, 11)
+        weights = synth.dit_weights(config, 3, rope)
+    dit = oracle_lib.OracleDit(weights, threads=threads)
+    inputs = synth.patch_inputs(config, 4)
+    cond = dit.cond_rows(inputs.cond_latent)
+    time_vector = dit.time_vector(1.0)
+    start = time.perf_counter()
+    dit.eval(inputs.mu, cond, inputs.noise, time_vector)
+    seconds = time.perf_counter() - start
+    log(f"CPU oracle: one DiT evaluation {seconds * 1e3:.0f} ms on {threads} threads")
+    return {"us_per_patch": round(seconds * 10 * 1e6, 1), "cores": threads,
+            "sample": "one evaluation x 10"}
+
+
+def main() -> int:
+    parser = argparse.ArgumentParser(description=__doc__.splitlines()[0])
+    parser.add_argument("--gpus", type=int, default=1)
+    parser.add_argument("--steps", type=int, default=50)
+    parser.add_argument("--warmup", type=int, default=5)
+    parser.add_argument("--no-cpu", action="store_true",
+                        help="skip the CPU baseline")
+    parser.add_argument("--no-patch", action="store_true",
+                        help="skip the DiT patch measurement")
+    args = parser.parse_args()
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print("bench.py measures one GPU: the DiT hot path runs one patch per "
+              "GPU and this build has no multi-GPU path; run with --gpus 1.",
+              file=sys.stderr)
+        return 2
+
+    import torch
+    from voxcpm_amd import ops, synth
+
+    if not torch.cuda.is_available():
+        print("bench.py needs a GPU", file=sys.stderr)
+        return 1
+    device = torch.device("cuda:0")
+    stream = torch.cuda.Stream(device=device)
+    torch.cuda.set_stream(stream)
+    log(f"device {torch.cuda.get_device_properties(0).gcnArchName}")
+
+    probe = read_probe(torch, device, stream)
+    log(f"read probe {probe:.0f} GB/s")
+    products = gpu_products(args, torch, ops, synth, device, stream)
+    patch = None if args.no_patch else gpu_patch(args, torch, ops, synth, device, stream)
+    baseline = None
+    if not args.no_cpu:
+        baseline = cpu_baseline(synth)
+        if patch is not None:
+            patch["cpu"] = cpu_patch(synth)
+
+    value = products["value"]
+    line = {
+        "metric": METRIC,
+        "value": round(value, 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(products["seconds"] / args.steps * 1e3, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {
+            "workload": "Q8_0 x bf16 skinny products, M=22, (K,N) in "
+                        "{(1024,3072),(1024,8192),(2048,2048),(2048,16384)}, "
+                        "weights rotated over >= 1 GiB per shape, HIP-graph launches",
+            "m": ROWS,
+            "shapes": SWEEP_SHAPES,
+            "hbm_frac": round(value / HBM_PEAK_GBS, 4),
+        },
+        "roofline": {
+            "bound": "hbm",
+            "achieved": round(products["launch_bytes"] / products["launch_us"] / 1e3, 1),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(products["launch_bytes"] / products["launch_us"] / 1e3
+                          / HBM_PEAK_GBS, 4),
+            "traffic": None,
+            "kernel": "SkinnyKernel (voxcpm_amd/csrc/q8_products.hip)",
+            "launch_bytes": products["launch_bytes"],
+            "launch_us": round(products["launch_us"], 3),
+        },
+        "cpu_baseline": baseline,
+        "read_probe_gbs": round(probe, 1),
+        "sweep": products["sweep"],
+        "patch": patch,
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -1,9 +1,10 @@
-"""Builds the voxcpm_amd HIP library for gfx950 in-tree.
+"""Builds the voxcpm_amd library for gfx950 in-tree.
 
     python -m voxcpm_amd.build        # or voxcpm_amd.build.build()
 
-Compiles every csrc/*.hip with hipcc (objects under _build/) and links
-voxcpm_amd/libvoxcpm_amd.so. Always rebuilds.
+Compiles every csrc/*.hip (the kernels and the C ABI) and host/*.cpp (the
+C++ operator surface over the C ABI) with hipcc, objects under _build/, and
+links voxcpm_amd/libvoxcpm_amd.so. Always rebuilds.
 """
 from __future__ import annotations
 
@@ -16,6 +17,7 @@ import sys
 PACKAGE = pathlib.Path(__file__).resolve().parent
 ROOT = PACKAGE.parent
 CSRC = PACKAGE / "csrc"
+HOST = PACKAGE / "host"
 BUILD = ROOT / "_build" / "voxcpm_amd"
 LIBRARY = PACKAGE / "libvoxcpm_amd.so"
 ARCH = "gfx950"
@@ -36,11 +38,11 @@ FLAGS = [
 
 
 def sources() -> list[pathlib.Path]:
-    return sorted(CSRC.glob("*.hip"))
+    return sorted(CSRC.glob("*.hip")) + sorted(HOST.glob("*.cpp"))
 
 
 def _compile(source: pathlib.Path) -> pathlib.Path:
-    obj = BUILD / (source.stem + ".o")
+    obj = BUILD / (source.parent.name + "_" + source.stem + ".o")
     cmd = [HIPCC, *FLAGS, "-c", str(source), "-o", str(obj)]
     result = subprocess.run(cmd, capture_output=True, text=True)
     if result.returncode != 0:
