@@ -31,6 +31,13 @@ int vx_q8_linear_planned(const uint16_t* x, const void* packed, float* y,
 int vx_q8_plan(size_t m, size_t k, size_t n, vx_scratch* scratch,
                int32_t* out7);
 
+/* float32 [n] -> bf16 bits [n] through the conversion the fused kernels use
+ * for their bf16 activations (gfx950's v_cvt_pk_bf16_f32), so that tests can
+ * check it bit for bit against the reference's rounding
+ * (kernels/device_math.hpp:13-19). n must be even. */
+int vx_test_pack_bf16(const float* input, uint16_t* output, size_t n,
+                      void* stream);
+
 #ifdef __cplusplus
 }
 #endif

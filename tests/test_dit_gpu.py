@@ -203,6 +203,33 @@ def test_guided_euler(vx, oracle, cuda, stream, zero_star):
     assert rel_max(xd.cpu().numpy(), ref) < 1e-5
 
 
+def test_fused_bf16_conversion_matches_reference_rounding(vx, cuda, stream):
+    """The fused kernels' bf16 activations come from gfx950's
+    v_cvt_pk_bf16_f32: bit for bit the reference's rule (round to nearest
+    even, NaN -> high half | 0x40; kernels/device_math.hpp:13-19), over random
+    bit patterns, ties, subnormals, infinities and NaNs."""
+    rng = np.random.default_rng(7)
+    bits = rng.integers(0, 2**32, size=1 << 20, dtype=np.uint64).astype(np.uint32)
+    ties = (rng.integers(0, 2**16, size=4096, dtype=np.uint32) << 16) | 0x8000
+    special = np.array([0x00000000, 0x80000000, 0x7F800000, 0xFF800000, 0x7FC00000,
+                        0xFFC00000, 0x7F800001, 0xFF800001, 0x7FBFFFFF, 0x00000001,
+                        0x807FFFFF, 0x7F7FFFFF, 0x7F7F8000, 0x3F808000, 0x3F818000,
+                        0x0000FFFF, 0x00008000, 0x00018000], dtype=np.uint32)
+    values = np.concatenate([bits, ties, special]).view(np.float32)
+    if values.size % 2:
+        values = np.append(values, np.float32(1.0))
+    x = torch.from_numpy(values.copy()).to(cuda)
+    out = torch.empty(values.size, dtype=torch.int16, device=cuda)
+    L, check = vxlib()
+    check(L.vx_test_pack_bf16(ptr(x), ptr(out), values.size, stream_ptr()))
+    torch.cuda.synchronize()
+    got = out.cpu().numpy().view(np.uint16)
+    want = synth.bf16_bits(values)
+    bad = np.nonzero(got != want)[0]
+    assert bad.size == 0, [(hex(values.view(np.uint32)[i]), hex(got[i]), hex(want[i]))
+                           for i in bad[:8]]
+
+
 # ---- the DiT ---------------------------------------------------------------------
 
 def make_dit(config, seed, vx, oracle, cuda):
@@ -245,6 +272,21 @@ def test_dit_velocity(vx, oracle, cuda, stream, config):
     # Bitwise run-to-run determinism.
     again = dit.velocity(mu, cond, x, 0.63).cpu().numpy()
     assert np.array_equal(got, again)
+
+
+def test_dit_velocity_unfused_rows(vx, oracle, cuda, stream):
+    """A patch of 7 frames gives 34 rows, beyond the fused kernels' 32: the
+    evaluation takes the per-kernel path (row-major products and the
+    separate norm, rotary, attention and SwiGLU kernels)."""
+    config = synth.dataclasses.replace(synth.DitConfig(layers=1), patch=7)
+    weights, dit, odit = make_dit(config, 36, vx, oracle, cuda)
+    inputs = synth.patch_inputs(config, 37)
+    mu, cond, x = (dev(a, cuda) for a in (inputs.mu, inputs.cond_latent, inputs.noise))
+    got = dit.velocity(mu, cond, x, 0.63).cpu().numpy()
+    ref = odit.velocity(inputs.mu, inputs.cond_latent, inputs.noise, 0.63)
+    error, cos = rel_max(got, ref), cosine(got, ref)
+    print(f"velocity (34 rows) rel-max {error:.2e} cosine {cos:.8f}")
+    assert error <= 1e-2 and cos >= 0.9999
 
 
 @pytest.mark.parametrize("config", [synth.SYNTHETIC_DIT, synth.VOXCPM2_DIT],

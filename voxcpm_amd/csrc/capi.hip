@@ -7,6 +7,7 @@
 #include "common.hpp"
 #include "products.hpp"
 #include "q8.hpp"
+#include "q8_tile.hpp"
 
 namespace vx {
 namespace {
@@ -50,6 +51,14 @@ struct vx_scratch {
 };
 
 namespace {
+
+__global__ void PackBf16Kernel(const float* input, std::uint32_t* output,
+                               std::size_t pairs) {
+  const std::size_t i =
+      static_cast<std::size_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i < pairs)
+    output[i] = vx::q8::PackBf16x2(input[2 * i], input[2 * i + 1]);
+}
 
 bool Aligned(const void* pointer, std::size_t bytes) {
   return reinterpret_cast<std::uintptr_t>(pointer) % bytes == 0;
@@ -163,6 +172,20 @@ int vx_q8_linear_planned(const uint16_t* x, const void* packed, float* y,
                     "vx_q8_linear_planned: plans apply to m <= 128");
   return Product(x, packed, y, nullptr, m, k, n, accumulate, scratch,
                  row_groups, waves, splits, stream);
+}
+
+int vx_test_pack_bf16(const float* input, uint16_t* output, size_t n,
+                      void* stream) {
+  if (input == nullptr || output == nullptr || n % 2 != 0 ||
+      !Aligned(output, 4))
+    return vx::Fail(VX_BAD_ARG, "vx_test_pack_bf16: bad arguments");
+  if (n == 0)
+    return vx::Succeed();
+  const std::size_t pairs = n / 2;
+  PackBf16Kernel<<<static_cast<unsigned>((pairs + 255) / 256), 256, 0,
+                   vx::Stream(stream)>>>(
+      input, reinterpret_cast<std::uint32_t*>(output), pairs);
+  return vx::LaunchStatus("vx_test_pack_bf16");
 }
 
 /* The plan vx_q8_linear would use: {mt, rg, waves, tiles, splits,

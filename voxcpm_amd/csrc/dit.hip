@@ -15,9 +15,11 @@
 #include <vector>
 
 #include "common.hpp"
+#include "dit_fused.hpp"
 #include "dit_kernels.hpp"
 #include "products.hpp"
 #include "q8.hpp"
+#include "q8_tile.hpp"
 
 namespace {
 
@@ -105,6 +107,14 @@ struct vx_dit {
   Bf16* time_bf16 = nullptr;
   std::map<std::uint32_t, float*> time_vectors;  // by the bits of t
 
+  // The fused path (up to 32 rows): residual stream and product inputs in
+  // fragment order (q8_tile.hpp).
+  bool fused = false;
+  vx::fused::Shape fused_shape{};
+  float* h_frag = nullptr;
+  Bf16* attention_frag = nullptr;
+  Bf16* swiglu_frag = nullptr;
+
   GraphKey graph_key;
   hipGraphExec_t graph = nullptr;
 
@@ -123,7 +133,9 @@ struct vx_dit {
           static_cast<void*>(x_rows), static_cast<void*>(gathered),
           static_cast<void*>(cond_rows), static_cast<void*>(velocity),
           static_cast<void*>(middle), static_cast<void*>(delta),
-          static_cast<void*>(bf16), static_cast<void*>(time_bf16)})
+          static_cast<void*>(bf16), static_cast<void*>(time_bf16),
+          static_cast<void*>(h_frag), static_cast<void*>(attention_frag),
+          static_cast<void*>(swiglu_frag)})
       if (pointer != nullptr)
         (void)hipFree(pointer);
   }
@@ -202,9 +214,39 @@ struct vx_dit {
   }
 
   /// EvaluateDit (generator.cpp:297-324) with ForwardStack
+  /// (transformer.cpp:55-100) on the fused kernels: 5 launches per layer
+  /// plus the input assembly and the output projection, which also takes
+  /// the guided Euler step when `x_update` is given.
+  int EvalFused(const float* mu, const float* cond, const float* x,
+                const float* time, float* velocity_out, float* x_update,
+                float cfg, float dt, int zero_star, hipStream_t stream) {
+    const vx::fused::Shape& fs = fused_shape;
+    vx::fused::InAssemble(x, weights.in_proj.weight, weights.in_proj.bias, mu,
+                          time, cond, h_frag, fs, stream);
+    for (const vx_dit_layer& layer : layers) {
+      vx::fused::Qkv(h_frag, layer.input_norm, layer.qkv, qkv, fs, stream);
+      vx::fused::Attention(qkv, weights.rope, attention_frag, fs, stream);
+      vx::fused::Residual(attention_frag, layer.o,
+                          static_cast<int>(q_width), fs.hidden, h_frag, fs,
+                          stream);
+      vx::fused::GateUp(h_frag, layer.post_norm, layer.gate_up, swiglu_frag,
+                        fs, stream);
+      vx::fused::Residual(swiglu_frag, layer.down, fs.ffn, fs.hidden, h_frag,
+                          fs, stream);
+    }
+    vx::fused::OutEuler(h_frag, weights.norm, weights.out_proj.weight,
+                        weights.out_proj.bias, velocity_out, x_update, cfg, dt,
+                        zero_star, fs, stream);
+    return vx::LaunchStatus("vx_dit_eval");
+  }
+
+  /// EvaluateDit (generator.cpp:297-324) with ForwardStack
   /// (transformer.cpp:55-100).
   int Eval(const float* mu, const float* cond, const float* x,
            const float* time, float* velocity_out, hipStream_t stream) {
+    if (fused)
+      return EvalFused(mu, cond, x, time, velocity_out, nullptr, 0.0F, 0.0F,
+                       0, stream);
     const std::size_t width = shape.hidden;
     const std::size_t patch = shape.patch;
     const std::size_t feat = shape.feat;
@@ -251,6 +293,11 @@ struct vx_dit {
     for (std::size_t step = 0; step < key.t.size(); ++step) {
       if (!key.evaluate[step])
         continue;  // zero velocity
+      if (fused) {
+        VX_TRY(EvalFused(mu, cond_rows, x, times[step], velocity, x, key.cfg,
+                         key.dt[step], key.zero_star, stream));
+        continue;
+      }
       VX_TRY(Eval(mu, cond_rows, x, times[step], velocity, stream));
       vx::kernels::GuidedEuler(velocity, x, values, key.cfg, key.dt[step],
                                key.zero_star != 0, stream);
@@ -330,6 +377,34 @@ int Create(vx_dit* dit) {
   VX_TRY(Allocate(&dit->delta, s.hidden));
   VX_TRY(Allocate(&dit->bf16, rows * wide));
   VX_TRY(Allocate(&dit->time_bf16, std::max<std::size_t>(s.hidden, s.time_in)));
+
+  vx::fused::Shape& fs = dit->fused_shape;
+  fs.rows = static_cast<int>(rows);
+  fs.length = static_cast<int>(dit->length);
+  fs.patch = static_cast<int>(s.patch);
+  fs.hidden = static_cast<int>(s.hidden);
+  fs.heads = static_cast<int>(s.heads);
+  fs.kv_heads = static_cast<int>(s.kv_heads);
+  fs.head_dim = static_cast<int>(s.head_dim);
+  fs.ffn = static_cast<int>(s.ffn);
+  fs.feat = static_cast<int>(s.feat);
+  fs.eps = s.eps;
+  dit->fused = vx::fused::Supported(fs);
+  if (dit->fused) {
+    const std::size_t h_count = vx::q8::FragElements(s.hidden);
+    const std::size_t a_count = vx::q8::FragElements(dit->q_width);
+    const std::size_t s_count = vx::q8::FragElements(s.ffn);
+    VX_TRY(Allocate(&dit->h_frag, h_count));
+    VX_TRY(Allocate(&dit->attention_frag, a_count));
+    VX_TRY(Allocate(&dit->swiglu_frag, s_count));
+    // Rows past the pair stay zero (never written, never read).
+    VX_HIP(hipMemset(dit->h_frag, 0, h_count * sizeof(float)),
+           "vx_dit_create: hipMemset");
+    VX_HIP(hipMemset(dit->attention_frag, 0, a_count * sizeof(Bf16)),
+           "vx_dit_create: hipMemset");
+    VX_HIP(hipMemset(dit->swiglu_frag, 0, s_count * sizeof(Bf16)),
+           "vx_dit_create: hipMemset");
+  }
 
   // The rows: two sequences of 3 + 2P positions; the outputs are the last
   // P rows of each (generator.cpp:108-124).

@@ -18,7 +18,11 @@ constexpr std::size_t kExactRows = 128;
 
 /// How a skinny product is split: `rg` row groups per workgroup, `waves`
 /// waves per workgroup splitting its pairs, `splits` workgroups along k.
+/// `engine` plans run the one-pass engine (q8_tile.hpp: every wave one pair
+/// at a time, the next in flight); the others the split kernel, which can
+/// also split k over workgroups.
 struct ProductPlan {
+  bool engine = false;
   int mt = 1;
   int rg = 1;
   int waves = 4;

@@ -23,6 +23,7 @@
 #include "common.hpp"
 #include "products.hpp"
 #include "q8.hpp"
+#include "q8_tile.hpp"
 
 namespace vx {
 namespace {
@@ -302,6 +303,70 @@ Launcher PickLauncher(int mt, int rg) {
   }
 }
 
+// ---- the one-pass engine on row-major activations ---------------------------
+
+template<int MT, int RG>
+void LaunchEngine(const q8::TileArgs& args, int tiles, int waves,
+                  hipStream_t stream) {
+  const std::size_t shared =
+      q8::EngineShared(MT, RG, waves, q8::ASource::kRowMajor);
+  q8::EngineKernel<MT, RG, q8::ASource::kRowMajor, q8::Output::kStore>
+      <<<tiles, waves * kWave, shared, stream>>>(args);
+}
+
+using EngineLauncher = void (*)(const q8::TileArgs&, int, int, hipStream_t);
+
+template<int MT>
+EngineLauncher EngineRg(int rg) {
+  if constexpr (MT * 4 <= 8) {
+    if (rg == 4)
+      return LaunchEngine<MT, 4>;
+  }
+  if constexpr (MT * 2 <= 8) {
+    if (rg == 2)
+      return LaunchEngine<MT, 2>;
+  }
+  if (rg == 1)
+    return LaunchEngine<MT, 1>;
+  return nullptr;
+}
+
+EngineLauncher PickEngine(int mt, int rg) {
+  switch (mt) {
+    case 1: return EngineRg<1>(rg);
+    case 2: return EngineRg<2>(rg);
+    case 3: return EngineRg<3>(rg);
+    case 4: return EngineRg<4>(rg);
+    case 5: return EngineRg<5>(rg);
+    case 6: return EngineRg<6>(rg);
+    case 7: return EngineRg<7>(rg);
+    case 8: return EngineRg<8>(rg);
+    default: return nullptr;
+  }
+}
+
+/// Engine plan: up to 256 row groups take one per workgroup; wider products
+/// share each activation fragment over 2 or 4 row groups (fewer workgroups
+/// read the activations). Waves split the pairs, up to 16 (8 for the larger
+/// register footprints).
+ProductPlan PlanEngine(std::size_t m, std::size_t k, std::size_t n) {
+  ProductPlan plan;
+  plan.engine = true;
+  plan.mt = static_cast<int>((m + 15) / 16);
+  const int groups = static_cast<int>(q8::Groups(n));
+  const int pairs = static_cast<int>(q8::Pairs(k));
+  int rg = groups <= 256 ? 1 : groups <= 512 ? 2 : 4;
+  while (rg > 1 && rg * plan.mt > 8)
+    rg /= 2;
+  plan.rg = rg;
+  plan.tiles = (groups + rg - 1) / rg;
+  plan.waves = q8::EngineThreads(plan.mt, rg) / kWave;  // idle waves add zeros
+  plan.splits = 1;
+  plan.pairs_per_split = pairs;
+  plan.pairs_per_wave = (pairs + plan.waves - 1) / plan.waves;
+  return plan;
+}
+
 }  // namespace
 
 int MaxWaves(int mt, int rg) { return ThreadsFor(mt, rg) / kWave; }
@@ -318,6 +383,8 @@ ProductPlan PlanSkinny(std::size_t m, std::size_t k, std::size_t n,
                        std::size_t scratch_floats,
                        std::size_t scratch_counters, int rg, int waves,
                        int splits) {
+  if (rg <= 0 && waves <= 0 && splits <= 0)
+    return PlanEngine(m, k, n);
   ProductPlan plan;
   plan.mt = static_cast<int>((m + 15) / 16);
   const int groups = static_cast<int>(q8::Groups(n));
@@ -365,6 +432,25 @@ int RunSkinny(const Bf16* x, const void* w, float* y, Bf16* y_bf16,
               std::size_t m, std::size_t k, std::size_t n, bool accumulate,
               const ProductPlan& plan, float* partials, unsigned* counters,
               hipStream_t stream) {
+  if (plan.engine) {
+    const EngineLauncher launch = PickEngine(plan.mt, plan.rg);
+    if (launch == nullptr)
+      return Fail(VX_UNSUPPORTED, "no product engine for this plan");
+    q8::TileArgs args{};
+    args.w = static_cast<const std::uint8_t*>(w);
+    args.m = static_cast<int>(m);
+    args.k = static_cast<int>(k);
+    args.n = static_cast<int>(n);
+    args.pairs = static_cast<int>(q8::Pairs(k));
+    args.groups = static_cast<int>(q8::Groups(n));
+    args.group_stride = 1;
+    args.x = x;
+    args.y = y_bf16 != nullptr ? nullptr : y;
+    args.y_bf16 = y_bf16;
+    args.accumulate = accumulate ? 1 : 0;
+    launch(args, plan.tiles, plan.waves, stream);
+    return LaunchStatus("q8 product");
+  }
   const Launcher launch = PickLauncher(plan.mt, plan.rg);
   if (launch == nullptr)
     return Fail(VX_UNSUPPORTED, "no product kernel for this plan");

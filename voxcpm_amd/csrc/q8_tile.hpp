@@ -1,0 +1,434 @@
+// The skinny Q8_0 product engine (m <= 128 activation rows), shared by the
+// standalone products and the DiT's fused layer kernels.
+//
+// A workgroup owns RG row groups (16 weight rows each) of the output and the
+// whole reduction length; its waves split the column pairs (two Q8_0
+// blocks, one panel unit per row group), PW pairs per wave per pass, the
+// next pass's weights and activations in flight while the current pass is
+// multiplied. Each 32-column block is one v_mfma_f32_16x16x32_bf16 from
+// zero (the float32 block sum) followed by acc = fmaf(f16 scale, sum, acc),
+// the arithmetic of kernels/wmma_products.hip:192-215. The waves' partial
+// sums meet in LDS and are added in wave order, so every run gives the same
+// bits.
+//
+// Activations come from one of three sources:
+//  - kRowMajor: bf16 [m][k] row-major (the drop-in product's x);
+//  - kFragBf16: bf16 in fragment order (below), written by the DiT kernels
+//    so that each wave's operand load is 1 KB of contiguous bytes;
+//  - kNormF32: the float32 residual stream in fragment order, RMS-normalised
+//    on the fly (kernels/generator_kernels.hip:91-108): each wave loads its
+//    pairs' values, the per-row sums of squares meet in LDS, and the operand
+//    is bf16((x * rsqrt(mean + eps)) * gamma), exactly the reference's
+//    normalised bf16 activations.
+//
+// and leave through one of three epilogues:
+//  - kStore: float32 [m][n] row-major (optionally accumulated) or bf16;
+//  - kResidual: added into the float32 fragment-order residual stream;
+//  - kSwiGlu: RG = 2 with the up rows `group_stride` row groups after the
+//    gate rows; bf16(silu(gate) * up) in bf16 fragment order
+//    (kernels/generator_kernels.hip:243-254).
+#ifndef VOXCPM_AMD_Q8_TILE_HPP_
+#define VOXCPM_AMD_Q8_TILE_HPP_
+
+#include <hip/hip_runtime.h>
+
+#include <cstddef>
+#include <cstdint>
+
+#include "common.hpp"
+#include "q8.hpp"
+
+namespace vx::q8 {
+
+// ---- fragment-order activation layouts (up to 32 rows) ----------------------
+//
+// The A operand of v_mfma_f32_16x16x32_bf16 for rows 16 t .. 16 t + 15 and
+// columns 64 p + 32 h .. + 31 is lane L = 16 octet + r16 holding row
+// 16 t + r16, columns 64 p + 32 h + 8 octet + 0..7. Fragment order stores
+// those eight values of each lane contiguously, lanes in order, then
+// (p, t, h) with h fastest:
+//   bf16: 16 bytes per lane, 1 KB per (p, t, h);
+//   f32:  32 bytes per lane as two 16-byte quarters (values 0..3, 4..7),
+//         quarter-major, so one 16-byte load per lane still reads 1 KB of
+//         contiguous bytes.
+// Rows run to 32 (two 16-row tiles); columns to a multiple of 64.
+
+constexpr int kFragRows = 32;
+
+__host__ __device__ inline std::size_t BfFragIndex(int row, int column) {
+  const int pair = column >> 6;
+  const int half = (column >> 5) & 1;
+  const int octet = (column >> 3) & 3;
+  const int t = row >> 4;
+  const int lane = 16 * octet + (row & 15);
+  return ((((static_cast<std::size_t>(pair) * 2 + t) * 2 + half) * 64 + lane) * 8) +
+         (column & 7);
+}
+
+__host__ __device__ inline std::size_t F32FragIndex(int row, int column) {
+  const int pair = column >> 6;
+  const int half = (column >> 5) & 1;
+  const int octet = (column >> 3) & 3;
+  const int quarter = (column >> 2) & 1;
+  const int t = row >> 4;
+  const int lane = 16 * octet + (row & 15);
+  return ((((static_cast<std::size_t>(pair) * 2 + t) * 2 + half) * 2 + quarter) * 64 +
+          lane) * 4 +
+         (column & 3);
+}
+
+/// Elements of a fragment-order matrix of `columns` columns (32 rows).
+inline std::size_t FragElements(std::size_t columns) {
+  return static_cast<std::size_t>(kFragRows) * ((columns + 63) / 64) * 64;
+}
+
+enum class ASource : int { kRowMajor = 0, kFragBf16 = 1, kNormF32 = 2 };
+enum class Output : int { kStore = 0, kResidual = 1, kSwiGlu = 2 };
+
+struct TileArgs {
+  const std::uint8_t* w;  // panels [groups][pairs] units
+  int m;                  // activation rows
+  int k;                  // reduction length (columns of x)
+  int n;                  // output columns (weight rows)
+  int pairs;              // Pairs(k)
+  int groups;             // Groups(n)
+  int group_stride;       // row group r of tile b: RgGroup(b, r, stride)
+  // activations
+  const Bf16* x;          // kRowMajor [m][k] / kFragBf16
+  const float* h;         // kNormF32: float32 fragment order [32][k]
+  const Bf16* gamma;      // kNormF32: [k]
+  float eps;              // kNormF32
+  // outputs
+  float* y;               // kStore float32 [m][n]
+  Bf16* y_bf16;           // kStore bf16 [m][n] (used when y is null)
+  int accumulate;         // kStore float32: y += product
+  float* residual;        // kResidual: float32 fragment order [32][n]
+  Bf16* frag_out;         // kSwiGlu: bf16 fragment order [32][n / 2]
+};
+
+/// Row group r of workgroup tile b: consecutive groups (stride 1) or a
+/// group and its partner `stride` groups later (SwiGLU's gate and up).
+__host__ __device__ inline int RgGroup(int tile, int r, int stride, int rg) {
+  return (tile / stride) * stride * rg + tile % stride + r * stride;
+}
+
+/// Maximum threads of a workgroup of the engine for (MT, RG): the larger
+/// register footprints take 8 waves.
+constexpr int EngineThreads(int mt, int rg) {
+  return (mt <= 2 && rg <= 2) ? 1024 : 512;
+}
+
+/// LDS bytes the engine needs for `waves` waves.
+inline std::size_t EngineShared(int mt, int rg, int waves, ASource source) {
+  std::size_t floats = static_cast<std::size_t>(waves) * rg * mt * 256;
+  if (source == ASource::kNormF32)
+    floats += static_cast<std::size_t>(waves) * kFragRows;
+  return floats * sizeof(float);
+}
+
+__device__ inline float Silu(float value) {
+  return value / (1.0F + expf(-value));
+}
+
+/// Two float32 -> two bf16 (nearest even) packed low / high, one
+/// v_cvt_pk_bf16_f32 on gfx950; the same bits as Bf16Bits, including the
+/// quiet-NaN rule (checked against it on the GPU).
+__device__ inline std::uint32_t PackBf16x2(float lo, float hi) {
+  typedef float F32x2 __attribute__((ext_vector_type(2)));
+  typedef __bf16 Bf16x2 __attribute__((ext_vector_type(2)));
+  return __builtin_bit_cast(std::uint32_t,
+                            __builtin_convertvector(F32x2{lo, hi}, Bf16x2));
+}
+
+/// Eight float32 -> eight bf16 (nearest even), packed for an MFMA operand.
+__device__ inline uint4 PackBf16x8(const float (&v)[8]) {
+  return uint4{PackBf16x2(v[0], v[1]), PackBf16x2(v[2], v[3]),
+               PackBf16x2(v[4], v[5]), PackBf16x2(v[6], v[7])};
+}
+
+/// One float32 -> bf16 bits through the same instruction.
+__device__ inline Bf16 Bf16Fast(float value) {
+  return static_cast<Bf16>(PackBf16x2(value, 0.0F) & 0xFFFFU);
+}
+
+__device__ inline float Bf16Lo(std::uint32_t word) {
+  return __uint_as_float(word << 16);
+}
+__device__ inline float Bf16Hi(std::uint32_t word) {
+  return __uint_as_float(word & 0xFFFF0000U);
+}
+
+/// One pair's operands in flight: RG weight fragments with their scale
+/// pairs, and the MT x 2 activation fragments.
+template<int MT, int RG>
+struct PairStage {
+  uint4 w[RG];
+  std::uint32_t scales[RG];
+  uint4 a[MT][2];
+};
+
+/// The engine. Grid: one workgroup per tile (RG row groups); blockDim.x =
+/// EngineThreads(MT, RG) (waves without pairs add zeros). PW pairs per wave
+/// per pass; kNormF32 needs every pair in one pass (pairs <= waves * PW).
+template<int MT, int RG, ASource SRC, Output OUT, int PW = 1>
+__global__ __launch_bounds__(EngineThreads(MT, RG)) void EngineKernel(TileArgs a) {
+  static_assert(SRC != ASource::kNormF32 || MT == 2, "norm source is 32 rows");
+  static_assert(OUT == Output::kStore || MT == 2, "fragment outputs are 32 rows");
+  static_assert(OUT != Output::kSwiGlu || RG == 2, "SwiGLU pairs two groups");
+  extern __shared__ float lds[];
+  const int lane = threadIdx.x % kWave;
+  const int wave = threadIdx.x / kWave;
+  constexpr int waves = EngineThreads(MT, RG) / kWave;
+  const int r16 = lane % 16;
+  const int octet = lane / 16;
+  const int tile = static_cast<int>(blockIdx.x);
+  const int k_blocks = a.k / 32;
+
+  const std::uint8_t* unit[RG];
+#pragma unroll
+  for (int r = 0; r < RG; ++r) {
+    const int g = min(RgGroup(tile, r, a.group_stride, RG), a.groups - 1);
+    unit[r] = a.w + static_cast<std::size_t>(g) * a.pairs * kUnitBytes;
+  }
+  bool row_ok[MT];
+#pragma unroll
+  for (int t = 0; t < MT; ++t)
+    row_ok[t] = 16 * t + r16 < a.m;
+
+  const auto load_weights = [&](int pair, PairStage<MT, RG>& s) {
+    const bool ok = pair < a.pairs;
+#pragma unroll
+    for (int r = 0; r < RG; ++r) {
+      const std::uint8_t* u = unit[r] + static_cast<std::size_t>(ok ? pair : 0) * kUnitBytes;
+      s.w[r] = ok ? *reinterpret_cast<const uint4*>(u + 16 * lane) : uint4{0U, 0U, 0U, 0U};
+      s.scales[r] = ok ? *reinterpret_cast<const std::uint32_t*>(u + kValueBytes + 4 * r16) : 0U;
+    }
+  };
+  const auto load_activations = [&](int pair, PairStage<MT, RG>& s) {
+    const bool ok = pair < a.pairs;
+#pragma unroll
+    for (int t = 0; t < MT; ++t)
+#pragma unroll
+      for (int hf = 0; hf < 2; ++hf) {
+        uint4 v{0U, 0U, 0U, 0U};
+        if constexpr (SRC == ASource::kRowMajor) {
+          if (ok && row_ok[t] && 2 * pair + hf < k_blocks)
+            v = *reinterpret_cast<const uint4*>(
+                a.x + static_cast<std::size_t>(16 * t + r16) * a.k + 64 * pair + 32 * hf +
+                8 * octet);
+        } else if constexpr (SRC == ASource::kFragBf16) {
+          if (ok && row_ok[t])
+            v = reinterpret_cast<const uint4*>(a.x)[((pair * 2 + t) * 2 + hf) * 64 + lane];
+        }
+        s.a[t][hf] = v;
+      }
+  };
+
+  F32x4 acc[RG][MT];
+#pragma unroll
+  for (int r = 0; r < RG; ++r)
+#pragma unroll
+    for (int t = 0; t < MT; ++t)
+      acc[r][t] = F32x4{0.0F, 0.0F, 0.0F, 0.0F};
+
+  const auto multiply = [&](const PairStage<MT, RG>& s) {
+    const F32x4 zero{0.0F, 0.0F, 0.0F, 0.0F};
+#pragma unroll
+    for (int r = 0; r < RG; ++r) {
+      const Bf16x8 b0 = Int8x8ToBf16(s.w[r].x, s.w[r].y);
+      const Bf16x8 b1 = Int8x8ToBf16(s.w[r].z, s.w[r].w);
+      const float s0 = HalfValue(static_cast<std::uint16_t>(s.scales[r] & 0xFFFFU));
+      const float s1 = HalfValue(static_cast<std::uint16_t>(s.scales[r] >> 16));
+#pragma unroll
+      for (int t = 0; t < MT; ++t) {
+        const F32x4 sum0 = Mfma16x16x32(AsBf16x8(s.a[t][0]), b0, zero);
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          acc[r][t][i] = fmaf(s0, sum0[i], acc[r][t][i]);
+        const F32x4 sum1 = Mfma16x16x32(AsBf16x8(s.a[t][1]), b1, zero);
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          acc[r][t][i] = fmaf(s1, sum1[i], acc[r][t][i]);
+      }
+    }
+  };
+
+  float* reduce = lds;
+  if constexpr (SRC == ASource::kNormF32) {
+    // Every pair in this pass: wave w owns pairs w, w + waves, ...
+    float* squares = lds + static_cast<std::size_t>(waves) * RG * MT * 256;
+    PairStage<MT, RG> stage[PW];
+    float4 hv[PW][2][2][2];  // [pair][t][half][quarter]
+    uint4 gamma_bits[PW][2];  // [pair][half]: 8 bf16 norm weights
+#pragma unroll
+    for (int p = 0; p < PW; ++p)
+      load_weights(wave + p * waves, stage[p]);
+#pragma unroll
+    for (int p = 0; p < PW; ++p) {
+      const int pair = wave + p * waves;
+#pragma unroll
+      for (int hf = 0; hf < 2; ++hf)
+        gamma_bits[p][hf] =
+            pair < a.pairs
+                ? *reinterpret_cast<const uint4*>(a.gamma + 64 * pair + 32 * hf + 8 * octet)
+                : uint4{0U, 0U, 0U, 0U};
+    }
+    float partial[2] = {0.0F, 0.0F};
+#pragma unroll
+    for (int p = 0; p < PW; ++p) {
+      const int pair = wave + p * waves;
+      const bool ok = pair < a.pairs;
+#pragma unroll
+      for (int t = 0; t < 2; ++t)
+#pragma unroll
+        for (int hf = 0; hf < 2; ++hf)
+#pragma unroll
+          for (int q = 0; q < 2; ++q) {
+            float4 v{0.0F, 0.0F, 0.0F, 0.0F};
+            if (ok && row_ok[t])
+              v = reinterpret_cast<const float4*>(
+                  a.h)[(((pair * 2 + t) * 2 + hf) * 2 + q) * 64 + lane];
+            hv[p][t][hf][q] = v;
+          }
+#pragma unroll
+      for (int t = 0; t < 2; ++t)
+#pragma unroll
+        for (int hf = 0; hf < 2; ++hf)
+#pragma unroll
+          for (int q = 0; q < 2; ++q) {
+            const float4 v = hv[p][t][hf][q];
+            partial[t] += v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
+          }
+    }
+    // The four octets of a row meet across lanes; waves meet in LDS.
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+      partial[t] += __shfl_xor(partial[t], 16, kWave);
+      partial[t] += __shfl_xor(partial[t], 32, kWave);
+    }
+    if (octet == 0) {
+      squares[wave * kFragRows + r16] = partial[0];
+      squares[wave * kFragRows + 16 + r16] = partial[1];
+    }
+    __syncthreads();
+    float inverse[2];
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+      float total = 0.0F;
+      for (int w = 0; w < waves; ++w)
+        total += squares[w * kFragRows + 16 * t + r16];
+      inverse[t] = rsqrtf(total / static_cast<float>(a.k) + a.eps);
+    }
+#pragma unroll
+    for (int p = 0; p < PW; ++p) {
+      const int pair = wave + p * waves;
+      const bool ok = pair < a.pairs;
+#pragma unroll
+      for (int hf = 0; hf < 2; ++hf) {
+        const uint4 g = gamma_bits[p][hf];
+        const float gamma[8] = {Bf16Lo(g.x), Bf16Hi(g.x), Bf16Lo(g.y), Bf16Hi(g.y),
+                                Bf16Lo(g.z), Bf16Hi(g.z), Bf16Lo(g.w), Bf16Hi(g.w)};
+#pragma unroll
+        for (int t = 0; t < 2; ++t) {
+          const float4 lo = hv[p][t][hf][0];
+          const float4 hi = hv[p][t][hf][1];
+          const float x[8] = {lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
+          float v[8];
+#pragma unroll
+          for (int i = 0; i < 8; ++i)
+            v[i] = x[i] * inverse[t] * gamma[i];
+          stage[p].a[t][hf] = (ok && row_ok[t]) ? PackBf16x8(v) : uint4{0U, 0U, 0U, 0U};
+        }
+      }
+    }
+#pragma unroll
+    for (int p = 0; p < PW; ++p)
+      if (wave + p * waves < a.pairs)
+        multiply(stage[p]);
+  } else {
+    // Passes of PW pairs per wave (slot p of the pass at base: pair
+    // base + p waves + wave); the next pass is loaded before this one is
+    // multiplied, so 2 PW pairs per wave are in flight.
+    PairStage<MT, RG> current[PW], next[PW];
+    const int step = waves * PW;
+#pragma unroll
+    for (int p = 0; p < PW; ++p) {
+      load_activations(p * waves + wave, current[p]);
+      load_weights(p * waves + wave, current[p]);
+    }
+    for (int base = 0; base < a.pairs; base += step) {
+      const bool more = base + step < a.pairs;
+      if (more) {
+#pragma unroll
+        for (int p = 0; p < PW; ++p) {
+          load_activations(base + step + p * waves + wave, next[p]);
+          load_weights(base + step + p * waves + wave, next[p]);
+        }
+      }
+#pragma unroll
+      for (int p = 0; p < PW; ++p)
+        if (base + p * waves + wave < a.pairs)
+          multiply(current[p]);
+      if (!more)
+        break;
+#pragma unroll
+      for (int p = 0; p < PW; ++p)
+        current[p] = next[p];
+    }
+  }
+
+  // Partial sums of the waves meet in LDS: [wave][fragment r MT + t][i][lane].
+  constexpr int kFragmentFloats = RG * MT * 256;
+#pragma unroll
+  for (int r = 0; r < RG; ++r)
+#pragma unroll
+    for (int t = 0; t < MT; ++t)
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        reduce[wave * kFragmentFloats + ((r * MT + t) * 4 + i) * 64 + lane] = acc[r][t][i];
+  __syncthreads();
+
+  // All waves' partials are read at once, then added in wave order.
+  constexpr int kWaves = waves;
+  const auto total_of = [&](int e) {
+    float parts[kWaves];
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w)
+      parts[w] = reduce[w * kFragmentFloats + e];
+    float total = parts[0];
+#pragma unroll
+    for (int w = 1; w < kWaves; ++w)
+      total += parts[w];
+    return total;
+  };
+  const int outputs = OUT == Output::kSwiGlu ? MT * 256 : kFragmentFloats;
+  for (int e = threadIdx.x; e < outputs; e += blockDim.x) {
+    const int f = e / 256;
+    const int i = (e / 64) % 4;
+    const int l = e % 64;
+    const int r = f / MT;
+    const int t = f % MT;
+    const int row = 16 * t + 4 * (l / 16) + i;
+    const int group = RgGroup(tile, r, a.group_stride, RG);
+    const int column = 16 * group + l % 16;
+    if (row >= a.m || group >= a.groups || column >= a.n)
+      continue;
+    const float v = total_of(e);
+    if constexpr (OUT == Output::kStore) {
+      const std::size_t at = static_cast<std::size_t>(row) * a.n + column;
+      if (a.y != nullptr)
+        a.y[at] = a.accumulate ? a.y[at] + v : v;
+      else
+        a.y_bf16[at] = Bf16Fast(v);
+    } else if constexpr (OUT == Output::kResidual) {
+      a.residual[F32FragIndex(row, column)] += v;
+    } else {
+      const float up = total_of(e + MT * 256);
+      a.frag_out[BfFragIndex(row, column)] = Bf16Fast(Silu(v) * up);
+    }
+  }
+}
+
+}  // namespace vx::q8
+
+#endif  // VOXCPM_AMD_Q8_TILE_HPP_
