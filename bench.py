@@ -33,6 +33,17 @@ SWEEP_SHAPES = [(1024, 3072), (1024, 8192), (2048, 2048), (2048, 16384)]
 SWEEP_ROWS = [1, 2, 22, 44, 128]
 ROWS = 22
 ROTATION_BYTES = 1.1e9
+BF16_PEAK_TFLOPS = 2500.0
+# HBM bytes per launch of the M=22 sweep kernels from two rocprofv3 PMC runs
+# (profiles/q8_skinny_m22_traffic.md): FETCH_SIZE KiB (scaled by 2.0, its
+# reading of a 256 MiB copy of known size) + WRITE_SIZE KiB (scale 1.0).
+# Measured, not computed: re-measure when the product kernel changes.
+FETCH_SCALE = 262144 / 131083.5
+TRAFFIC_KIB = {(1024, 3072): (1835.5, 264.0), (1024, 8192): (4562.0, 704.0),
+               (2048, 2048): (2555.5, 176.0), (2048, 16384): (17799.0, 1408.0)}
+PREFILL_M = [129, 256, 512, 1024]
+PREFILL_N = [2048, 6144, 16384]
+PREFILL_K = 2048
 METRIC = "Q8_0 GEMM GB/s (% HBM peak) at M=22; us per 10-step CFG DiT patch"
 
 
@@ -160,6 +171,59 @@ def gpu_products(args, torch, ops, synth, device, stream):
     return result
 
 
+def gpu_prefill(args, torch, ops, synth, device, stream):
+    """Prefill-sized Q8_0 products (m > 128, matrix-core bound): TFLOP/s of
+    2 m n k per launch, launches replayed from a HIP graph over a few
+    rotating weight copies."""
+    rows = []
+    k = PREFILL_K
+    for n in PREFILL_N:
+        rng = synth.Rng(7, n)
+        blocks = torch.from_numpy(synth.q8_blocks(rng, n, k)).to(device)
+        packed = ops.q8_pack(blocks, n, k)
+        copies = 4
+        pool = packed.repeat(copies).view(copies, -1)
+        del blocks
+        for m in PREFILL_M:
+            x = torch.from_numpy(synth.activations(rng, m, k).view(np.int16)).to(
+                device).view(torch.bfloat16)
+            y = torch.empty((m, n), dtype=torch.float32, device=device)
+            ops.q8_linear(x, pool[0], n, y=y)
+            count = 20
+            g = graph_of(torch, stream, lambda i: ops.q8_linear(x, pool[i % copies], n, y=y),
+                         count)
+            g.replay()
+            seconds = time_graph(torch, stream, g) / count
+            tflops = 2.0 * m * n * k / seconds / 1e12
+            rows.append({"m": m, "k": k, "n": n, "us": round(seconds * 1e6, 2),
+                         "tflops": round(tflops, 1),
+                         "mfma_frac": round(tflops / BF16_PEAK_TFLOPS, 4)})
+            log(f"  prefill M={m} K={k} N={n}: {seconds * 1e6:.1f} us, {tflops:.1f} TFLOP/s")
+            del g
+        del pool, packed
+    torch.cuda.empty_cache()
+    return rows
+
+
+def pmc_workload(torch, ops, synth, device, stream) -> None:
+    """Eager launches for counter runs: a plain 256 MiB device copy (the
+    calibration of FETCH_SIZE / WRITE_SIZE against known bytes), then 20
+    launches of each M=22 sweep shape on rotating copies."""
+    src = torch.ones(1 << 25, dtype=torch.int64, device=device)
+    dst = torch.empty_like(src)
+    for _ in range(5):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    del src, dst
+    scratch = ops.Scratch(128, 16384)
+    products = [Product(ops, synth, torch, device, k, n, seed=0) for k, n in SWEEP_SHAPES]
+    for p in products:
+        for _ in range(20):
+            p.launch(ops, scratch, ROWS)
+    torch.cuda.synchronize()
+    log("pmc workload done: 5 copies of 256 MiB, 20 launches per sweep shape")
+
+
 def gpu_patch(args, torch, ops, synth, device, stream):
     config = synth.SYNTHETIC_DIT
     log("building the synthetic DiT (12 blocks, 214 MB of Q8_0)")
@@ -281,6 +345,10 @@ def main() -> int:
                         help="skip the CPU baseline")
     parser.add_argument("--no-patch", action="store_true",
                         help="skip the DiT patch measurement")
+    parser.add_argument("--no-prefill", action="store_true",
+                        help="skip the prefill-sized products")
+    parser.add_argument("--pmc-workload", action="store_true",
+                        help="only run the eager launches that counter runs read")
     args = parser.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
@@ -299,10 +367,14 @@ def main() -> int:
     stream = torch.cuda.Stream(device=device)
     torch.cuda.set_stream(stream)
     log(f"device {torch.cuda.get_device_properties(0).gcnArchName}")
+    if args.pmc_workload:
+        pmc_workload(torch, ops, synth, device, stream)
+        return 0
 
     probe = read_probe(torch, device, stream)
     log(f"read probe {probe:.0f} GB/s")
     products = gpu_products(args, torch, ops, synth, device, stream)
+    prefill = None if args.no_prefill else gpu_prefill(args, torch, ops, synth, device, stream)
     patch = None if args.no_patch else gpu_patch(args, torch, ops, synth, device, stream)
     baseline = None
     if not args.no_cpu:
@@ -339,14 +411,16 @@ def main() -> int:
             "unit": "GB/s",
             "frac": round(products["launch_bytes"] / products["launch_us"] / 1e3
                           / HBM_PEAK_GBS, 4),
-            "traffic": None,
-            "kernel": "SkinnyKernel (voxcpm_amd/csrc/q8_products.hip)",
+            "traffic": round(sum(f * FETCH_SCALE + w for f, w in TRAFFIC_KIB.values())
+                             * 1024 / len(TRAFFIC_KIB)),
+            "kernel": "EngineKernel (voxcpm_amd/csrc/q8_tile.hpp) via vx_q8_linear",
             "launch_bytes": products["launch_bytes"],
             "launch_us": round(products["launch_us"], 3),
         },
         "cpu_baseline": baseline,
         "read_probe_gbs": round(probe, 1),
         "sweep": products["sweep"],
+        "prefill": prefill,
         "patch": patch,
     }
     print(json.dumps(line), flush=True)
