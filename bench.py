@@ -259,6 +259,21 @@ def gpu_patch(args, torch, ops, synth, device, stream):
         stop.synchronize()
         cold.append(start.elapsed_time(stop) * 1e3)
     cold_us = float(np.median(cold))
+    # The persistent evaluation (one launch per Euler step, grid barriers
+    # between the layer's phases), selected explicitly.
+    from voxcpm_amd import _lib
+    dit.set_path(_lib.DIT_PATH_PERSISTENT)
+    for _ in range(2):
+        dit.patch(mu, cond, x, t, dt, evaluate, config.cfg, config.zero_star)
+    torch.cuda.synchronize()
+    start.record(stream)
+    for _ in range(patches):
+        dit.patch(mu, cond, x, t, dt, evaluate, config.cfg, config.zero_star)
+    stop.record(stream)
+    stop.synchronize()
+    dit.status()
+    persistent_us = start.elapsed_time(stop) * 1e3 / patches
+    dit.set_path(_lib.DIT_PATH_AUTO)
     # Algorithmic bytes of a patch: 10 evaluations x 12 blocks of weights,
     # in/out projections per evaluation and cond_proj once; the time MLP is
     # cached per t and not counted.
@@ -268,10 +283,12 @@ def gpu_patch(args, torch, ops, synth, device, stream):
     evaluations = int(np.sum(evaluate))
     patch_bytes = evaluations * (config.layers * block + io) + q8_bytes(config.feat, config.hidden)
     log(f"patch: {warm_us:.1f} us warm, {cold_us:.1f} us cold "
-        f"({patch_bytes / 1e6:.1f} MB of weights per patch)")
+        f"({patch_bytes / 1e6:.1f} MB of weights per patch); "
+        f"persistent evaluation {persistent_us:.1f} us")
     dit.close()
     gpu_patch.weights = weights
     return {"us_warm": round(warm_us, 2), "us_cold": round(cold_us, 2),
+            "us_warm_persistent": round(persistent_us, 2),
             "patches_timed": patches, "evaluations": evaluations,
             "bytes": patch_bytes,
             "gbs_warm": round(patch_bytes / warm_us / 1e3, 1),

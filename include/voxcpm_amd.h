@@ -234,6 +234,14 @@ int vx_dit_patch(vx_dit* dit, const float* mu, const float* cond_latent,
                  const int32_t* evaluate, size_t steps, float cfg,
                  int zero_star, void* stream);
 
+/* Synchronizes with the device and reports whether every evaluation so far
+ * completed: VX_HIP_ERROR when a persistent evaluation gave up waiting at
+ * a grid barrier (its results are invalid; the handle is reset for later
+ * calls). No reference counterpart: the reference's launches cannot wait
+ * on each other, and its GpuError (device.hpp:16-30) covers launch errors,
+ * which every entry point here still returns. */
+int vx_dit_status(vx_dit* dit);
+
 /* EulerSchedule (generator.cpp:63-80, generator.hpp:34-44) on the host:
  * writes `timesteps` entries. skip = 1 marks CFG-Zero*'s zero-velocity
  * first steps as not evaluated; sway = 0 gives the uniform schedule. */

@@ -38,6 +38,34 @@ int vx_q8_plan(size_t m, size_t k, size_t n, vx_scratch* scratch,
 int vx_test_pack_bf16(const float* input, uint16_t* output, size_t n,
                       void* stream);
 
+/* The DiT evaluation paths. AUTO (the default) takes FUSED where the shape
+ * allows (five launches per layer on fragment-order activations), else
+ * UNFUSED (the reference's launch sequence of transformer.cpp:55-100:
+ * norm, qkv, rotary, attention, o, norm, gate_up, SwiGLU, down).
+ * PERSISTENT (one launch per evaluation, grid barriers between the layer's
+ * phases, weights loaded ahead of each barrier) is selected explicitly.
+ * Tests pin every path against the same oracle. */
+#define VX_DIT_PATH_AUTO 0
+#define VX_DIT_PATH_PERSISTENT 1
+#define VX_DIT_PATH_FUSED 2
+#define VX_DIT_PATH_UNFUSED 3
+
+/* Selects the evaluation path of later calls (VX_UNSUPPORTED when the
+ * shape has no such path). No reference counterpart: the reference has one
+ * path. */
+int vx_dit_set_path(vx_dit* dit, int path);
+/* The path that runs now (AUTO resolved), or -1 for a null handle. */
+int vx_dit_path(const vx_dit* dit);
+
+/* Timestamps of later persistent evaluations into a device buffer of at
+ * least vx_dit_trace_bytes() bytes (NULL stops recording): per workgroup
+ * and grid barrier, s_memrealtime (100 MHz) at arrival and at exit, and
+ * within the phase before it when its activations and its products were
+ * done; slot 0 holds the launch's start and end. Counterpart of Generator::set_trace
+ * (generator.hpp:58-95), which times the reference's stages. */
+int vx_dit_set_trace(vx_dit* dit, void* buffer, size_t bytes);
+size_t vx_dit_trace_bytes(const vx_dit* dit);
+
 #ifdef __cplusplus
 }
 #endif

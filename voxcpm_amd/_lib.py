@@ -15,6 +15,12 @@ VX_UNSUPPORTED = 1
 VX_BAD_ARG = 2
 VX_HIP_ERROR = 3
 
+# DiT evaluation paths (voxcpm_amd_internal.h).
+DIT_PATH_AUTO = 0
+DIT_PATH_PERSISTENT = 1
+DIT_PATH_FUSED = 2
+DIT_PATH_UNFUSED = 3
+
 c_size = ctypes.c_size_t
 c_int = ctypes.c_int
 c_float = ctypes.c_float
@@ -93,6 +99,11 @@ _SIGNATURES = {
     "vx_dit_eval": ([c_void_p] * 6 + [c_void_p], c_int),
     "vx_dit_velocity": ([c_void_p] * 4 + [c_float, c_void_p, c_void_p], c_int),
     "vx_dit_patch": ([c_void_p] * 7 + [c_size, c_float, c_int, c_void_p], c_int),
+    "vx_dit_status": ([c_void_p], c_int),
+    "vx_dit_set_path": ([c_void_p, c_int], c_int),
+    "vx_dit_path": ([c_void_p], c_int),
+    "vx_dit_set_trace": ([c_void_p, c_void_p, c_size], c_int),
+    "vx_dit_trace_bytes": ([c_void_p], c_size),
     "vx_euler_schedule": ([c_size, c_float, c_int, c_void_p, c_void_p,
                            c_void_p], c_int),
     "vx_rope_table": ([ctypes.c_double, c_size, c_void_p, c_float, c_size,

@@ -213,6 +213,31 @@ class Dit:
             lib().vx_dit_destroy(self.handle)
             self.handle = ctypes.c_void_p()
 
+    def set_path(self, path: int) -> None:
+        """Selects the evaluation path (voxcpm_amd._lib.DIT_PATH_*)."""
+        check(lib().vx_dit_set_path(self.handle, path))
+
+    @property
+    def path(self) -> int:
+        """The evaluation path that runs (AUTO resolved)."""
+        return lib().vx_dit_path(self.handle)
+
+    def set_trace(self, enable: bool = True) -> torch.Tensor | None:
+        """Records persistent evaluations' timestamps into a new int64 device
+        tensor [grid][barriers + 1][4] (returned), or stops recording."""
+        if not enable:
+            check(lib().vx_dit_set_trace(self.handle, None, 0))
+            self._trace = None
+            return None
+        words = lib().vx_dit_trace_bytes(self.handle) // 8
+        self._trace = torch.zeros(words, dtype=torch.int64, device=self.device)
+        check(lib().vx_dit_set_trace(self.handle, _ptr(self._trace), words * 8))
+        return self._trace
+
+    def status(self) -> None:
+        """Synchronizes; raises VxError if a persistent evaluation timed out."""
+        check(lib().vx_dit_status(self.handle))
+
     def __del__(self):
         try:
             self.close()
