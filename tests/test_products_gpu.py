@@ -29,6 +29,9 @@ SHAPES = [
     (8192, 512, [1, 22]),
     (1024, 72, [3, 22]),  # rows not a multiple of 16
     (2048, 2, [1]),
+    # odd block counts: the last pair's second block is past k
+    (96, 40, [1, 9, 22, 32]),
+    (160, 17, [3, 22]),
 ]
 LIMIT = 1e-5
 

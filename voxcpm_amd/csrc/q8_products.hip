@@ -305,42 +305,55 @@ Launcher PickLauncher(int mt, int rg) {
 
 // ---- the one-pass engine on row-major activations ---------------------------
 
-template<int MT, int RG>
+template<int MT, int RG, int PW, int JR>
 void LaunchEngine(const q8::TileArgs& args, int tiles, int waves,
                   hipStream_t stream) {
   const std::size_t shared =
-      q8::EngineShared(MT, RG, waves, q8::ASource::kRowMajor);
-  q8::EngineKernel<MT, RG, q8::ASource::kRowMajor, q8::Output::kStore>
+      q8::EngineShared(MT, RG, waves, q8::ASource::kRowMajor, PW);
+  q8::EngineKernel<MT, RG, q8::ASource::kRowMajor, q8::Output::kStore, PW, JR>
       <<<tiles, waves * kWave, shared, stream>>>(args);
 }
 
 using EngineLauncher = void (*)(const q8::TileArgs&, int, int, hipStream_t);
 
+/// Up to 32 rows the engine stages the rows through LDS in JR load groups
+/// of 8 rows; more rows load straight into the operands. One pair per wave
+/// per pass measures fastest on MI355X at every sweep shape (deeper
+/// in-flight passes need more registers and LDS and lose).
+template<int MT, int RG>
+EngineLauncher EngineJr(int m) {
+  if constexpr (q8::StagesRows(q8::ASource::kRowMajor, MT)) {
+    if (m <= 16 * MT - 8)
+      return LaunchEngine<MT, RG, 1, 2 * MT - 1>;
+  }
+  return LaunchEngine<MT, RG, 1, 2 * MT>;
+}
+
 template<int MT>
-EngineLauncher EngineRg(int rg) {
+EngineLauncher EngineRg(int rg, int m) {
   if constexpr (MT * 4 <= 8) {
     if (rg == 4)
-      return LaunchEngine<MT, 4>;
+      return EngineJr<MT, 4>(m);
   }
   if constexpr (MT * 2 <= 8) {
     if (rg == 2)
-      return LaunchEngine<MT, 2>;
+      return EngineJr<MT, 2>(m);
   }
   if (rg == 1)
-    return LaunchEngine<MT, 1>;
+    return EngineJr<MT, 1>(m);
   return nullptr;
 }
 
-EngineLauncher PickEngine(int mt, int rg) {
+EngineLauncher PickEngine(int mt, int rg, int m) {
   switch (mt) {
-    case 1: return EngineRg<1>(rg);
-    case 2: return EngineRg<2>(rg);
-    case 3: return EngineRg<3>(rg);
-    case 4: return EngineRg<4>(rg);
-    case 5: return EngineRg<5>(rg);
-    case 6: return EngineRg<6>(rg);
-    case 7: return EngineRg<7>(rg);
-    case 8: return EngineRg<8>(rg);
+    case 1: return EngineRg<1>(rg, m);
+    case 2: return EngineRg<2>(rg, m);
+    case 3: return EngineRg<3>(rg, m);
+    case 4: return EngineRg<4>(rg, m);
+    case 5: return EngineRg<5>(rg, m);
+    case 6: return EngineRg<6>(rg, m);
+    case 7: return EngineRg<7>(rg, m);
+    case 8: return EngineRg<8>(rg, m);
     default: return nullptr;
   }
 }
@@ -433,7 +446,7 @@ int RunSkinny(const Bf16* x, const void* w, float* y, Bf16* y_bf16,
               const ProductPlan& plan, float* partials, unsigned* counters,
               hipStream_t stream) {
   if (plan.engine) {
-    const EngineLauncher launch = PickEngine(plan.mt, plan.rg);
+    const EngineLauncher launch = PickEngine(plan.mt, plan.rg, static_cast<int>(m));
     if (launch == nullptr)
       return Fail(VX_UNSUPPORTED, "no product engine for this plan");
     q8::TileArgs args{};

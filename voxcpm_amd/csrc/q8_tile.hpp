@@ -12,7 +12,8 @@
 // bits.
 //
 // Activations come from one of three sources:
-//  - kRowMajor: bf16 [m][k] row-major (the drop-in product's x);
+//  - kRowMajor: bf16 [m][k] row-major (the drop-in product's x); up to
+//    32 rows are staged per wave through LDS from whole-line loads;
 //  - kFragBf16: bf16 in fragment order (below), written by the DiT kernels
 //    so that each wave's operand load is 1 KB of contiguous bytes;
 //  - kNormF32: the float32 residual stream in fragment order, RMS-normalised
@@ -118,9 +119,28 @@ constexpr int EngineThreads(int mt, int rg) {
   return (mt <= 2 && rg <= 2) ? 1024 : 512;
 }
 
-/// LDS bytes the engine needs for `waves` waves.
-inline std::size_t EngineShared(int mt, int rg, int waves, ASource source) {
-  std::size_t floats = static_cast<std::size_t>(waves) * rg * mt * 256;
+/// Row-major activations of up to 32 rows are staged per wave through LDS
+/// (below); more rows are loaded straight into the MFMA operands.
+__host__ __device__ constexpr bool StagesRows(ASource source, int mt) {
+  return source == ASource::kRowMajor && mt <= 2;
+}
+
+/// Floats of one wave's private row-staging region: PW pairs of 16 MT rows
+/// x 128 bytes.
+__host__ __device__ constexpr int StageFloats(int mt, int pw) {
+  return pw * mt * 16 * 32;
+}
+
+/// LDS bytes the engine needs for `waves` waves. The row-staging regions
+/// and the waves' partial sums share the same bytes (a barrier separates
+/// them).
+inline std::size_t EngineShared(int mt, int rg, int waves, ASource source, int pw = 1) {
+  std::size_t per_wave = static_cast<std::size_t>(rg) * mt * 256;
+  if (StagesRows(source, mt))
+    per_wave = per_wave > static_cast<std::size_t>(StageFloats(mt, pw))
+                   ? per_wave
+                   : static_cast<std::size_t>(StageFloats(mt, pw));
+  std::size_t floats = static_cast<std::size_t>(waves) * per_wave;
   if (source == ASource::kNormF32)
     floats += static_cast<std::size_t>(waves) * kFragRows;
   return floats * sizeof(float);
@@ -170,7 +190,8 @@ struct PairStage {
 /// The engine. Grid: one workgroup per tile (RG row groups); blockDim.x =
 /// EngineThreads(MT, RG) (waves without pairs add zeros). PW pairs per wave
 /// per pass; kNormF32 needs every pair in one pass (pairs <= waves * PW).
-template<int MT, int RG, ASource SRC, Output OUT, int PW = 1>
+/// Staged row-major sources load JR groups of 8 rows (8 JR >= m).
+template<int MT, int RG, ASource SRC, Output OUT, int PW = 1, int JR = 2 * MT>
 __global__ __launch_bounds__(EngineThreads(MT, RG)) void EngineKernel(TileArgs a) {
   static_assert(SRC != ASource::kNormF32 || MT == 2, "norm source is 32 rows");
   static_assert(OUT == Output::kStore || MT == 2, "fragment outputs are 32 rows");
@@ -221,6 +242,47 @@ __global__ __launch_bounds__(EngineThreads(MT, RG)) void EngineKernel(TileArgs a
             v = reinterpret_cast<const uint4*>(a.x)[((pair * 2 + t) * 2 + hf) * 64 + lane];
         }
         s.a[t][hf] = v;
+      }
+  };
+
+  // Row staging (row-major x of up to 32 rows): a pair's rows come in as
+  // whole 128-byte row segments, eight rows per load instruction (lane L:
+  // row 8 j + L / 8, bytes 16 (L % 8) .. + 15 of the segment), go to the
+  // wave's private LDS region with each 16-byte chunk index XORed with
+  // row % 8 (conflict-free writes and reads), and come back as the MFMA A
+  // fragments. A wave-load then touches 8 full cache lines instead of 16
+  // half-used ones.
+  static_assert(JR >= 1 && JR <= 2 * MT, "JR load groups of 8 rows cover the m rows");
+  struct RawRows {
+    uint4 v[JR];
+  };
+  const auto load_rows = [&](int pair, RawRows& raw) {
+    const int column = 64 * pair + 8 * (lane % 8);
+    const bool ok = pair < a.pairs && column < a.k;
+#pragma unroll
+    for (int j = 0; j < JR; ++j) {
+      const int row = 8 * j + lane / 8;
+      raw.v[j] = (ok && row < a.m)
+                     ? *reinterpret_cast<const uint4*>(
+                           a.x + static_cast<std::size_t>(row) * a.k + column)
+                     : uint4{0U, 0U, 0U, 0U};
+    }
+  };
+  const auto stage_rows = [&](int p, const RawRows& raw, PairStage<MT, RG>& s) {
+    uint4* region = reinterpret_cast<uint4*>(lds + wave * StageFloats(MT, PW)) + p * MT * 128;
+#pragma unroll
+    for (int j = 0; j < JR; ++j) {
+      const int row = 8 * j + lane / 8;
+      if (row < a.m)
+        region[row * 8 + ((lane % 8) ^ (row % 8))] = raw.v[j];
+    }
+#pragma unroll
+    for (int t = 0; t < MT; ++t)
+#pragma unroll
+      for (int hf = 0; hf < 2; ++hf) {
+        const int row = 16 * t + r16;
+        const int chunk = 4 * hf + octet;
+        s.a[t][hf] = row_ok[t] ? region[row * 8 + (chunk ^ (row % 8))] : uint4{0U, 0U, 0U, 0U};
       }
   };
 
@@ -345,6 +407,27 @@ __global__ __launch_bounds__(EngineThreads(MT, RG)) void EngineKernel(TileArgs a
     for (int p = 0; p < PW; ++p)
       if (wave + p * waves < a.pairs)
         multiply(stage[p]);
+  } else if constexpr (StagesRows(SRC, MT)) {
+    // Passes of PW pairs per wave (pair base + p waves + wave), every load
+    // of a pass issued before its first product; plans pick PW so that one
+    // pass covers k.
+    for (int base = 0; base < a.pairs; base += waves * PW) {
+      PairStage<MT, RG> stage[PW];
+      RawRows raw[PW];
+#pragma unroll
+      for (int p = 0; p < PW; ++p) {
+        load_weights(base + p * waves + wave, stage[p]);
+        load_rows(base + p * waves + wave, raw[p]);
+      }
+#pragma unroll
+      for (int p = 0; p < PW; ++p) {
+        stage_rows(p, raw[p], stage[p]);
+        if (base + p * waves + wave < a.pairs)
+          multiply(stage[p]);
+      }
+    }
+    // The partial sums below reuse the staging regions.
+    __syncthreads();
   } else {
     // Passes of PW pairs per wave (slot p of the pass at base: pair
     // base + p waves + wave); the next pass is loaded before this one is
