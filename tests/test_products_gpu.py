@@ -173,6 +173,27 @@ def test_products_beyond_32_rows(vx, oracle, cuda, stream, rows):
         assert oracle.q8_check(y, x, blocks, before if accumulate else None) <= LIMIT
 
 
+@pytest.mark.parametrize("rows,k,n", [(100, 1024, 16400), (128, 2048, 16384)])
+def test_tiled_exact_products(vx, oracle, cuda, stream, rows, k, n):
+    """More than 64 rows over wide outputs take the LDS-tiled kernel; it
+    keeps the exact per-block arithmetic (ragged rows and columns, and
+    accumulation)."""
+    rng = synth.Rng(77, rows + n)
+    blocks = reference_weights(rng, n, k)
+    packed = vx.q8_pack(to_device(blocks, cuda), n, k)
+    x = reference_activations(rng, rows, k)
+    before = rng.normal(rows * n).astype(np.float32).reshape(rows, n)
+    scratch = vx.Scratch(128, n)
+    cols = np.arange(0, n, 5)
+    for accumulate in (False, True):
+        y = run_product(vx, to_device(x, cuda), packed, n,
+                        before if accumulate else None, None, scratch, cuda)
+        worst = oracle.q8_check(np.ascontiguousarray(y[:, cols]), x,
+                                np.ascontiguousarray(blocks[cols]),
+                                np.ascontiguousarray(before[:, cols]) if accumulate else None)
+        assert worst <= LIMIT, f"accumulate {accumulate}: worst {worst:.3e}"
+
+
 def test_bf16_output_is_rounded_float_output(vx, cuda, stream):
     k, n, rows = 1024, 4096, 22
     rng = synth.Rng(0, 3)
@@ -221,7 +242,9 @@ def expanded_check(y, x, blocks, oracle, before=None):
 
 @pytest.mark.parametrize("rows,k,n", [(129, 2048, 2048), (256, 2048, 6144),
                                       (300, 1024, 2560), (512, 2048, 2048),
-                                      (1024, 2048, 1040)])
+                                      (1024, 2048, 1040),
+                                      # 128-row tiles, ragged rows and columns
+                                      (700, 1024, 4112)])
 def test_prefill_expansion(vx, oracle, cuda, stream, rows, k, n):
     """More than 128 rows: W as bf16(scale * q), float32 sums; the
     reference allows 1e-4 there (products_test.cpp:301-309)."""

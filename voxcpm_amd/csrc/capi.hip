@@ -85,8 +85,8 @@ int Product(const uint16_t* x, const void* packed, float* y, uint16_t* y_bf16,
             size_t m, size_t k, size_t n, int accumulate, vx_scratch* scratch,
             int rg, int waves, int splits, void* stream) {
   if (m > vx::kExactRows)
-    return vx::RunPrefill(x, packed, y, y_bf16, m, k, n, accumulate != 0,
-                          vx::Stream(stream));
+    return vx::RunTiled(x, packed, y, y_bf16, m, k, n, accumulate != 0, false,
+                        vx::Stream(stream));
   const vx::ProductPlan plan = vx::PlanSkinny(
       m, k, n, scratch != nullptr ? scratch->partial_floats : 0,
       scratch != nullptr ? scratch->counter_count : 0, rg, waves, splits);

@@ -1,5 +1,5 @@
 // Internal interface of the Q8_0 product kernels (q8_products.hip,
-// q8_prefill.hip) for the C ABI and the DiT.
+// q8_tiled.hip) for the C ABI and the DiT.
 #ifndef VOXCPM_AMD_PRODUCTS_HPP_
 #define VOXCPM_AMD_PRODUCTS_HPP_
 
@@ -23,6 +23,7 @@ constexpr std::size_t kExactRows = 128;
 /// also split k over workgroups.
 struct ProductPlan {
   bool engine = false;
+  bool tiled = false;  // default plans of more than 32 rows: RunTiled, exact
   int mt = 1;
   int rg = 1;
   int waves = 4;
@@ -50,10 +51,12 @@ int RunSkinny(const Bf16* x, const void* w, float* y, Bf16* y_bf16,
               const ProductPlan& plan, float* partials, unsigned* counters,
               hipStream_t stream);
 
-/// Launches the expanded product (any m; meant for m > 128).
-int RunPrefill(const Bf16* x, const void* w, float* y, Bf16* y_bf16,
-               std::size_t m, std::size_t k, std::size_t n, bool accumulate,
-               hipStream_t stream);
+/// Launches the LDS-tiled product (q8_tiled.hip; meant for m > 32): the
+/// exact per-block arithmetic, or with `exact` false the expansion to
+/// bf16(scale * q) of products of more than 128 rows.
+int RunTiled(const Bf16* x, const void* w, float* y, Bf16* y_bf16, std::size_t m,
+             std::size_t k, std::size_t n, bool accumulate, bool exact,
+             hipStream_t stream);
 
 }  // namespace vx
 

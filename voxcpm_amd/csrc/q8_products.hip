@@ -364,8 +364,20 @@ EngineLauncher PickEngine(int mt, int rg, int m) {
 /// register footprints).
 ProductPlan PlanEngine(std::size_t m, std::size_t k, std::size_t n) {
   ProductPlan plan;
-  plan.engine = true;
   plan.mt = static_cast<int>((m + 15) / 16);
+  if (plan.mt > 4 && (m + 63) / 64 * ((n + 127) / 128) >= 256) {
+    // More than 64 rows over wide outputs: the LDS-tiled kernel
+    // (q8_tiled.hip), faster there than the engine on MI355X.
+    plan.tiled = true;
+    plan.rg = 8;
+    plan.waves = 4;
+    plan.tiles = static_cast<int>((n + 127) / 128);
+    plan.splits = 1;
+    plan.pairs_per_split = static_cast<int>(q8::Pairs(k));
+    plan.pairs_per_wave = plan.pairs_per_split;
+    return plan;
+  }
+  plan.engine = true;
   const int groups = static_cast<int>(q8::Groups(n));
   const int pairs = static_cast<int>(q8::Pairs(k));
   int rg = groups <= 256 ? 1 : groups <= 512 ? 2 : 4;
@@ -445,6 +457,8 @@ int RunSkinny(const Bf16* x, const void* w, float* y, Bf16* y_bf16,
               std::size_t m, std::size_t k, std::size_t n, bool accumulate,
               const ProductPlan& plan, float* partials, unsigned* counters,
               hipStream_t stream) {
+  if (plan.tiled)
+    return RunTiled(x, w, y, y_bf16, m, k, n, accumulate, true, stream);
   if (plan.engine) {
     const EngineLauncher launch = PickEngine(plan.mt, plan.rg, static_cast<int>(m));
     if (launch == nullptr)

@@ -27,7 +27,12 @@
 //  - kResidual: added into the float32 fragment-order residual stream;
 //  - kSwiGlu: RG = 2 with the up rows `group_stride` row groups after the
 //    gate rows; bf16(silu(gate) * up) in bf16 fragment order
-//    (kernels/generator_kernels.hip:243-254).
+//    (kernels/generator_kernels.hip:243-254);
+//  - kTileMajor: float32 tile-major [groups][32][16] (2 KB per row group,
+//    rows m..31 zero) written as whole 16-byte chunks with device-scope
+//    stores that have completed when the engine body returns, so that
+//    another workgroup of the same launch may read them after an atomic
+//    handshake.
 #ifndef VOXCPM_AMD_Q8_TILE_HPP_
 #define VOXCPM_AMD_Q8_TILE_HPP_
 
@@ -84,7 +89,7 @@ inline std::size_t FragElements(std::size_t columns) {
 }
 
 enum class ASource : int { kRowMajor = 0, kFragBf16 = 1, kNormF32 = 2 };
-enum class Output : int { kStore = 0, kResidual = 1, kSwiGlu = 2 };
+enum class Output : int { kStore = 0, kResidual = 1, kSwiGlu = 2, kTileMajor = 3 };
 
 struct TileArgs {
   const std::uint8_t* w;  // panels [groups][pairs] units
@@ -134,16 +139,40 @@ __host__ __device__ constexpr int StageFloats(int mt, int pw) {
 /// LDS bytes the engine needs for `waves` waves. The row-staging regions
 /// and the waves' partial sums share the same bytes (a barrier separates
 /// them).
-inline std::size_t EngineShared(int mt, int rg, int waves, ASource source, int pw = 1) {
+__host__ __device__ constexpr std::size_t EngineShared(int mt, int rg, int waves,
+                                                      ASource source, int pw = 1) {
   std::size_t per_wave = static_cast<std::size_t>(rg) * mt * 256;
-  if (StagesRows(source, mt))
-    per_wave = per_wave > static_cast<std::size_t>(StageFloats(mt, pw))
-                   ? per_wave
-                   : static_cast<std::size_t>(StageFloats(mt, pw));
+  if (StagesRows(source, mt) && static_cast<std::size_t>(StageFloats(mt, pw)) > per_wave)
+    per_wave = static_cast<std::size_t>(StageFloats(mt, pw));
   std::size_t floats = static_cast<std::size_t>(waves) * per_wave;
   if (source == ASource::kNormF32)
     floats += static_cast<std::size_t>(waves) * kFragRows;
   return floats * sizeof(float);
+}
+
+/// Floats of LDS the kTileMajor epilogue stages its 32 x 16 block in,
+/// after the engine's own region.
+constexpr int kTileBlockFloats = 32 * 16;
+
+/// Element (row, column) of a tile-major float32 matrix [groups][32][16].
+__host__ __device__ inline std::size_t TileIndex(int row, int column) {
+  return (static_cast<std::size_t>(column / 16) * 32 + row) * 16 + column % 16;
+}
+
+/// 16 bytes with one device-scope store (global_store_dwordx4 with sc1, the
+/// cache policy of a relaxed agent-scope atomic store): written through to
+/// memory, visible to every compute die once the store has completed.
+__device__ inline void StoreDevice16(void* p, const uint4& v) {
+  typedef unsigned U32x4 __attribute__((ext_vector_type(4)));
+  const U32x4 d{v.x, v.y, v.z, v.w};
+  asm volatile("global_store_dwordx4 %0, %1, off sc1" : : "v"(p), "v"(d) : "memory");
+}
+
+/// Every memory operation this wave issued has completed.
+__device__ inline void WaitMemory() {
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+  __builtin_amdgcn_s_waitcnt(0);
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
 }
 
 __device__ inline float Silu(float value) {
@@ -192,10 +221,11 @@ struct PairStage {
 /// per pass; kNormF32 needs every pair in one pass (pairs <= waves * PW).
 /// Staged row-major sources load JR groups of 8 rows (8 JR >= m).
 template<int MT, int RG, ASource SRC, Output OUT, int PW = 1, int JR = 2 * MT>
-__global__ __launch_bounds__(EngineThreads(MT, RG)) void EngineKernel(TileArgs a) {
+__device__ __forceinline__ void EngineBody(const TileArgs& a) {
   static_assert(SRC != ASource::kNormF32 || MT == 2, "norm source is 32 rows");
   static_assert(OUT == Output::kStore || MT == 2, "fragment outputs are 32 rows");
   static_assert(OUT != Output::kSwiGlu || RG == 2, "SwiGLU pairs two groups");
+  static_assert(OUT != Output::kTileMajor || RG == 1, "tile-major blocks are one group");
   extern __shared__ float lds[];
   const int lane = threadIdx.x % kWave;
   const int wave = threadIdx.x / kWave;
@@ -215,6 +245,39 @@ __global__ __launch_bounds__(EngineThreads(MT, RG)) void EngineKernel(TileArgs a
 #pragma unroll
   for (int t = 0; t < MT; ++t)
     row_ok[t] = 16 * t + r16 < a.m;
+
+  // Output element e of the tile (thread e, e + threads, ...): fragment
+  // f = r MT + t, accumulator i, lane l -> (row, column); false past m / n.
+  constexpr int kThreads = EngineThreads(MT, RG);
+  constexpr int kOutputsPerThread = (RG * MT * 256 + kThreads - 1) / kThreads;
+  const auto output_of = [&](int e, int& row, int& column) {
+    const int f = e / 256;
+    const int i = (e / 64) % 4;
+    const int l = e % 64;
+    const int r = f / MT;
+    const int t = f % MT;
+    row = 16 * t + 4 * (l / 16) + i;
+    const int group = RgGroup(tile, r, a.group_stride, RG);
+    column = 16 * group + l % 16;
+    return row < a.m && group < a.groups && column < a.n;
+  };
+  // The values the epilogue adds to (the residual stream, an accumulated
+  // y) are loaded now, beside the first weights, instead of after the sums.
+  float before[kOutputsPerThread];
+#pragma unroll
+  for (int u = 0; u < kOutputsPerThread; ++u) {
+    before[u] = 0.0F;
+    const int e = static_cast<int>(threadIdx.x) + u * kThreads;
+    int row, column;
+    if (e >= RG * MT * 256 || !output_of(e, row, column))
+      continue;
+    if constexpr (OUT == Output::kResidual) {
+      before[u] = a.residual[F32FragIndex(row, column)];
+    } else if constexpr (OUT == Output::kStore) {
+      if (a.y != nullptr && a.accumulate)
+        before[u] = a.y[static_cast<std::size_t>(row) * a.n + column];
+    }
+  }
 
   const auto load_weights = [&](int pair, PairStage<MT, RG>& s) {
     const bool ok = pair < a.pairs;
@@ -316,6 +379,9 @@ __global__ __launch_bounds__(EngineThreads(MT, RG)) void EngineKernel(TileArgs a
   };
 
   float* reduce = lds;
+  // kTileMajor: the output block, after the engine's region.
+  float* block = lds + EngineShared(MT, RG, waves, SRC, PW) / sizeof(float);
+  (void)block;
   if constexpr (SRC == ASource::kNormF32) {
     // Every pair in this pass: wave w owns pairs w, w + waves, ...
     float* squares = lds + static_cast<std::size_t>(waves) * RG * MT * 256;
@@ -485,31 +551,47 @@ __global__ __launch_bounds__(EngineThreads(MT, RG)) void EngineKernel(TileArgs a
     return total;
   };
   const int outputs = OUT == Output::kSwiGlu ? MT * 256 : kFragmentFloats;
-  for (int e = threadIdx.x; e < outputs; e += blockDim.x) {
-    const int f = e / 256;
-    const int i = (e / 64) % 4;
-    const int l = e % 64;
-    const int r = f / MT;
-    const int t = f % MT;
-    const int row = 16 * t + 4 * (l / 16) + i;
-    const int group = RgGroup(tile, r, a.group_stride, RG);
-    const int column = 16 * group + l % 16;
-    if (row >= a.m || group >= a.groups || column >= a.n)
+#pragma unroll
+  for (int u = 0; u < kOutputsPerThread; ++u) {
+    const int e = static_cast<int>(threadIdx.x) + u * kThreads;
+    int row, column;
+    if (e >= outputs || !output_of(e, row, column))
       continue;
     const float v = total_of(e);
     if constexpr (OUT == Output::kStore) {
       const std::size_t at = static_cast<std::size_t>(row) * a.n + column;
       if (a.y != nullptr)
-        a.y[at] = a.accumulate ? a.y[at] + v : v;
+        a.y[at] = a.accumulate ? before[u] + v : v;
       else
         a.y_bf16[at] = Bf16Fast(v);
     } else if constexpr (OUT == Output::kResidual) {
-      a.residual[F32FragIndex(row, column)] += v;
-    } else {
+      a.residual[F32FragIndex(row, column)] = before[u] + v;
+    } else if constexpr (OUT == Output::kSwiGlu) {
       const float up = total_of(e + MT * 256);
       a.frag_out[BfFragIndex(row, column)] = Bf16Fast(Silu(v) * up);
+    } else {
+      block[row * 16 + column % 16] = v;
     }
   }
+  if constexpr (OUT == Output::kTileMajor) {
+    // The 32 x 16 block (rows past m zero) in whole 16-byte chunks: thread
+    // (row, quad) -> 16 contiguous bytes of row `row` of the group's 2 KB.
+    __syncthreads();
+    if (threadIdx.x < 128) {
+      const int row = static_cast<int>(threadIdx.x) / 4;
+      const int quad = static_cast<int>(threadIdx.x) % 4;
+      const float4 v = row < a.m ? *reinterpret_cast<const float4*>(block + row * 16 + 4 * quad)
+                                 : float4{0.0F, 0.0F, 0.0F, 0.0F};
+      StoreDevice16(a.y + (static_cast<std::size_t>(tile) * 32 + row) * 16 + 4 * quad,
+                    __builtin_bit_cast(uint4, v));
+    }
+    WaitMemory();
+  }
+}
+
+template<int MT, int RG, ASource SRC, Output OUT, int PW = 1, int JR = 2 * MT>
+__global__ __launch_bounds__(EngineThreads(MT, RG)) void EngineKernel(TileArgs a) {
+  EngineBody<MT, RG, SRC, OUT, PW, JR>(a);
 }
 
 }  // namespace vx::q8

@@ -1,0 +1,306 @@
+// Q8_0 x bfloat16 products of more than 32 activation rows on gfx950's
+// matrix cores: LDS-tiled, BM activation rows x 128 weight rows per
+// workgroup, 64 columns (one panel pair, two Q8_0 blocks) per step.
+//
+// Two arithmetics, as the reference dispatches them (gemm.cpp:259-313):
+//  - exact (up to 128 rows, kernels/wmma_products.hip:192-215): the int8
+//    values become bf16 exactly, each 32-column block is one
+//    v_mfma_f32_16x16x32_bf16 from zero, and acc = fmaf(f16 scale, block
+//    sum, acc) walks the blocks in k order;
+//  - expanded (more rows, gemm.cpp:305-312 with
+//    kernels/wmma_products.hip:94-112): every weight becomes
+//    bf16_rne(f32(f16 scale) * q) once per workgroup and step, and the MFMAs
+//    accumulate over all of k in float32.
+//
+// Per step the threads load the step after next into registers (two
+// register sets, so a load has two steps of MFMAs to arrive), convert the
+// next step's weights into the other LDS buffer, and multiply the current
+// one: BM / 32 x 2 waves, each 32 activation rows x 64 weight rows of the
+// tile. Consecutive tiles (the activation-row tiles of one weight tile
+// first) are placed on one compute die, whose L2 then serves their shared
+// weights.
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+#include "common.hpp"
+#include "products.hpp"
+#include "q8.hpp"
+#include "q8_tile.hpp"
+
+namespace vx {
+namespace {
+
+using q8::AsBf16x8;
+using q8::Bf16x8;
+using q8::F32x4;
+using q8::Int8x8ToBf16;
+using q8::kUnitBytes;
+using q8::kValueBytes;
+using q8::Mfma16x16x32;
+using q8::PackBf16x2;
+
+constexpr int kTileN = 128;
+// LDS rows: 64 bf16 plus 8 of padding (144 bytes, 9 chunks of 16 bytes), so
+// that the fragment reads of 16 consecutive rows fall on distinct banks.
+constexpr int kRowChunks = 9;
+constexpr int kDies = 8;
+
+struct TiledArgs {
+  const Bf16* x;
+  const std::uint8_t* w;
+  float* y;
+  Bf16* y_bf16;
+  int m, k, n;
+  int pairs, groups;
+  int m_tiles, n_tiles;
+  int accumulate;
+};
+
+/// 8 int8 values (two little-endian dwords) times `scale`, each rounded to
+/// bf16 (nearest even) by v_cvt_pk_bf16_f32.
+__device__ inline uint4 Expand(std::uint32_t w0, std::uint32_t w1, float scale) {
+  const auto v = [&](std::uint32_t word, int byte) {
+    return scale * static_cast<float>(static_cast<std::int8_t>(word >> (8 * byte)));
+  };
+  return uint4{PackBf16x2(v(w0, 0), v(w0, 1)), PackBf16x2(v(w0, 2), v(w0, 3)),
+               PackBf16x2(v(w1, 0), v(w1, 1)), PackBf16x2(v(w1, 2), v(w1, 3))};
+}
+
+/// Logical tile of workgroup `b` of `blocks`: workgroup b runs on die b % 8;
+/// die d takes a contiguous range of logical tiles (the first blocks % 8
+/// dies one more). A bijection on 0..blocks-1.
+__device__ inline int DieOrdered(int b, int blocks) {
+  const int per = blocks / kDies;
+  const int extra = blocks % kDies;
+  const int die = b % kDies;
+  const int index = b / kDies;
+  return die < extra ? die * (per + 1) + index
+                     : extra * (per + 1) + (die - extra) * per + index;
+}
+
+/// A tile shape: BM activation rows, WM waves along them (x 2 along the 128
+/// weight rows, each wave BM / WM x 64), D register sets of prefetched
+/// steps, and the workgroups per compute unit the registers are sized for.
+template<int BM, int WM, int D, int MINB>
+struct TileShape {
+  static constexpr int kBm = BM;
+  static constexpr int kThreads = WM * 2 * kWave;
+  static constexpr int kAPieces = BM * 8 / kThreads;  // 16-byte A pieces per thread per step
+  static constexpr int kUnits = 8 / (WM * 2);         // panel units per wave per step
+  static constexpr int kMi = BM / WM / 16;             // 16-row MFMA tiles per wave
+  static constexpr int kD = D;
+  static constexpr int kMinBlocks = MINB;
+};
+
+template<class T, bool EXACT>
+__global__ __launch_bounds__(T::kThreads, T::kMinBlocks) void TiledKernel(TiledArgs a) {
+  constexpr int BM = T::kBm;
+  constexpr int kThreads = T::kThreads;
+  constexpr int kAPieces = T::kAPieces;
+  constexpr int kUnits = T::kUnits;
+  constexpr int kMi = T::kMi;
+  constexpr int D = T::kD;
+  __shared__ uint4 lds_a[2][BM * kRowChunks];
+  __shared__ uint4 lds_b[2][kTileN * kRowChunks];
+  __shared__ float lds_s[EXACT ? 2 : 1][EXACT ? kTileN * 2 : 1];
+  const int tid = static_cast<int>(threadIdx.x);
+  const int lane = tid % kWave;
+  const int wave = tid / kWave;
+  const int r16 = lane % 16;
+  const int octet = lane / 16;
+  const int logical = DieOrdered(static_cast<int>(blockIdx.x), a.m_tiles * a.n_tiles);
+  const int row0 = (logical % a.m_tiles) * BM;
+  const int group0 = (logical / a.m_tiles) * (kTileN / 16);
+
+  struct Staging {
+    uint4 x[kAPieces];
+    uint4 w[kUnits];
+    std::uint32_t scales[kUnits];
+  };
+  const auto fetch = [&](int pair, Staging& s) {
+#pragma unroll
+    for (int i = 0; i < kAPieces; ++i) {
+      const int piece = tid + kThreads * i;
+      const int row = row0 + piece / 8;
+      const int column = 64 * pair + 8 * (piece % 8);
+      s.x[i] = (row < a.m && column < a.k)
+                   ? *reinterpret_cast<const uint4*>(a.x + static_cast<std::size_t>(row) * a.k +
+                                                     column)
+                   : uint4{0U, 0U, 0U, 0U};
+    }
+#pragma unroll
+    for (int u = 0; u < kUnits; ++u) {
+      const int group = min(group0 + kUnits * wave + u, a.groups - 1);
+      const std::uint8_t* unit =
+          a.w + (static_cast<std::size_t>(group) * a.pairs + pair) * kUnitBytes;
+      s.w[u] = *reinterpret_cast<const uint4*>(unit + 16 * lane);
+      s.scales[u] = *reinterpret_cast<const std::uint32_t*>(unit + kValueBytes + 4 * r16);
+    }
+  };
+  const auto store = [&](int buffer, const Staging& s) {
+#pragma unroll
+    for (int i = 0; i < kAPieces; ++i) {
+      const int piece = tid + kThreads * i;
+      lds_a[buffer][(piece / 8) * kRowChunks + piece % 8] = s.x[i];
+    }
+#pragma unroll
+    for (int u = 0; u < kUnits; ++u) {
+      const int row = 16 * (kUnits * wave + u) + r16;
+      const float s0 = HalfValue(static_cast<std::uint16_t>(s.scales[u] & 0xFFFFU));
+      const float s1 = HalfValue(static_cast<std::uint16_t>(s.scales[u] >> 16));
+      uint4 first, second;
+      if constexpr (EXACT) {
+        first = __builtin_bit_cast(uint4, Int8x8ToBf16(s.w[u].x, s.w[u].y));
+        second = __builtin_bit_cast(uint4, Int8x8ToBf16(s.w[u].z, s.w[u].w));
+        if (octet == 0) {
+          lds_s[buffer][2 * row] = s0;
+          lds_s[buffer][2 * row + 1] = s1;
+        }
+      } else {
+        first = Expand(s.w[u].x, s.w[u].y, s0);
+        second = Expand(s.w[u].z, s.w[u].w, s1);
+      }
+      lds_b[buffer][row * kRowChunks + octet] = first;
+      lds_b[buffer][row * kRowChunks + 4 + octet] = second;
+    }
+  };
+
+  const int wm = wave / 2;
+  const int wn = wave % 2;
+  F32x4 acc[kMi][4];
+#pragma unroll
+  for (int i = 0; i < kMi; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      acc[i][j] = F32x4{0.0F, 0.0F, 0.0F, 0.0F};
+
+  const auto compute = [&](int buffer) {
+    const F32x4 zero{0.0F, 0.0F, 0.0F, 0.0F};
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      Bf16x8 af[kMi], bf[4];
+      float scale[4];
+#pragma unroll
+      for (int i = 0; i < kMi; ++i)
+        af[i] = AsBf16x8(
+            lds_a[buffer][((BM / (kThreads / kWave / 2)) * wm + 16 * i + r16) * kRowChunks +
+                          4 * h + octet]);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int row = 64 * wn + 16 * j + r16;
+        bf[j] = AsBf16x8(lds_b[buffer][row * kRowChunks + 4 * h + octet]);
+        if constexpr (EXACT)
+          scale[j] = lds_s[buffer][2 * row + h];
+      }
+#pragma unroll
+      for (int i = 0; i < kMi; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          if constexpr (EXACT) {
+            const F32x4 sum = Mfma16x16x32(af[i], bf[j], zero);
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+              acc[i][j][e] = fmaf(scale[j], sum[e], acc[i][j][e]);
+          } else {
+            acc[i][j] = Mfma16x16x32(af[i], bf[j], acc[i][j]);
+          }
+        }
+    }
+  };
+
+  // D register sets: set q % D holds step q from its fetch (D steps ahead)
+  // until its store; LDS buffer q % 2 holds step q while it is multiplied.
+  // The loop is unrolled over a multiple of D and 2 so that both indices
+  // are compile-time.
+  constexpr int U = D % 2 == 0 ? D : 2 * D;
+  Staging staged[D];
+#pragma unroll
+  for (int d = 0; d < D; ++d)
+    if (d < a.pairs)
+      fetch(d, staged[d]);
+  store(0, staged[0]);
+  __syncthreads();
+  for (int p = 0; p < a.pairs; p += U) {
+#pragma unroll
+    for (int d = 0; d < U; ++d) {
+      const int q = p + d;
+      if (q >= a.pairs)
+        break;
+      if (q + D < a.pairs)
+        fetch(q + D, staged[d % D]);
+      compute(d % 2);
+      if (q + 1 < a.pairs)
+        store((d + 1) % 2, staged[(d + 1) % D]);
+      __syncthreads();
+    }
+  }
+
+  constexpr int kRowsPerWave = BM / (kThreads / kWave / 2);
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int column = 16 * group0 + 64 * wn + 16 * j + r16;
+    if (column >= a.n)
+      continue;
+#pragma unroll
+    for (int i = 0; i < kMi; ++i)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int row = row0 + kRowsPerWave * wm + 16 * i + 4 * octet + e;
+        if (row >= a.m)
+          continue;
+        const std::size_t at = static_cast<std::size_t>(row) * a.n + column;
+        if (a.y_bf16 != nullptr)
+          a.y_bf16[at] = q8::Bf16Fast(acc[i][j][e]);
+        else
+          a.y[at] = a.accumulate ? a.y[at] + acc[i][j][e] : acc[i][j][e];
+      }
+  }
+}
+
+template<class T, bool EXACT>
+void Launch(const TiledArgs& args, hipStream_t stream) {
+  TiledKernel<T, EXACT><<<args.m_tiles * args.n_tiles, T::kThreads, 0, stream>>>(args);
+}
+
+using Small = TileShape<64, 2, 2, 2>;
+using Large = TileShape<128, 4, 2, 1>;
+
+}  // namespace
+
+int RunTiled(const Bf16* x, const void* w, float* y, Bf16* y_bf16, std::size_t m,
+             std::size_t k, std::size_t n, bool accumulate, bool exact,
+             hipStream_t stream) {
+  TiledArgs args;
+  args.x = x;
+  args.w = static_cast<const std::uint8_t*>(w);
+  args.y = y;
+  args.y_bf16 = y_bf16;
+  args.m = static_cast<int>(m);
+  args.k = static_cast<int>(k);
+  args.n = static_cast<int>(n);
+  args.pairs = static_cast<int>(q8::Pairs(k));
+  args.groups = static_cast<int>(q8::Groups(n));
+  args.n_tiles = static_cast<int>((n + kTileN - 1) / kTileN);
+  args.accumulate = accumulate ? 1 : 0;
+  // 128-row tiles (8 waves of 32 x 64) once they give at least 192
+  // workgroups, else 64-row tiles (4 waves, two workgroups per compute
+  // unit): the faster of the two at every prefill shape measured on MI355X.
+  const std::size_t tiles128 = (m + 127) / 128 * static_cast<std::size_t>(args.n_tiles);
+  const int bm = m > 64 && tiles128 >= 192 ? 128 : 64;
+  args.m_tiles = static_cast<int>((m + bm - 1) / bm);
+  if (bm == 64) {
+    if (exact)
+      Launch<Small, true>(args, stream);
+    else
+      Launch<Small, false>(args, stream);
+  } else {
+    if (exact)
+      Launch<Large, true>(args, stream);
+    else
+      Launch<Large, false>(args, stream);
+  }
+  return LaunchStatus(exact ? "q8 tiled product" : "q8 expanded product");
+}
+
+}  // namespace vx
