@@ -118,11 +118,6 @@ struct vx_dit {
   float* h_frag = nullptr;
   Bf16* attention_frag = nullptr;
   Bf16* swiglu_frag = nullptr;
-  // qkv with the attention in one launch (vx::fused::QkvAttention): the
-  // tile-major qkv and the per-head arrival counters.
-  bool fuses_attention = false;
-  float* qkv_tiles = nullptr;
-  unsigned* head_arrivals = nullptr;
 
   // The persistent evaluation (one launch per evaluation): its write-once
   // workspace and barrier counters.
@@ -159,8 +154,7 @@ struct vx_dit {
           static_cast<void*>(middle), static_cast<void*>(delta),
           static_cast<void*>(bf16), static_cast<void*>(time_bf16),
           static_cast<void*>(h_frag), static_cast<void*>(attention_frag),
-          static_cast<void*>(swiglu_frag), static_cast<void*>(qkv_tiles),
-          static_cast<void*>(head_arrivals), static_cast<void*>(workspace.h),
+          static_cast<void*>(swiglu_frag), static_cast<void*>(workspace.h),
           static_cast<void*>(workspace.qkv),
           static_cast<void*>(workspace.attention),
           static_cast<void*>(workspace.swiglu),
@@ -280,13 +274,8 @@ struct vx_dit {
     vx::fused::InAssemble(x, weights.in_proj.weight, weights.in_proj.bias, mu,
                           time, cond, h_frag, fs, stream);
     for (const vx_dit_layer& layer : layers) {
-      if (fuses_attention) {
-        vx::fused::QkvAttention(h_frag, layer.input_norm, layer.qkv, weights.rope,
-                                qkv_tiles, head_arrivals, attention_frag, fs, stream);
-      } else {
-        vx::fused::Qkv(h_frag, layer.input_norm, layer.qkv, qkv, fs, stream);
-        vx::fused::Attention(qkv, weights.rope, attention_frag, fs, stream);
-      }
+      vx::fused::Qkv(h_frag, layer.input_norm, layer.qkv, qkv, fs, stream);
+      vx::fused::Attention(qkv, weights.rope, attention_frag, fs, stream);
       vx::fused::Residual(attention_frag, layer.o,
                           static_cast<int>(q_width), fs.hidden, h_frag, fs,
                           stream);
@@ -465,13 +454,7 @@ int Create(vx_dit* dit) {
            "vx_dit_create: hipMemset");
     VX_HIP(hipMemset(dit->swiglu_frag, 0, s_count * sizeof(Bf16)),
            "vx_dit_create: hipMemset");
-    dit->fuses_attention = false && vx::fused::FusesAttention(fs);
-    if (dit->fuses_attention) {
-      VX_TRY(Allocate(&dit->qkv_tiles, vx::q8::Groups(dit->qkv_width) * 32 * 16));
-      VX_TRY(Allocate(&dit->head_arrivals, s.heads));
-      VX_HIP(hipMemset(dit->head_arrivals, 0, s.heads * sizeof(unsigned)),
-             "vx_dit_create: hipMemset");
-    }
+
     dit->grid = vx::persistent::GridSize();
     const int layers = static_cast<int>(s.layers);
     dit->persistent = vx::persistent::Supported(fs, layers, dit->grid) &&

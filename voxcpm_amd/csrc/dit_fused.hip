@@ -129,18 +129,6 @@ struct AttentionArgs {
   float scale;
 };
 
-/// Element d of a rotated head vector `p` at table row `table`:
-/// (a, b) at (i, i + half) -> (a c - b s, b c + a s).
-__device__ inline float Rotated(const float* p, int d, int half,
-                                const float* table) {
-  if (table == nullptr)
-    return p[d];
-  if (d < half)
-    return p[d] * table[d] - p[d + half] * table[half + d];
-  const int i = d - half;
-  return p[d] * table[i] + p[i] * table[half + i];
-}
-
 // One workgroup per (branch, head). Every thread issues its loads at once:
 // for query/key row r and dimensions d..d+3 (d < head_dim / 2) the pair
 // halves of q and k, the two halves of v and the row's cos / sin. The
@@ -258,238 +246,6 @@ __global__ __launch_bounds__(256) void AttentionKernel(AttentionArgs a) {
       out[x] *= inverse[i];
     const int row = branch * a.length + i;
     *reinterpret_cast<uint4*>(a.out + BfFragIndex(row, head * dims + d)) = q8::PackBf16x8(out);
-  }
-}
-
-// ---- qkv with each head's attention in its last workgroup ---------------------
-//
-// The qkv product writes its 16-column groups tile-major with device-scope
-// stores (q8_tile.hpp kTileMajor), then counts itself in for every head the
-// group feeds (a q group one head, a k or v group the heads sharing its kv
-// head). The workgroup whose arrival completes a head (3 head_dim / 16
-// groups) resets the head's counter and runs that head's rotary embedding
-// and attention for both branches, so the attention costs no launch of its
-// own. Every group of a head was written whole and its stores completed
-// before its workgroup counted in, and nothing in the launch reads a group
-// before its head completes, so the last workgroup's plain loads see them.
-
-struct HeadArgs {
-  const float* qkv;     // tile-major [groups][32][16]
-  const float* rope;    // [length][head_dim] cos | sin, or null
-  unsigned* arrivals;   // [heads], zero between launches
-  Bf16* out;            // bf16 fragment order [32][heads head_dim]
-  int rows, length, heads, kv_heads, head_dim, q_width;
-  float scale;
-};
-
-constexpr int kHeadThreads = 1024;
-
-/// LDS floats of one head's attention: rotated, scaled queries, rotated
-/// keys and values [32][head_dim + 4] each, the softmax weights [2][16][16],
-/// the inverse sums [32] and the bf16 result [32][head_dim].
-__host__ __device__ inline int HeadFloats(int head_dim) {
-  return 3 * 32 * (head_dim + 4) + 2 * kMaxLength * kMaxLength + 32 + 16 * head_dim;
-}
-
-/// Rotary embedding (kernels/generator_kernels.hip:110-158) and
-/// bidirectional attention within each branch (160-241) of head `head` for
-/// all rows, from the tile-major qkv; the head's bf16 output block goes to
-/// fragment order. 1024 threads.
-__device__ void HeadAttention(const HeadArgs& a, int head, float* lds) {
-  const int tid = static_cast<int>(threadIdx.x);
-  const int dims = a.head_dim;
-  const int half = dims / 2;
-  const int kv_head = head / (a.heads / a.kv_heads);
-  const int stride = dims + 4;
-  float* qs = lds;                                        // [32][stride]
-  float* ks = qs + 32 * stride;                           // [32][stride]
-  float* vs = ks + 32 * stride;                           // [32][stride]
-  float* weights = vs + 32 * stride;                      // [2][16][16]
-  float* inverse = weights + 2 * kMaxLength * kMaxLength;  // [32]
-  Bf16* result = reinterpret_cast<Bf16*>(inverse + 32);    // [32][dims]
-  const int quads = half / 4;
-  const int q_column = head * dims;
-  const int k_column = a.q_width + kv_head * dims;
-  const int v_column = a.q_width + (a.kv_heads + kv_head) * dims;
-  for (int e = tid; e < a.rows * quads; e += kHeadThreads) {
-    const int r = e / quads;  // row of the pair
-    const int d = 4 * (e % quads);
-    const auto quad = [&](int column) {
-      return *reinterpret_cast<const float4*>(a.qkv + q8::TileIndex(r, column));
-    };
-    const float4 q0 = quad(q_column + d);
-    const float4 q1 = quad(q_column + half + d);
-    const float4 k0 = quad(k_column + d);
-    const float4 k1 = quad(k_column + half + d);
-    const float4 v0 = quad(v_column + d);
-    const float4 v1 = quad(v_column + half + d);
-    float4 c{1.0F, 1.0F, 1.0F, 1.0F};
-    float4 sn{0.0F, 0.0F, 0.0F, 0.0F};
-    if (a.rope != nullptr) {
-      const float* table = a.rope + static_cast<std::size_t>(r % a.length) * dims;
-      c = *reinterpret_cast<const float4*>(table + d);
-      sn = *reinterpret_cast<const float4*>(table + half + d);
-    }
-    const float qa[4] = {q0.x, q0.y, q0.z, q0.w};
-    const float qb[4] = {q1.x, q1.y, q1.z, q1.w};
-    const float ka[4] = {k0.x, k0.y, k0.z, k0.w};
-    const float kb[4] = {k1.x, k1.y, k1.z, k1.w};
-    const float cs[4] = {c.x, c.y, c.z, c.w};
-    const float ss[4] = {sn.x, sn.y, sn.z, sn.w};
-    float qf[4], qs2[4], kf[4], ks2[4];
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      // (a, b) at (i, i + half) -> (a c - b s, b c + a s)
-      qf[j] = qa[j];
-      qs2[j] = qb[j];
-      kf[j] = ka[j];
-      ks2[j] = kb[j];
-      if (a.rope != nullptr) {
-        qf[j] = qa[j] * cs[j] - qb[j] * ss[j];
-        qs2[j] = qb[j] * cs[j] + qa[j] * ss[j];
-        kf[j] = ka[j] * cs[j] - kb[j] * ss[j];
-        ks2[j] = kb[j] * cs[j] + ka[j] * ss[j];
-      }
-    }
-    const float scale = a.scale;
-    *reinterpret_cast<float4*>(qs + r * stride + d) =
-        float4{qf[0] * scale, qf[1] * scale, qf[2] * scale, qf[3] * scale};
-    *reinterpret_cast<float4*>(qs + r * stride + half + d) =
-        float4{qs2[0] * scale, qs2[1] * scale, qs2[2] * scale, qs2[3] * scale};
-    *reinterpret_cast<float4*>(ks + r * stride + d) = float4{kf[0], kf[1], kf[2], kf[3]};
-    *reinterpret_cast<float4*>(ks + r * stride + half + d) =
-        float4{ks2[0], ks2[1], ks2[2], ks2[3]};
-    *reinterpret_cast<float4*>(vs + r * stride + d) = v0;
-    *reinterpret_cast<float4*>(vs + r * stride + half + d) = v1;
-  }
-  __syncthreads();
-  {
-    // Scores: thread -> (branch, query i, key j, half of the dimensions);
-    // the two halves meet by one shuffle, the 16 keys of a query are 32
-    // consecutive lanes.
-    const int part = tid % 2;
-    const int j = (tid / 2) % kMaxLength;
-    const int i = (tid / 32) % kMaxLength;
-    const int branch = tid / 512;
-    const bool valid = i < a.length && j < a.length;
-    float partial[4] = {0.0F, 0.0F, 0.0F, 0.0F};
-    if (valid) {
-      const int base = branch * a.length;
-      const float4* qp = reinterpret_cast<const float4*>(qs + (base + i) * stride) + part * quads;
-      const float4* kp = reinterpret_cast<const float4*>(ks + (base + j) * stride) + part * quads;
-      for (int c = 0; c < quads; c += 4) {
-        float4 qv[4], kv[4];
-#pragma unroll
-        for (int u = 0; u < 4; ++u) {
-          qv[u] = qp[c + u];
-          kv[u] = kp[c + u];
-        }
-#pragma unroll
-        for (int u = 0; u < 4; ++u)
-          partial[u] += qv[u].x * kv[u].x + qv[u].y * kv[u].y + qv[u].z * kv[u].z +
-                        qv[u].w * kv[u].w;
-      }
-    }
-    float dot = (partial[0] + partial[1]) + (partial[2] + partial[3]);
-    dot += __shfl_xor(dot, 1, kWave);
-    const float score = valid ? dot : -INFINITY;
-    float maximum = score;
-#pragma unroll
-    for (int offset = 2; offset < 2 * kMaxLength; offset *= 2)
-      maximum = fmaxf(maximum, __shfl_xor(maximum, offset, kWave));
-    const float weight = valid ? expf(score - maximum) : 0.0F;
-    float sum = weight;
-#pragma unroll
-    for (int offset = 2; offset < 2 * kMaxLength; offset *= 2)
-      sum += __shfl_xor(sum, offset, kWave);
-    if (part == 0) {
-      weights[(branch * kMaxLength + i) * kMaxLength + j] = weight;
-      if (j == 0 && i < a.length)
-        inverse[branch * a.length + i] = 1.0F / sum;
-    }
-  }
-  __syncthreads();
-  // Weighted values: thread -> (row, octet of dimensions, half of the
-  // keys); the halves meet through one lane shuffle.
-  const int octets = dims / 8;
-  const int units = a.rows * octets * 2;
-  for (int e = tid; e < ((units + kWave - 1) / kWave) * kWave; e += kHeadThreads) {
-    const bool active = e < units;
-    const int part = e % 2;
-    const int r = active ? e / 2 / octets : 0;
-    const int branch = r / a.length;
-    const int i = r % a.length;
-    const int d = active ? 8 * ((e / 2) % octets) : 0;
-    float o[8] = {0, 0, 0, 0, 0, 0, 0, 0};
-#pragma unroll
-    for (int u = 0; u < kMaxLength / 2; ++u) {
-      const int j = part * (kMaxLength / 2) + u;
-      if (active && j < a.length) {
-        const float w = weights[(branch * kMaxLength + i) * kMaxLength + j];
-        const float* vrow = vs + (branch * a.length + j) * stride + d;
-        const float4 lo = *reinterpret_cast<const float4*>(vrow);
-        const float4 hi = *reinterpret_cast<const float4*>(vrow + 4);
-        o[0] += w * lo.x; o[1] += w * lo.y; o[2] += w * lo.z; o[3] += w * lo.w;
-        o[4] += w * hi.x; o[5] += w * hi.y; o[6] += w * hi.z; o[7] += w * hi.w;
-      }
-    }
-#pragma unroll
-    for (int x = 0; x < 8; ++x)
-      o[x] += __shfl_xor(o[x], 1, kWave);
-    if (active && part == 0) {
-#pragma unroll
-      for (int x = 0; x < 8; ++x)
-        o[x] *= inverse[r];
-      *reinterpret_cast<uint4*>(result + r * dims + d) = q8::PackBf16x8(o);
-    }
-  }
-  __syncthreads();
-  // The head's block [32][dims] in 16-byte chunks: thread -> (tile t,
-  // octet, row r16), rows past the pair as zeros.
-  for (int e = tid; e < 2 * octets * 16; e += kHeadThreads) {
-    const int r16 = e % 16;
-    const int octet = (e / 16) % octets;
-    const int row = 16 * (e / (16 * octets)) + r16;
-    const uint4 v = row < a.rows
-                        ? *reinterpret_cast<const uint4*>(result + row * dims + 8 * octet)
-                        : uint4{0U, 0U, 0U, 0U};
-    *reinterpret_cast<uint4*>(a.out + BfFragIndex(row, head * dims + 8 * octet)) = v;
-  }
-}
-
-template<int PW>
-__global__ __launch_bounds__(kHeadThreads) void QkvAttentionKernel(q8::TileArgs t, HeadArgs a) {
-  q8::EngineBody<2, 1, q8::ASource::kNormF32, q8::Output::kTileMajor, PW>(t);
-  __syncthreads();
-  extern __shared__ float lds[];
-  __shared__ int last[8];
-  const int tid = static_cast<int>(threadIdx.x);
-  const int group_heads = a.heads / a.kv_heads;
-  const int column = 16 * static_cast<int>(blockIdx.x);
-  int first_head, count;
-  if (column < a.q_width) {
-    first_head = column / a.head_dim;
-    count = 1;
-  } else {
-    first_head = (((column - a.q_width) / a.head_dim) % a.kv_heads) * group_heads;
-    count = group_heads;
-  }
-  const unsigned per_head = 3U * static_cast<unsigned>(a.head_dim / 16);
-  if (tid < count) {
-    unsigned* counter = a.arrivals + first_head + tid;
-    const unsigned before =
-        __hip_atomic_fetch_add(counter, 1U, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    const bool complete = before + 1U == per_head;
-    if (complete)
-      __hip_atomic_store(counter, 0U, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    last[tid] = complete ? 1 : 0;
-  }
-  __syncthreads();
-  for (int h = 0; h < count; ++h) {
-    if (last[h] == 0)
-      continue;
-    HeadAttention(a, first_head + h, lds);
-    __syncthreads();
   }
 }
 
@@ -731,44 +487,6 @@ void Qkv(const float* h, const Bf16* norm, const void* weight, float* qkv,
   else
     LaunchEngine<q8::ASource::kNormF32, q8::Output::kStore, 1, 2>(
         args, args.groups, kMaxWaves, stream);
-}
-
-bool FusesAttention(const Shape& s) {
-  return s.head_dim % 32 == 0 && s.head_dim <= 128 && s.heads / s.kv_heads <= 8 &&
-         s.hidden <= 64 * 2 * kMaxWaves;
-}
-
-void QkvAttention(const float* h, const Bf16* norm, const void* weight, const float* rope,
-                  float* qkv_tiles, unsigned* arrivals, Bf16* out, const Shape& s,
-                  hipStream_t stream) {
-  const int n = (s.heads + 2 * s.kv_heads) * s.head_dim;
-  q8::TileArgs args = BaseArgs(weight, s.rows, s.hidden, n);
-  args.h = h;
-  args.gamma = norm;
-  args.eps = s.eps;
-  args.y = qkv_tiles;
-  HeadArgs a{};
-  a.qkv = qkv_tiles;
-  a.rope = rope;
-  a.arrivals = arrivals;
-  a.out = out;
-  a.rows = s.rows;
-  a.length = s.length;
-  a.heads = s.heads;
-  a.kv_heads = s.kv_heads;
-  a.head_dim = s.head_dim;
-  a.q_width = s.heads * s.head_dim;
-  a.scale = 1.0F / std::sqrt(static_cast<float>(s.head_dim));
-  const int pw = args.pairs <= kMaxWaves ? 1 : 2;
-  const std::size_t engine =
-      q8::EngineShared(2, 1, kMaxWaves, q8::ASource::kNormF32, pw) +
-      q8::kTileBlockFloats * sizeof(float);
-  const std::size_t head = static_cast<std::size_t>(HeadFloats(s.head_dim)) * sizeof(float);
-  const std::size_t shared = std::max(engine, head);
-  if (pw == 1)
-    QkvAttentionKernel<1><<<args.groups, kHeadThreads, shared, stream>>>(args, a);
-  else
-    QkvAttentionKernel<2><<<args.groups, kHeadThreads, shared, stream>>>(args, a);
 }
 
 void Attention(const float* qkv, const float* rope, Bf16* out, const Shape& s,

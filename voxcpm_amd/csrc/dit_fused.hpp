@@ -46,19 +46,6 @@ void InAssemble(const float* x, const void* in_weight, const Bf16* in_bias,
 void Qkv(const float* h, const Bf16* norm, const void* weight, float* qkv,
          const Shape& s, hipStream_t stream);
 
-/// Whether QkvAttention takes this shape (head_dim a multiple of 32 up to
-/// 128, at most 8 query heads per kv head).
-bool FusesAttention(const Shape& s);
-
-/// Qkv and Attention in one launch: the qkv product written tile-major to
-/// `qkv_tiles` [(heads + 2 kv_heads) head_dim / 16][32][16], and each
-/// head's rotary embedding and attention run by the workgroup that
-/// completes the head (`arrivals` [heads], zero before the first launch and
-/// left zero by every launch); output as Attention's.
-void QkvAttention(const float* h, const Bf16* norm, const void* weight, const float* rope,
-                  float* qkv_tiles, unsigned* arrivals, Bf16* out, const Shape& s,
-                  hipStream_t stream);
-
 /// Rotary embedding and bidirectional attention within each branch from
 /// the qkv rows; output bf16 fragment order [32][heads head_dim].
 void Attention(const float* qkv, const float* rope, Bf16* out, const Shape& s,

@@ -27,12 +27,7 @@
 //  - kResidual: added into the float32 fragment-order residual stream;
 //  - kSwiGlu: RG = 2 with the up rows `group_stride` row groups after the
 //    gate rows; bf16(silu(gate) * up) in bf16 fragment order
-//    (kernels/generator_kernels.hip:243-254);
-//  - kTileMajor: float32 tile-major [groups][32][16] (2 KB per row group,
-//    rows m..31 zero) written as whole 16-byte chunks with device-scope
-//    stores that have completed when the engine body returns, so that
-//    another workgroup of the same launch may read them after an atomic
-//    handshake.
+//    (kernels/generator_kernels.hip:243-254).
 #ifndef VOXCPM_AMD_Q8_TILE_HPP_
 #define VOXCPM_AMD_Q8_TILE_HPP_
 
@@ -60,6 +55,9 @@ namespace vx::q8 {
 // Rows run to 32 (two 16-row tiles); columns to a multiple of 64.
 
 constexpr int kFragRows = 32;
+// Floats per wave of the norm prologue's row sums of squares (32 rows,
+// padded so that the two halves of the waves read disjoint banks).
+constexpr int kSquaresStride = 36;
 
 __host__ __device__ inline std::size_t BfFragIndex(int row, int column) {
   const int pair = column >> 6;
@@ -89,7 +87,7 @@ inline std::size_t FragElements(std::size_t columns) {
 }
 
 enum class ASource : int { kRowMajor = 0, kFragBf16 = 1, kNormF32 = 2 };
-enum class Output : int { kStore = 0, kResidual = 1, kSwiGlu = 2, kTileMajor = 3 };
+enum class Output : int { kStore = 0, kResidual = 1, kSwiGlu = 2 };
 
 struct TileArgs {
   const std::uint8_t* w;  // panels [groups][pairs] units
@@ -146,33 +144,8 @@ __host__ __device__ constexpr std::size_t EngineShared(int mt, int rg, int waves
     per_wave = static_cast<std::size_t>(StageFloats(mt, pw));
   std::size_t floats = static_cast<std::size_t>(waves) * per_wave;
   if (source == ASource::kNormF32)
-    floats += static_cast<std::size_t>(waves) * kFragRows;
+    floats += static_cast<std::size_t>(waves) * kSquaresStride;
   return floats * sizeof(float);
-}
-
-/// Floats of LDS the kTileMajor epilogue stages its 32 x 16 block in,
-/// after the engine's own region.
-constexpr int kTileBlockFloats = 32 * 16;
-
-/// Element (row, column) of a tile-major float32 matrix [groups][32][16].
-__host__ __device__ inline std::size_t TileIndex(int row, int column) {
-  return (static_cast<std::size_t>(column / 16) * 32 + row) * 16 + column % 16;
-}
-
-/// 16 bytes with one device-scope store (global_store_dwordx4 with sc1, the
-/// cache policy of a relaxed agent-scope atomic store): written through to
-/// memory, visible to every compute die once the store has completed.
-__device__ inline void StoreDevice16(void* p, const uint4& v) {
-  typedef unsigned U32x4 __attribute__((ext_vector_type(4)));
-  const U32x4 d{v.x, v.y, v.z, v.w};
-  asm volatile("global_store_dwordx4 %0, %1, off sc1" : : "v"(p), "v"(d) : "memory");
-}
-
-/// Every memory operation this wave issued has completed.
-__device__ inline void WaitMemory() {
-  __atomic_signal_fence(__ATOMIC_SEQ_CST);
-  __builtin_amdgcn_s_waitcnt(0);
-  __atomic_signal_fence(__ATOMIC_SEQ_CST);
 }
 
 __device__ inline float Silu(float value) {
@@ -225,7 +198,6 @@ __device__ __forceinline__ void EngineBody(const TileArgs& a) {
   static_assert(SRC != ASource::kNormF32 || MT == 2, "norm source is 32 rows");
   static_assert(OUT == Output::kStore || MT == 2, "fragment outputs are 32 rows");
   static_assert(OUT != Output::kSwiGlu || RG == 2, "SwiGLU pairs two groups");
-  static_assert(OUT != Output::kTileMajor || RG == 1, "tile-major blocks are one group");
   extern __shared__ float lds[];
   const int lane = threadIdx.x % kWave;
   const int wave = threadIdx.x / kWave;
@@ -379,9 +351,6 @@ __device__ __forceinline__ void EngineBody(const TileArgs& a) {
   };
 
   float* reduce = lds;
-  // kTileMajor: the output block, after the engine's region.
-  float* block = lds + EngineShared(MT, RG, waves, SRC, PW) / sizeof(float);
-  (void)block;
   if constexpr (SRC == ASource::kNormF32) {
     // Every pair in this pass: wave w owns pairs w, w + waves, ...
     float* squares = lds + static_cast<std::size_t>(waves) * RG * MT * 256;
@@ -435,18 +404,24 @@ __device__ __forceinline__ void EngineBody(const TileArgs& a) {
       partial[t] += __shfl_xor(partial[t], 32, kWave);
     }
     if (octet == 0) {
-      squares[wave * kFragRows + r16] = partial[0];
-      squares[wave * kFragRows + 16 + r16] = partial[1];
+      squares[wave * kSquaresStride + r16] = partial[0];
+      squares[wave * kSquaresStride + 16 + r16] = partial[1];
     }
     __syncthreads();
-    float inverse[2];
+    // Lane l adds row l % 32 over one half of the waves (the halves' reads
+    // fall on different banks), the halves meet by one shuffle, and every
+    // lane takes its two rows' inverses from the lanes that hold them.
+    constexpr int kHalf = waves / 2;
+    const int first = (lane / 32) * kHalf;
+    float total = 0.0F;
 #pragma unroll
-    for (int t = 0; t < 2; ++t) {
-      float total = 0.0F;
-      for (int w = 0; w < waves; ++w)
-        total += squares[w * kFragRows + 16 * t + r16];
-      inverse[t] = rsqrtf(total / static_cast<float>(a.k) + a.eps);
-    }
+    for (int w = 0; w < kHalf; ++w)
+      total += squares[(first + w) * kSquaresStride + lane % 32];
+    total += __shfl_xor(total, 32, kWave);
+    const float row_inverse = rsqrtf(total / static_cast<float>(a.k) + a.eps);
+    float inverse[2];
+    inverse[0] = __shfl(row_inverse, r16, kWave);
+    inverse[1] = __shfl(row_inverse, 16 + r16, kWave);
 #pragma unroll
     for (int p = 0; p < PW; ++p) {
       const int pair = wave + p * waves;
@@ -566,26 +541,10 @@ __device__ __forceinline__ void EngineBody(const TileArgs& a) {
         a.y_bf16[at] = Bf16Fast(v);
     } else if constexpr (OUT == Output::kResidual) {
       a.residual[F32FragIndex(row, column)] = before[u] + v;
-    } else if constexpr (OUT == Output::kSwiGlu) {
+    } else {
       const float up = total_of(e + MT * 256);
       a.frag_out[BfFragIndex(row, column)] = Bf16Fast(Silu(v) * up);
-    } else {
-      block[row * 16 + column % 16] = v;
     }
-  }
-  if constexpr (OUT == Output::kTileMajor) {
-    // The 32 x 16 block (rows past m zero) in whole 16-byte chunks: thread
-    // (row, quad) -> 16 contiguous bytes of row `row` of the group's 2 KB.
-    __syncthreads();
-    if (threadIdx.x < 128) {
-      const int row = static_cast<int>(threadIdx.x) / 4;
-      const int quad = static_cast<int>(threadIdx.x) % 4;
-      const float4 v = row < a.m ? *reinterpret_cast<const float4*>(block + row * 16 + 4 * quad)
-                                 : float4{0.0F, 0.0F, 0.0F, 0.0F};
-      StoreDevice16(a.y + (static_cast<std::size_t>(tile) * 32 + row) * 16 + 4 * quad,
-                    __builtin_bit_cast(uint4, v));
-    }
-    WaitMemory();
   }
 }
 
