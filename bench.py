@@ -39,8 +39,8 @@ BF16_PEAK_TFLOPS = 2500.0
 # reading of a 256 MiB copy of known size) + WRITE_SIZE KiB (scale 1.0).
 # Measured, not computed: re-measure when the product kernel changes.
 FETCH_SCALE = 262144 / 131083.5
-TRAFFIC_KIB = {(1024, 3072): (1835.5, 264.0), (1024, 8192): (4562.0, 704.0),
-               (2048, 2048): (2555.5, 176.0), (2048, 16384): (17799.0, 1408.0)}
+TRAFFIC_KIB = {(1024, 3072): (1832.5, 264.0), (1024, 8192): (4558.5, 704.0),
+               (2048, 2048): (2552.5, 176.0), (2048, 16384): (17806.5, 1408.0)}
 PREFILL_M = [129, 256, 512, 1024]
 PREFILL_N = [2048, 6144, 16384]
 PREFILL_K = 2048
@@ -157,6 +157,21 @@ def gpu_products(args, torch, ops, synth, device, stream):
     for row in sweep:
         if row["m"] == ROWS:
             log(f"  M=22 K={row['k']} N={row['n']}: {row['us']} us, {row['gbs']} GB/s")
+    # The per-launch read ceiling: each shape's bytes, rotated and replayed
+    # from a HIP graph the same way, read once with no arithmetic
+    # (vx_stream_read): what one launch of that size can reach on this GPU.
+    sink = torch.zeros(1, dtype=torch.int32, device=device)
+    ceiling = []
+    for p in products:
+        count = max(p.copies, 64)
+        g = graph_of(torch, stream,
+                     lambda i, p=p: ops.stream_read(p.pool[i % p.copies], sink), count)
+        g.replay()
+        us = time_graph(torch, stream, g) / count * 1e6
+        ceiling.append({"k": p.k, "n": p.n, "us": round(us, 3),
+                        "gbs": round(p.bytes / us / 1e3, 1)})
+        log(f"  read ceiling K={p.k} N={p.n}: {us:.3f} us, {p.bytes / us / 1e3:.1f} GB/s")
+        del g
     launches = 4 * args.steps
     result = {
         "value": value,
@@ -165,6 +180,7 @@ def gpu_products(args, torch, ops, synth, device, stream):
         "launch_bytes": step_bytes / 4,
         "launch_us": seconds / launches * 1e6,
         "sweep": sweep,
+        "ceiling": ceiling,
     }
     del products
     torch.cuda.empty_cache()
@@ -400,6 +416,7 @@ def main() -> int:
             patch["cpu"] = cpu_patch(synth)
 
     value = products["value"]
+    ceiling_gbs = products["step_bytes"] / sum(c["us"] for c in products["ceiling"]) / 1e3
     line = {
         "metric": METRIC,
         "value": round(value, 1),
@@ -430,9 +447,16 @@ def main() -> int:
                           / HBM_PEAK_GBS, 4),
             "traffic": round(sum(f * FETCH_SCALE + w for f, w in TRAFFIC_KIB.values())
                              * 1024 / len(TRAFFIC_KIB)),
-            "kernel": "EngineKernel (voxcpm_amd/csrc/q8_tile.hpp) via vx_q8_linear",
+            "kernel": "EngineKernel<2, RG, kRowMajor, kStore, 1, 3> "
+                      "(voxcpm_amd/csrc/q8_tile.hpp) via vx_q8_linear",
             "launch_bytes": products["launch_bytes"],
             "launch_us": round(products["launch_us"], 3),
+            # The same bytes per launch read with no arithmetic, launched the
+            # same way: the achievable per-launch ceiling (launch and memory
+            # latency included) against which `value` is also quoted.
+            "read_ceiling_gbs": round(ceiling_gbs, 1),
+            "frac_of_read_ceiling": round(value / ceiling_gbs, 4),
+            "read_ceiling": products["ceiling"],
         },
         "cpu_baseline": baseline,
         "read_probe_gbs": round(probe, 1),

@@ -38,6 +38,16 @@ int vx_q8_plan(size_t m, size_t k, size_t n, vx_scratch* scratch,
 int vx_test_pack_bf16(const float* input, uint16_t* output, size_t n,
                       void* stream);
 
+/* Reads `bytes` (a multiple of 16) at `data` once with coalesced 16-byte
+ * loads, one load per thread, and writes nothing unless the data's XOR is
+ * `never` (then `sink` [1] receives it). The achievable per-launch ceiling
+ * beside the products: the same bytes, launched and rotated the same way,
+ * with no arithmetic. Counterpart of ReadProbe
+ * (kernels/skinny_gemm.hip:340-358), the reference benchmark's plain-read
+ * reference. */
+int vx_stream_read(const void* data, size_t bytes, uint32_t never,
+                   uint32_t* sink, void* stream);
+
 /* The DiT evaluation paths. AUTO (the default) takes FUSED where the shape
  * allows (five launches per layer on fragment-order activations), else
  * UNFUSED (the reference's launch sequence of transformer.cpp:55-100:

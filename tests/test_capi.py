@@ -59,6 +59,9 @@ def test_argument_validation_without_gpu():
     handle = ctypes.c_void_p()
     assert L.vx_scratch_create(ctypes.byref(handle), 0, 4096) == VX_BAD_ARG
     assert L.vx_dit_create(None, None, None) == VX_BAD_ARG
+    assert L.vx_stream_read(None, 64, 0, dummy, None) == VX_BAD_ARG
+    assert L.vx_stream_read(dummy, 24, 0, dummy, None) == VX_BAD_ARG
+    assert L.vx_stream_read(unaligned, 32, 0, dummy, None) == VX_BAD_ARG
 
 
 def test_dit_create_rejects_bad_shapes():

@@ -258,3 +258,23 @@ def test_prefill_expansion(vx, oracle, cuda, stream, rows, k, n):
                         before if accumulate else None, None, None, cuda)
         worst = expanded_check(y, x, blocks, oracle, before if accumulate else None)
         assert worst <= 1e-4, f"worst {worst:.3e}"
+
+
+def test_stream_read_reads_every_byte(vx, cuda, stream):
+    """The read-ceiling kernel loads every 16-byte chunk: the XOR of the
+    buffer's words reaches the sink only when it equals `never`."""
+    words = np.arange(1, 4096 * 4 + 1, dtype=np.uint32) * np.uint32(2654435761)
+    data = torch.from_numpy(words.view(np.int32)).to(cuda)
+    chunk_xor = np.bitwise_xor.reduce(words.reshape(-1, 4), axis=1)
+    sink = torch.zeros(1, dtype=torch.int32, device=cuda)
+    # `never` equal to one chunk's XOR: exactly that chunk writes it.
+    target = int(chunk_xor[1234])
+    vx.stream_read(data, sink, never=target)
+    torch.cuda.synchronize()
+    assert int(sink.cpu().numpy().view(np.uint32)[0]) == target
+    sink.zero_()
+    missing = int(np.uint32(0xFFFFFFFF))
+    assert missing not in set(chunk_xor.tolist())
+    vx.stream_read(data, sink, never=missing)
+    torch.cuda.synchronize()
+    assert int(sink.cpu().numpy()[0]) == 0

@@ -60,6 +60,22 @@ __global__ void PackBf16Kernel(const float* input, std::uint32_t* output,
     output[i] = vx::q8::PackBf16x2(input[2 * i], input[2 * i + 1]);
 }
 
+// One 16-byte load per thread of `chunks` chunks; the XOR of the loaded
+// words is stored only when it equals `never`, so the loads stay live and
+// nothing is written.
+__global__ __launch_bounds__(256) void StreamReadKernel(const uint4* data,
+                                                        std::size_t chunks,
+                                                        std::uint32_t never,
+                                                        std::uint32_t* sink) {
+  const std::size_t i = static_cast<std::size_t>(blockIdx.x) * 256 + threadIdx.x;
+  if (i >= chunks)
+    return;
+  const uint4 v = data[i];
+  const std::uint32_t x = v.x ^ v.y ^ v.z ^ v.w;
+  if (x == never)
+    sink[0] = x;
+}
+
 bool Aligned(const void* pointer, std::size_t bytes) {
   return reinterpret_cast<std::uintptr_t>(pointer) % bytes == 0;
 }
@@ -186,6 +202,19 @@ int vx_test_pack_bf16(const float* input, uint16_t* output, size_t n,
                    vx::Stream(stream)>>>(
       input, reinterpret_cast<std::uint32_t*>(output), pairs);
   return vx::LaunchStatus("vx_test_pack_bf16");
+}
+
+int vx_stream_read(const void* data, size_t bytes, uint32_t never,
+                   uint32_t* sink, void* stream) {
+  if (data == nullptr || sink == nullptr || bytes % 16 != 0 || !Aligned(data, 16))
+    return vx::Fail(VX_BAD_ARG, "vx_stream_read: bad arguments");
+  if (bytes == 0)
+    return vx::Succeed();
+  const std::size_t chunks = bytes / 16;
+  StreamReadKernel<<<static_cast<unsigned>((chunks + 255) / 256), 256, 0,
+                     vx::Stream(stream)>>>(static_cast<const uint4*>(data), chunks, never,
+                                            sink);
+  return vx::LaunchStatus("vx_stream_read");
 }
 
 /* The plan vx_q8_linear would use: {mt, rg, waves, tiles, splits,

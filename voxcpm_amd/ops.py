@@ -16,7 +16,7 @@ from ._lib import DitLayer, DitProjection, DitShape, DitWeights, check, lib
 
 __all__ = [
     "Scratch", "Dit", "q8_pack", "q8_unpack_blocks", "q8_unpack_bf16",
-    "q8_linear", "q8_linear_bf16", "q8_plan", "euler_schedule", "rope_table",
+    "q8_linear", "q8_linear_bf16", "q8_plan", "stream_read", "euler_schedule", "rope_table",
 ]
 
 
@@ -112,6 +112,14 @@ def q8_linear_bf16(x: torch.Tensor, packed: torch.Tensor, n: int,
     check(lib().vx_q8_linear_bf16(_ptr(x), _ptr(packed), _ptr(y), m, k, n,
                                   handle, _stream(stream)))
     return y
+
+
+def stream_read(data: torch.Tensor, sink: torch.Tensor, never: int = 0x9E3779B9,
+                stream=None) -> None:
+    """One coalesced read of `data`'s bytes (the per-launch read ceiling);
+    `sink` (int32 [1]) changes only if the bytes' XOR equals `never`."""
+    check(lib().vx_stream_read(_ptr(data), data.numel() * data.element_size(), never,
+                               _ptr(sink), _stream(stream)))
 
 
 def q8_plan(m: int, k: int, n: int, scratch: Scratch | None = None) -> dict:
