@@ -193,6 +193,9 @@ def gpu_prefill(args, torch, ops, synth, device, stream):
     rotating weight copies."""
     rows = []
     k = PREFILL_K
+    # The product scratch (as the reference's Bf16Gemm owns its workspace):
+    # small grids split k into its partial-sum area.
+    scratch = ops.Scratch(128, 16384)
     for n in PREFILL_N:
         rng = synth.Rng(7, n)
         blocks = torch.from_numpy(synth.q8_blocks(rng, n, k)).to(device)
@@ -204,9 +207,10 @@ def gpu_prefill(args, torch, ops, synth, device, stream):
             x = torch.from_numpy(synth.activations(rng, m, k).view(np.int16)).to(
                 device).view(torch.bfloat16)
             y = torch.empty((m, n), dtype=torch.float32, device=device)
-            ops.q8_linear(x, pool[0], n, y=y)
+            ops.q8_linear(x, pool[0], n, y=y, scratch=scratch)
             count = 20
-            g = graph_of(torch, stream, lambda i: ops.q8_linear(x, pool[i % copies], n, y=y),
+            g = graph_of(torch, stream,
+                         lambda i: ops.q8_linear(x, pool[i % copies], n, y=y, scratch=scratch),
                          count)
             g.replay()
             seconds = time_graph(torch, stream, g) / count

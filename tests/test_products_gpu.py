@@ -244,7 +244,10 @@ def expanded_check(y, x, blocks, oracle, before=None):
                                       (300, 1024, 2560), (512, 2048, 2048),
                                       (1024, 2048, 1040),
                                       # 128-row tiles, ragged rows and columns
-                                      (700, 1024, 4112)])
+                                      (700, 1024, 4112),
+                                      # columns not a multiple of 4 (the split
+                                      # reduction's scalar path)
+                                      (200, 512, 1042)])
 def test_prefill_expansion(vx, oracle, cuda, stream, rows, k, n):
     """More than 128 rows: W as bf16(scale * q), float32 sums; the
     reference allows 1e-4 there (products_test.cpp:301-309)."""
@@ -253,11 +256,20 @@ def test_prefill_expansion(vx, oracle, cuda, stream, rows, k, n):
     packed = vx.q8_pack(to_device(blocks, cuda), n, k)
     x = synth.activations(rng, rows, k)
     before = rng.normal(rows * n).astype(np.float32).reshape(rows, n)
-    for accumulate in (False, True):
-        y = run_product(vx, to_device(x, cuda), packed, n,
-                        before if accumulate else None, None, None, cuda)
-        worst = expanded_check(y, x, blocks, oracle, before if accumulate else None)
-        assert worst <= 1e-4, f"worst {worst:.3e}"
+    # Without a scratch one pass over k; with one, small grids split k over
+    # workgroups and add the splits in order in a second launch.
+    scratch = vx.Scratch(128, max(n, 4096))
+    results = []
+    for use_scratch in (None, scratch):
+        for accumulate in (False, True):
+            y = run_product(vx, to_device(x, cuda), packed, n,
+                            before if accumulate else None, None, use_scratch, cuda)
+            worst = expanded_check(y, x, blocks, oracle, before if accumulate else None)
+            assert worst <= 1e-4, f"scratch {use_scratch is not None}: worst {worst:.3e}"
+            results.append(y)
+    # A split product repeats bit for bit.
+    again = run_product(vx, to_device(x, cuda), packed, n, None, None, scratch, cuda)
+    assert np.array_equal(again, results[2])
 
 
 def test_stream_read_reads_every_byte(vx, cuda, stream):

@@ -102,6 +102,8 @@ int Product(const uint16_t* x, const void* packed, float* y, uint16_t* y_bf16,
             int rg, int waves, int splits, void* stream) {
   if (m > vx::kExactRows)
     return vx::RunTiled(x, packed, y, y_bf16, m, k, n, accumulate != 0, false,
+                        scratch != nullptr ? scratch->partials : nullptr,
+                        scratch != nullptr ? scratch->partial_floats : 0,
                         vx::Stream(stream));
   const vx::ProductPlan plan = vx::PlanSkinny(
       m, k, n, scratch != nullptr ? scratch->partial_floats : 0,

@@ -53,10 +53,12 @@ int RunSkinny(const Bf16* x, const void* w, float* y, Bf16* y_bf16,
 
 /// Launches the LDS-tiled product (q8_tiled.hip; meant for m > 32): the
 /// exact per-block arithmetic, or with `exact` false the expansion to
-/// bf16(scale * q) of products of more than 128 rows.
+/// bf16(scale * q) of products of more than 128 rows. Small grids split k
+/// over workgroups when `partials` holds partial_floats >= 2 m n floats
+/// (a second launch adds the splits in order).
 int RunTiled(const Bf16* x, const void* w, float* y, Bf16* y_bf16, std::size_t m,
              std::size_t k, std::size_t n, bool accumulate, bool exact,
-             hipStream_t stream);
+             float* partials, std::size_t partial_floats, hipStream_t stream);
 
 }  // namespace vx
 

@@ -457,8 +457,8 @@ int RunSkinny(const Bf16* x, const void* w, float* y, Bf16* y_bf16,
               std::size_t m, std::size_t k, std::size_t n, bool accumulate,
               const ProductPlan& plan, float* partials, unsigned* counters,
               hipStream_t stream) {
-  if (plan.tiled)
-    return RunTiled(x, w, y, y_bf16, m, k, n, accumulate, true, stream);
+  if (plan.tiled)  // at least 256 tiles by the plan: no split over k
+    return RunTiled(x, w, y, y_bf16, m, k, n, accumulate, true, nullptr, 0, stream);
   if (plan.engine) {
     const EngineLauncher launch = PickEngine(plan.mt, plan.rg, static_cast<int>(m));
     if (launch == nullptr)

@@ -55,6 +55,11 @@ struct TiledArgs {
   int pairs, groups;
   int m_tiles, n_tiles;
   int accumulate;
+  // Split over k (splits > 1): workgroup tile t of split s takes pairs
+  // [s pairs_per_split, ...) and stores its float32 sums to
+  // partials [splits][m][n]; ReduceSplitsKernel adds them in split order.
+  int splits, pairs_per_split;
+  float* partials;
 };
 
 /// 8 int8 values (two little-endian dwords) times `scale`, each rounded to
@@ -109,16 +114,22 @@ __global__ __launch_bounds__(T::kThreads, T::kMinBlocks) void TiledKernel(TiledA
   const int wave = tid / kWave;
   const int r16 = lane % 16;
   const int octet = lane / 16;
-  const int logical = DieOrdered(static_cast<int>(blockIdx.x), a.m_tiles * a.n_tiles);
-  const int row0 = (logical % a.m_tiles) * BM;
-  const int group0 = (logical / a.m_tiles) * (kTileN / 16);
+  const int tiles = a.m_tiles * a.n_tiles;
+  const int logical = DieOrdered(static_cast<int>(blockIdx.x), tiles * a.splits);
+  const int split = logical / tiles;
+  const int tile = logical % tiles;
+  const int row0 = (tile % a.m_tiles) * BM;
+  const int group0 = (tile / a.m_tiles) * (kTileN / 16);
+  const int first_pair = split * a.pairs_per_split;
+  const int steps = min(a.pairs, first_pair + a.pairs_per_split) - first_pair;
 
   struct Staging {
     uint4 x[kAPieces];
     uint4 w[kUnits];
     std::uint32_t scales[kUnits];
   };
-  const auto fetch = [&](int pair, Staging& s) {
+  const auto fetch = [&](int step, Staging& s) {
+    const int pair = first_pair + step;
 #pragma unroll
     for (int i = 0; i < kAPieces; ++i) {
       const int piece = tid + kThreads * i;
@@ -217,20 +228,21 @@ __global__ __launch_bounds__(T::kThreads, T::kMinBlocks) void TiledKernel(TiledA
   Staging staged[D];
 #pragma unroll
   for (int d = 0; d < D; ++d)
-    if (d < a.pairs)
+    if (d < steps)
       fetch(d, staged[d]);
-  store(0, staged[0]);
+  if (steps > 0)
+    store(0, staged[0]);
   __syncthreads();
-  for (int p = 0; p < a.pairs; p += U) {
+  for (int p = 0; p < steps; p += U) {
 #pragma unroll
     for (int d = 0; d < U; ++d) {
       const int q = p + d;
-      if (q >= a.pairs)
+      if (q >= steps)
         break;
-      if (q + D < a.pairs)
+      if (q + D < steps)
         fetch(q + D, staged[d % D]);
       compute(d % 2);
-      if (q + 1 < a.pairs)
+      if (q + 1 < steps)
         store((d + 1) % 2, staged[(d + 1) % D]);
       __syncthreads();
     }
@@ -250,7 +262,9 @@ __global__ __launch_bounds__(T::kThreads, T::kMinBlocks) void TiledKernel(TiledA
         if (row >= a.m)
           continue;
         const std::size_t at = static_cast<std::size_t>(row) * a.n + column;
-        if (a.y_bf16 != nullptr)
+        if (a.splits > 1)
+          a.partials[static_cast<std::size_t>(split) * a.m * a.n + at] = acc[i][j][e];
+        else if (a.y_bf16 != nullptr)
           a.y_bf16[at] = q8::Bf16Fast(acc[i][j][e]);
         else
           a.y[at] = a.accumulate ? a.y[at] + acc[i][j][e] : acc[i][j][e];
@@ -258,9 +272,50 @@ __global__ __launch_bounds__(T::kThreads, T::kMinBlocks) void TiledKernel(TiledA
   }
 }
 
+/// y (+)= the splits' partial sums added in split order, or their bf16
+/// rounding; four consecutive elements per thread (n % 4 == 0), else one.
+__global__ __launch_bounds__(256) void ReduceSplitsKernel(TiledArgs a) {
+  const std::size_t count = static_cast<std::size_t>(a.m) * a.n;
+  const std::size_t plane = count;
+  const std::size_t first =
+      (static_cast<std::size_t>(blockIdx.x) * 256 + threadIdx.x) * 4;
+  if (first >= count)
+    return;
+  const int width = a.n % 4 == 0 ? 4 : 1;
+  for (int v = 0; v < 4; v += width) {
+    const std::size_t at = first + v;
+    if (at >= count)
+      break;
+    float sum[4] = {0.0F, 0.0F, 0.0F, 0.0F};
+    for (int s = 0; s < a.splits; ++s) {
+      const float* part = a.partials + s * plane + at;
+      if (width == 4) {
+        const float4 p = *reinterpret_cast<const float4*>(part);
+        sum[0] += p.x;
+        sum[1] += p.y;
+        sum[2] += p.z;
+        sum[3] += p.w;
+      } else {
+        sum[0] += part[0];
+      }
+    }
+    for (int e = 0; e < width; ++e) {
+      if (a.y_bf16 != nullptr)
+        a.y_bf16[at + e] = q8::Bf16Fast(sum[e]);
+      else
+        a.y[at + e] = a.accumulate ? a.y[at + e] + sum[e] : sum[e];
+    }
+  }
+}
+
 template<class T, bool EXACT>
 void Launch(const TiledArgs& args, hipStream_t stream) {
-  TiledKernel<T, EXACT><<<args.m_tiles * args.n_tiles, T::kThreads, 0, stream>>>(args);
+  TiledKernel<T, EXACT>
+      <<<args.m_tiles * args.n_tiles * args.splits, T::kThreads, 0, stream>>>(args);
+  if (args.splits > 1) {
+    const std::size_t quads = (static_cast<std::size_t>(args.m) * args.n + 3) / 4;
+    ReduceSplitsKernel<<<static_cast<unsigned>((quads + 255) / 256), 256, 0, stream>>>(args);
+  }
 }
 
 using Small = TileShape<64, 2, 2, 2>;
@@ -270,7 +325,7 @@ using Large = TileShape<128, 4, 2, 1>;
 
 int RunTiled(const Bf16* x, const void* w, float* y, Bf16* y_bf16, std::size_t m,
              std::size_t k, std::size_t n, bool accumulate, bool exact,
-             hipStream_t stream) {
+             float* partials, std::size_t partial_floats, hipStream_t stream) {
   TiledArgs args;
   args.x = x;
   args.w = static_cast<const std::uint8_t*>(w);
@@ -289,6 +344,17 @@ int RunTiled(const Bf16* x, const void* w, float* y, Bf16* y_bf16, std::size_t m
   const std::size_t tiles128 = (m + 127) / 128 * static_cast<std::size_t>(args.n_tiles);
   const int bm = m > 64 && tiles128 >= 192 ? 128 : 64;
   args.m_tiles = static_cast<int>((m + bm - 1) / bm);
+  // Grids of at most 144 tiles split k (powers of two, at least four
+  // steps each, up to 384 workgroups) when the scratch holds the partial
+  // sums: measured faster on MI355X there, slower on larger grids, where
+  // the second launch costs more than the parallelism gains.
+  args.splits = 1;
+  const std::size_t tiles = static_cast<std::size_t>(args.m_tiles) * args.n_tiles;
+  while (tiles <= 144 && tiles * 2 * args.splits <= 384 && args.pairs >= 8 * args.splits &&
+         2 * args.splits * m * n <= partial_floats)
+    args.splits *= 2;
+  args.pairs_per_split = (args.pairs + args.splits - 1) / args.splits;
+  args.partials = partials;
   if (bm == 64) {
     if (exact)
       Launch<Small, true>(args, stream);
