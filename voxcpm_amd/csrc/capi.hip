@@ -88,7 +88,8 @@ int CheckProduct(const void* x, const void* w, const void* y, std::size_t m,
     return vx::Fail(VX_BAD_ARG, std::string(what) +
                                     ": m, n must be positive and k a positive "
                                     "multiple of 32");
-  if (m > (1U << 24) || n > (1U << 24) || k > (1U << 24))
+  // Activation offsets of the skinny kernels are 32-bit byte offsets.
+  if (m > (1U << 24) || n > (1U << 24) || k > (1U << 22))
     return vx::Fail(VX_BAD_ARG, std::string(what) + ": shape too large");
   if (!Aligned(x, 16) || !Aligned(w, 16))
     return vx::Fail(VX_BAD_ARG,

@@ -441,7 +441,22 @@ q8::TileArgs BaseArgs(const void* weight, int m, int k, int n) {
   args.pairs = PairsOf(k);
   args.groups = (n + 15) / 16;
   args.group_stride = 1;
+  args.row_blocks = 1;
+  args.rows_per_block = m;
   return args;
+}
+
+/// Row blocks of a launch of `tiles` tiles over `rows` rows: up to 4 while
+/// the grid stays within one workgroup per compute unit (256) and blocks
+/// keep at least 5 rows; tiles a multiple of 8 keep a tile's blocks on one
+/// compute die.
+void SetRowBlocks(q8::TileArgs& args, int tiles, int rows, int max_blocks = 4) {
+  int blocks = 1;
+  while (tiles % 8 == 0 && blocks < max_blocks && tiles * 2 * blocks <= 256 &&
+         (rows + 2 * blocks - 1) / (2 * blocks) >= 5)
+    blocks *= 2;
+  args.row_blocks = blocks;
+  args.rows_per_block = (rows + blocks - 1) / blocks;
 }
 
 }  // namespace
@@ -513,12 +528,16 @@ void Residual(const Bf16* act, const void* weight, int k, int n, float* h,
   q8::TileArgs args = BaseArgs(weight, s.rows, k, n);
   args.x = act;
   args.residual = h;
+  // o and down have few output groups (hidden / 16): row blocks spread
+  // them over the compute units, each loading only its rows' activations.
+  SetRowBlocks(args, args.groups, s.rows);
+  const int grid = args.groups * args.row_blocks;
   if (args.pairs > 2 * kMaxWaves)  // four or more pairs per wave: two per pass
     LaunchEngine<q8::ASource::kFragBf16, q8::Output::kResidual, 1, 2>(
-        args, args.groups, kMaxWaves, stream);
+        args, grid, kMaxWaves, stream);
   else
     LaunchEngine<q8::ASource::kFragBf16, q8::Output::kResidual, 1, 1>(
-        args, args.groups, kMaxWaves, stream);
+        args, grid, kMaxWaves, stream);
 }
 
 void GateUp(const float* h, const Bf16* norm, const void* weight, Bf16* out,

@@ -31,6 +31,7 @@ struct ProductPlan {
   int splits = 1;
   int pairs_per_split = 0;
   int pairs_per_wave = 0;
+  int row_blocks = 1;  // engine plans: activation-row blocks per tile
 };
 
 /// Largest row-group count per workgroup the kernels have for `mt` tiles.

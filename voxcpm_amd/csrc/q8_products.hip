@@ -386,6 +386,13 @@ ProductPlan PlanEngine(std::size_t m, std::size_t k, std::size_t n) {
   plan.rg = rg;
   plan.tiles = (groups + rg - 1) / rg;
   plan.waves = q8::EngineThreads(plan.mt, rg) / kWave;  // idle waves add zeros
+  // Few tiles: row blocks (each workgroup loads its rows' activations only)
+  // fill the compute units; tiles a multiple of 8 keep a tile's blocks on
+  // one compute die. Measured on MI355X for the (2048, 2048) M=22 shape.
+  plan.row_blocks = 1;
+  while (plan.tiles % 8 == 0 && plan.row_blocks < 4 && plan.tiles * 2 * plan.row_blocks <= 256 &&
+         static_cast<int>(m) >= 10 * plan.row_blocks)
+    plan.row_blocks *= 2;
   plan.splits = 1;
   plan.pairs_per_split = pairs;
   plan.pairs_per_wave = (pairs + plan.waves - 1) / plan.waves;
@@ -471,11 +478,13 @@ int RunSkinny(const Bf16* x, const void* w, float* y, Bf16* y_bf16,
     args.pairs = static_cast<int>(q8::Pairs(k));
     args.groups = static_cast<int>(q8::Groups(n));
     args.group_stride = 1;
+    args.row_blocks = plan.row_blocks;
+    args.rows_per_block = static_cast<int>((m + plan.row_blocks - 1) / plan.row_blocks);
     args.x = x;
     args.y = y_bf16 != nullptr ? nullptr : y;
     args.y_bf16 = y_bf16;
     args.accumulate = accumulate ? 1 : 0;
-    launch(args, plan.tiles, plan.waves, stream);
+    launch(args, plan.tiles * plan.row_blocks, plan.waves, stream);
     return LaunchStatus("q8 product");
   }
   const Launcher launch = PickLauncher(plan.mt, plan.rg);

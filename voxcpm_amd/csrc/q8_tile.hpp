@@ -97,6 +97,14 @@ struct TileArgs {
   int pairs;              // Pairs(k)
   int groups;             // Groups(n)
   int group_stride;       // row group r of tile b: RgGroup(b, r, stride)
+  // Row blocks (>= 1): the grid is row_blocks x the tiles; workgroup
+  // b = tile + tiles * block takes activation rows
+  // [block rows_per_block, + rows_per_block) of the tile, so that a launch
+  // of few tiles fills the compute units and each loads only its rows.
+  // The blocks of a tile lie a multiple of 8 workgroups apart (tiles a
+  // multiple of 8), on one compute die, whose L2 serves their weights.
+  int row_blocks;
+  int rows_per_block;
   // activations
   const Bf16* x;          // kRowMajor [m][k] / kFragBf16
   const float* h;         // kNormF32: float32 fragment order [32][k]
@@ -180,6 +188,27 @@ __device__ inline float Bf16Hi(std::uint32_t word) {
   return __uint_as_float(word & 0xFFFF0000U);
 }
 
+// Activation loads go through buffer resources: a lane whose value is
+// masked (a row outside the block, a pair past k) loads at an offset past
+// the buffer's range, which returns zero without a memory access. A load
+// guarded by a per-lane condition would instead be a divergent branch
+// whose zero-filling side writes the same registers, which makes the
+// compiler wait for each load before the next: a wave's loads would
+// arrive one round trip after another instead of together.
+__device__ inline __amdgpu_buffer_rsrc_t BufferOf(const void* base, std::uint32_t bytes) {
+  // Raw buffer, 32-bit data format (the gfx9 family's word 3).
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0,
+                                           static_cast<int>(bytes), 0x00020000);
+}
+constexpr std::uint32_t kPastBuffer = 0x7FFFFFF0U;
+/// 16 bytes at `offset` of the buffer, or zero (no access) unless `keep`.
+__device__ inline uint4 BufferLoad16(__amdgpu_buffer_rsrc_t buffer, std::uint32_t offset,
+                                     bool keep) {
+  return __builtin_bit_cast(
+      uint4, __builtin_amdgcn_raw_buffer_load_b128(
+                 buffer, static_cast<int>(keep ? offset : kPastBuffer), 0, 0));
+}
+
 /// One pair's operands in flight: RG weight fragments with their scale
 /// pairs, and the MT x 2 activation fragments.
 template<int MT, int RG>
@@ -204,7 +233,11 @@ __device__ __forceinline__ void EngineBody(const TileArgs& a) {
   constexpr int waves = EngineThreads(MT, RG) / kWave;
   const int r16 = lane % 16;
   const int octet = lane / 16;
-  const int tile = static_cast<int>(blockIdx.x);
+  const int tiles = static_cast<int>(gridDim.x) / a.row_blocks;
+  const int tile = static_cast<int>(blockIdx.x) % tiles;
+  const int row_lo = (static_cast<int>(blockIdx.x) / tiles) * a.rows_per_block;
+  const int row_hi = min(a.m, row_lo + a.rows_per_block);
+  const auto in_rows = [&](int row) { return row >= row_lo && row < row_hi; };
   const int k_blocks = a.k / 32;
 
   const std::uint8_t* unit[RG];
@@ -216,7 +249,15 @@ __device__ __forceinline__ void EngineBody(const TileArgs& a) {
   bool row_ok[MT];
 #pragma unroll
   for (int t = 0; t < MT; ++t)
-    row_ok[t] = 16 * t + r16 < a.m;
+    row_ok[t] = in_rows(16 * t + r16);
+  // The activations as buffers: row-major [m][k] bf16, fragment-order bf16
+  // (32 rows x pairs x 64 columns) or fragment-order float32.
+  const __amdgpu_buffer_rsrc_t x_buffer = BufferOf(
+      a.x, SRC == ASource::kRowMajor
+               ? 2U * static_cast<std::uint32_t>(a.m) * static_cast<std::uint32_t>(a.k)
+               : 4096U * static_cast<std::uint32_t>(a.pairs));
+  const __amdgpu_buffer_rsrc_t h_buffer =
+      BufferOf(a.h, 8192U * static_cast<std::uint32_t>(a.pairs));
 
   // Output element e of the tile (thread e, e + threads, ...): fragment
   // f = r MT + t, accumulator i, lane l -> (row, column); false past m / n.
@@ -231,7 +272,7 @@ __device__ __forceinline__ void EngineBody(const TileArgs& a) {
     row = 16 * t + 4 * (l / 16) + i;
     const int group = RgGroup(tile, r, a.group_stride, RG);
     column = 16 * group + l % 16;
-    return row < a.m && group < a.groups && column < a.n;
+    return in_rows(row) && group < a.groups && column < a.n;
   };
   // The values the epilogue adds to (the residual stream, an accumulated
   // y) are loaded now, beside the first weights, instead of after the sums.
@@ -251,13 +292,15 @@ __device__ __forceinline__ void EngineBody(const TileArgs& a) {
     }
   }
 
+  // Pairs past k load pair 0's unit, branch-free: their stages are never
+  // multiplied.
   const auto load_weights = [&](int pair, PairStage<MT, RG>& s) {
     const bool ok = pair < a.pairs;
 #pragma unroll
     for (int r = 0; r < RG; ++r) {
       const std::uint8_t* u = unit[r] + static_cast<std::size_t>(ok ? pair : 0) * kUnitBytes;
-      s.w[r] = ok ? *reinterpret_cast<const uint4*>(u + 16 * lane) : uint4{0U, 0U, 0U, 0U};
-      s.scales[r] = ok ? *reinterpret_cast<const std::uint32_t*>(u + kValueBytes + 4 * r16) : 0U;
+      s.w[r] = *reinterpret_cast<const uint4*>(u + 16 * lane);
+      s.scales[r] = *reinterpret_cast<const std::uint32_t*>(u + kValueBytes + 4 * r16);
     }
   };
   const auto load_activations = [&](int pair, PairStage<MT, RG>& s) {
@@ -268,13 +311,14 @@ __device__ __forceinline__ void EngineBody(const TileArgs& a) {
       for (int hf = 0; hf < 2; ++hf) {
         uint4 v{0U, 0U, 0U, 0U};
         if constexpr (SRC == ASource::kRowMajor) {
-          if (ok && row_ok[t] && 2 * pair + hf < k_blocks)
-            v = *reinterpret_cast<const uint4*>(
-                a.x + static_cast<std::size_t>(16 * t + r16) * a.k + 64 * pair + 32 * hf +
-                8 * octet);
+          v = BufferLoad16(x_buffer,
+                           2U * static_cast<std::uint32_t>((16 * t + r16) * a.k + 64 * pair +
+                                                           32 * hf + 8 * octet),
+                           ok && row_ok[t] && 2 * pair + hf < k_blocks);
         } else if constexpr (SRC == ASource::kFragBf16) {
-          if (ok && row_ok[t])
-            v = reinterpret_cast<const uint4*>(a.x)[((pair * 2 + t) * 2 + hf) * 64 + lane];
+          v = BufferLoad16(x_buffer,
+                           16U * static_cast<std::uint32_t>(((pair * 2 + t) * 2 + hf) * 64 + lane),
+                           ok && row_ok[t]);
         }
         s.a[t][hf] = v;
       }
@@ -293,23 +337,24 @@ __device__ __forceinline__ void EngineBody(const TileArgs& a) {
   };
   const auto load_rows = [&](int pair, RawRows& raw) {
     const int column = 64 * pair + 8 * (lane % 8);
-    const bool ok = pair < a.pairs && column < a.k;
+    // Lanes past k or outside the rows load an in-range address and keep
+    // zero.
+    const bool column_ok = column < a.k && pair < a.pairs;
 #pragma unroll
     for (int j = 0; j < JR; ++j) {
       const int row = 8 * j + lane / 8;
-      raw.v[j] = (ok && row < a.m)
-                     ? *reinterpret_cast<const uint4*>(
-                           a.x + static_cast<std::size_t>(row) * a.k + column)
-                     : uint4{0U, 0U, 0U, 0U};
+      raw.v[j] = BufferLoad16(x_buffer, 2U * static_cast<std::uint32_t>(row * a.k + column),
+                              column_ok && in_rows(row));
     }
   };
   const auto stage_rows = [&](int p, const RawRows& raw, PairStage<MT, RG>& s) {
     uint4* region = reinterpret_cast<uint4*>(lds + wave * StageFloats(MT, PW)) + p * MT * 128;
 #pragma unroll
     for (int j = 0; j < JR; ++j) {
+      // Rows outside the block were loaded as zero; writing them keeps the
+      // code branch-free (they are never read as operands).
       const int row = 8 * j + lane / 8;
-      if (row < a.m)
-        region[row * 8 + ((lane % 8) ^ (row % 8))] = raw.v[j];
+      region[row * 8 + ((lane % 8) ^ (row % 8))] = raw.v[j];
     }
 #pragma unroll
     for (int t = 0; t < MT; ++t)
@@ -365,11 +410,12 @@ __device__ __forceinline__ void EngineBody(const TileArgs& a) {
       const int pair = wave + p * waves;
 #pragma unroll
       for (int hf = 0; hf < 2; ++hf)
-        gamma_bits[p][hf] =
-            pair < a.pairs
-                ? *reinterpret_cast<const uint4*>(a.gamma + 64 * pair + 32 * hf + 8 * octet)
-                : uint4{0U, 0U, 0U, 0U};
+        gamma_bits[p][hf] = *reinterpret_cast<const uint4*>(
+            a.gamma + 64 * (pair < a.pairs ? pair : 0) + 32 * hf + 8 * octet);
     }
+    // The weights and norm weights are in flight before the residual
+    // stream's loads are issued.
+    __builtin_amdgcn_sched_barrier(0);
     float partial[2] = {0.0F, 0.0F};
 #pragma unroll
     for (int p = 0; p < PW; ++p) {
@@ -381,11 +427,11 @@ __device__ __forceinline__ void EngineBody(const TileArgs& a) {
         for (int hf = 0; hf < 2; ++hf)
 #pragma unroll
           for (int q = 0; q < 2; ++q) {
-            float4 v{0.0F, 0.0F, 0.0F, 0.0F};
-            if (ok && row_ok[t])
-              v = reinterpret_cast<const float4*>(
-                  a.h)[(((pair * 2 + t) * 2 + hf) * 2 + q) * 64 + lane];
-            hv[p][t][hf][q] = v;
+            hv[p][t][hf][q] = __builtin_bit_cast(
+                float4, BufferLoad16(h_buffer,
+                                     16U * static_cast<std::uint32_t>(
+                                               (((pair * 2 + t) * 2 + hf) * 2 + q) * 64 + lane),
+                                     ok && row_ok[t]));
           }
 #pragma unroll
       for (int t = 0; t < 2; ++t)
