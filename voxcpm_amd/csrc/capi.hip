@@ -88,8 +88,9 @@ int CheckProduct(const void* x, const void* w, const void* y, std::size_t m,
     return vx::Fail(VX_BAD_ARG, std::string(what) +
                                     ": m, n must be positive and k a positive "
                                     "multiple of 32");
-  // Activation offsets of the skinny kernels are 32-bit byte offsets.
-  if (m > (1U << 24) || n > (1U << 24) || k > (1U << 22))
+  // Activation offsets are 32-bit byte offsets (x below 1 GiB).
+  if (m > (1U << 24) || n > (1U << 24) || k > (1U << 22) ||
+      static_cast<unsigned long long>(m) * k > (1ULL << 29))
     return vx::Fail(VX_BAD_ARG, std::string(what) + ": shape too large");
   if (!Aligned(x, 16) || !Aligned(w, 16))
     return vx::Fail(VX_BAD_ARG,

@@ -208,6 +208,12 @@ __device__ inline uint4 BufferLoad16(__amdgpu_buffer_rsrc_t buffer, std::uint32_
       uint4, __builtin_amdgcn_raw_buffer_load_b128(
                  buffer, static_cast<int>(keep ? offset : kPastBuffer), 0, 0));
 }
+/// 4 bytes at `offset` of the buffer, or zero (no access) unless `keep`.
+__device__ inline std::uint32_t BufferLoad4(__amdgpu_buffer_rsrc_t buffer, std::uint32_t offset,
+                                            bool keep) {
+  return static_cast<std::uint32_t>(__builtin_amdgcn_raw_buffer_load_b32(
+      buffer, static_cast<int>(keep ? offset : kPastBuffer), 0, 0));
+}
 
 /// One pair's operands in flight: RG weight fragments with their scale
 /// pairs, and the MT x 2 activation fragments.

@@ -120,33 +120,45 @@ __global__ __launch_bounds__(T::kThreads, T::kMinBlocks) void TiledKernel(TiledA
   const int tile = logical % tiles;
   const int row0 = (tile % a.m_tiles) * BM;
   const int group0 = (tile / a.m_tiles) * (kTileN / 16);
+  const __amdgpu_buffer_rsrc_t x_buffer = q8::BufferOf(
+      a.x, 2U * static_cast<std::uint32_t>(a.m) * static_cast<std::uint32_t>(a.k));
   const int first_pair = split * a.pairs_per_split;
   const int steps = min(a.pairs, first_pair + a.pairs_per_split) - first_pair;
+  // The tile's panel groups as one buffer (under 2^31 bytes for k <= 2^22).
+  const std::uint32_t group_bytes = static_cast<std::uint32_t>(a.pairs) * kUnitBytes;
+  const __amdgpu_buffer_rsrc_t w_buffer =
+      q8::BufferOf(a.w + static_cast<std::size_t>(group0) * group_bytes,
+                   static_cast<std::uint32_t>(min(kTileN / 16, a.groups - group0)) * group_bytes);
 
   struct Staging {
     uint4 x[kAPieces];
     uint4 w[kUnits];
     std::uint32_t scales[kUnits];
   };
+  // Every step issues the same loads, steps past the split's end included:
+  // buffer loads at an offset past the buffer read zero without an access,
+  // so rows past m, columns past k and dead steps cost no traffic, and with
+  // no branch around them the compiler counts the loads in flight and waits
+  // for the oldest step only.
   const auto fetch = [&](int step, Staging& s) {
     const int pair = first_pair + step;
+    const bool live = step < steps;
 #pragma unroll
     for (int i = 0; i < kAPieces; ++i) {
       const int piece = tid + kThreads * i;
       const int row = row0 + piece / 8;
       const int column = 64 * pair + 8 * (piece % 8);
-      s.x[i] = (row < a.m && column < a.k)
-                   ? *reinterpret_cast<const uint4*>(a.x + static_cast<std::size_t>(row) * a.k +
-                                                     column)
-                   : uint4{0U, 0U, 0U, 0U};
+      s.x[i] = q8::BufferLoad16(x_buffer, 2U * static_cast<std::uint32_t>(row * a.k + column),
+                                live && row < a.m && column < a.k);
     }
 #pragma unroll
     for (int u = 0; u < kUnits; ++u) {
-      const int group = min(group0 + kUnits * wave + u, a.groups - 1);
-      const std::uint8_t* unit =
-          a.w + (static_cast<std::size_t>(group) * a.pairs + pair) * kUnitBytes;
-      s.w[u] = *reinterpret_cast<const uint4*>(unit + 16 * lane);
-      s.scales[u] = *reinterpret_cast<const std::uint32_t*>(unit + kValueBytes + 4 * r16);
+      const int group = min(kUnits * wave + u, a.groups - 1 - group0);
+      const std::uint32_t unit =
+          static_cast<std::uint32_t>(group) * group_bytes +
+          static_cast<std::uint32_t>(live ? pair : 0) * kUnitBytes;
+      s.w[u] = q8::BufferLoad16(w_buffer, unit + 16 * lane, live);
+      s.scales[u] = q8::BufferLoad4(w_buffer, unit + kValueBytes + 4 * r16, live);
     }
   };
   const auto store = [&](int buffer, const Staging& s) {
@@ -225,13 +237,13 @@ __global__ __launch_bounds__(T::kThreads, T::kMinBlocks) void TiledKernel(TiledA
   // The loop is unrolled over a multiple of D and 2 so that both indices
   // are compile-time.
   constexpr int U = D % 2 == 0 ? D : 2 * D;
+  // The stores after the last step write zeros into the LDS buffer that
+  // no later step reads.
   Staging staged[D];
 #pragma unroll
   for (int d = 0; d < D; ++d)
-    if (d < steps)
-      fetch(d, staged[d]);
-  if (steps > 0)
-    store(0, staged[0]);
+    fetch(d, staged[d]);
+  store(0, staged[0]);
   __syncthreads();
   for (int p = 0; p < steps; p += U) {
 #pragma unroll
@@ -239,11 +251,9 @@ __global__ __launch_bounds__(T::kThreads, T::kMinBlocks) void TiledKernel(TiledA
       const int q = p + d;
       if (q >= steps)
         break;
-      if (q + D < steps)
-        fetch(q + D, staged[d % D]);
+      fetch(q + D, staged[d % D]);
       compute(d % 2);
-      if (q + 1 < steps)
-        store((d + 1) % 2, staged[(d + 1) % D]);
+      store((d + 1) % 2, staged[(d + 1) % D]);
       __syncthreads();
     }
   }
