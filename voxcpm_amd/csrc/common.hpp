@@ -85,6 +85,37 @@ __device__ inline float WaveMax(float value) {
   return value;
 }
 
+/// `x` of the lane a DPP control picks within each row of 16 lanes (a VALU
+/// move, no LDS round trip).
+template<int kCtrl>
+__device__ inline float RowDpp(float x) {
+  return __int_as_float(
+      __builtin_amdgcn_update_dpp(0, __float_as_int(x), kCtrl, 0xF, 0xF, false));
+}
+constexpr int kDppXor1 = 0xB1;         // quad_perm [1, 0, 3, 2]
+constexpr int kDppXor2 = 0x4E;         // quad_perm [2, 3, 0, 1]
+constexpr int kDppHalfMirror = 0x141;  // lane i of 8 <- lane 7 - i
+constexpr int kDppMirror = 0x140;      // lane i of 16 <- lane 15 - i
+
+/// Sum over each row of 16 lanes by pairs at xor 1 and 2, then the
+/// mirrored halves of 8 and of 16 lanes; every lane of the row receives the
+/// same bits (each step adds the same two values).
+__device__ inline float RowSum16(float value) {
+  value += RowDpp<kDppXor1>(value);
+  value += RowDpp<kDppXor2>(value);
+  value += RowDpp<kDppHalfMirror>(value);
+  value += RowDpp<kDppMirror>(value);
+  return value;
+}
+
+__device__ inline float RowMax16(float value) {
+  value = fmaxf(value, RowDpp<kDppXor1>(value));
+  value = fmaxf(value, RowDpp<kDppXor2>(value));
+  value = fmaxf(value, RowDpp<kDppHalfMirror>(value));
+  value = fmaxf(value, RowDpp<kDppMirror>(value));
+  return value;
+}
+
 /// Sum over a block of up to 1024 threads; `scratch` holds one float per
 /// wave. Every thread receives the total, added in wave order.
 __device__ inline float BlockSum(float value, float* scratch) {

@@ -134,8 +134,11 @@ struct AttentionArgs {
 // halves of q and k, the two halves of v and the row's cos / sin. The
 // rotated, scaled queries, rotated keys and values go to LDS; then the
 // scores of all (query, key) pairs (16 lanes per query row), the softmax
-// over the keys (max, exp, sum within the 16 lanes) and the weighted values
-// (8 consecutive dimensions per thread, one 16-byte bf16 store).
+// over the keys (max, exp, sum within the 16 lanes by DPP moves) and the
+// weighted values (4 consecutive dimensions per thread). The dot
+// products and the weighted sums read LDS 16 bytes at a time, unrolled, so
+// that their reads are in flight together instead of one latency per term;
+// the terms are still added in index order.
 constexpr int kMaxLength = 16;
 
 __global__ __launch_bounds__(256) void AttentionKernel(AttentionArgs a) {
@@ -146,10 +149,12 @@ __global__ __launch_bounds__(256) void AttentionKernel(AttentionArgs a) {
   const int half = dims / 2;
   const int width = (a.heads + 2 * a.kv_heads) * dims;
   const int kv_head = head / (a.heads / a.kv_heads);
-  const int stride = dims + 1;  // padded rows: keys of one query spread over banks
+  // Rows padded by 16 bytes: 16-byte reads stay aligned and consecutive
+  // keys start 4 banks apart.
+  const int stride = dims + 4;
   float* qs = stage;                              // [length][stride]
   float* ks = qs + kMaxLength * stride;           // [length][stride]
-  float* vs = ks + kMaxLength * stride;           // [length][dims]
+  float* vs = ks + kMaxLength * stride;           // [kMaxLength][dims], zero past length
   float* weights = vs + kMaxLength * dims;        // [length][kMaxLength]
   float* inverse = weights + kMaxLength * kMaxLength;  // [length]
   const int quads = half / 4;
@@ -201,6 +206,8 @@ __global__ __launch_bounds__(256) void AttentionKernel(AttentionArgs a) {
       vs[r * dims + half + d + j] = vb[j];
     }
   }
+  for (int e = threadIdx.x; e < (kMaxLength - a.length) * dims; e += blockDim.x)
+    vs[a.length * dims + e] = 0.0F;
   __syncthreads();
   {
     // Scores: thread (query i, key j) = (t / 16, t % 16).
@@ -209,20 +216,24 @@ __global__ __launch_bounds__(256) void AttentionKernel(AttentionArgs a) {
     const bool valid = i < a.length && j < a.length;
     float score = -INFINITY;
     if (valid) {
+      const float4* query = reinterpret_cast<const float4*>(qs + i * stride);
+      const float4* key = reinterpret_cast<const float4*>(ks + j * stride);
       float dot = 0.0F;
-      for (int d = 0; d < dims; ++d)
-        dot += qs[i * stride + d] * ks[j * stride + d];
+#pragma unroll 4
+      for (int d4 = 0; d4 < dims / 4; ++d4) {
+        const float4 q = query[d4];
+        const float4 k = key[d4];
+        dot += q.x * k.x;
+        dot += q.y * k.y;
+        dot += q.z * k.z;
+        dot += q.w * k.w;
+      }
       score = dot;
     }
-    float maximum = score;
-#pragma unroll
-    for (int offset = kMaxLength / 2; offset > 0; offset /= 2)
-      maximum = fmaxf(maximum, __shfl_xor(maximum, offset, kWave));
+    static_assert(kMaxLength == 16, "one query's keys are one DPP row");
+    const float maximum = RowMax16(score);
     const float weight = valid ? expf(score - maximum) : 0.0F;
-    float sum = weight;
-#pragma unroll
-    for (int offset = kMaxLength / 2; offset > 0; offset /= 2)
-      sum += __shfl_xor(sum, offset, kWave);
+    const float sum = RowSum16(weight);
     if (i < kMaxLength) {
       weights[i * kMaxLength + j] = weight;
       if (j == 0)
@@ -230,22 +241,36 @@ __global__ __launch_bounds__(256) void AttentionKernel(AttentionArgs a) {
     }
   }
   __syncthreads();
-  const int octets = dims / 8;
-  for (int e = threadIdx.x; e < a.length * octets; e += blockDim.x) {
-    const int i = e / octets;
-    const int d = 8 * (e % octets);
-    float out[8] = {0, 0, 0, 0, 0, 0, 0, 0};
-    for (int j = 0; j < a.length; ++j) {
-      const float w = weights[i * kMaxLength + j];
+  // Weighted values: four consecutive dimensions per thread.
+  const int quarters = dims / 4;
+  for (int e = threadIdx.x; e < a.length * quarters; e += blockDim.x) {
+    const int i = e / quarters;
+    const int d = 4 * (e % quarters);
+    const float4* w4 = reinterpret_cast<const float4*>(weights + i * kMaxLength);
+    float w[kMaxLength];
 #pragma unroll
-      for (int x = 0; x < 8; ++x)
-        out[x] += w * vs[j * dims + d + x];
+    for (int j4 = 0; j4 < kMaxLength / 4; ++j4) {
+      const float4 v = w4[j4];
+      w[4 * j4] = v.x;
+      w[4 * j4 + 1] = v.y;
+      w[4 * j4 + 2] = v.z;
+      w[4 * j4 + 3] = v.w;
     }
+    float out[4] = {0, 0, 0, 0};
+    // Keys past the length have weight 0 and zero values: they add +0.
 #pragma unroll
-    for (int x = 0; x < 8; ++x)
-      out[x] *= inverse[i];
+    for (int j = 0; j < kMaxLength; ++j) {
+      const float4 v = *reinterpret_cast<const float4*>(vs + j * dims + d);
+      out[0] += w[j] * v.x;
+      out[1] += w[j] * v.y;
+      out[2] += w[j] * v.z;
+      out[3] += w[j] * v.w;
+    }
+    const float inv = inverse[i];
     const int row = branch * a.length + i;
-    *reinterpret_cast<uint4*>(a.out + BfFragIndex(row, head * dims + d)) = q8::PackBf16x8(out);
+    *reinterpret_cast<uint2*>(a.out + BfFragIndex(row, head * dims + d)) =
+        uint2{q8::PackBf16x2(out[0] * inv, out[1] * inv),
+              q8::PackBf16x2(out[2] * inv, out[3] * inv)};
   }
 }
 
@@ -516,7 +541,7 @@ void Attention(const float* qkv, const float* rope, Bf16* out, const Shape& s,
   a.head_dim = s.head_dim;
   a.scale = 1.0F / std::sqrt(static_cast<float>(s.head_dim));
   const std::size_t shared =
-      (static_cast<std::size_t>(kMaxLength) * (3 * s.head_dim + 2) +
+      (static_cast<std::size_t>(kMaxLength) * (3 * s.head_dim + 8) +
        kMaxLength * kMaxLength + kMaxLength) *
       sizeof(float);
   AttentionKernel<<<dim3(2, static_cast<unsigned>(s.heads)), 256, shared,
