@@ -116,6 +116,34 @@ __device__ inline float RowMax16(float value) {
   return value;
 }
 
+/// x[l] + x[l ^ 16] by one v_permlane16_swap (rows 0 and 1, 2 and 3 meet);
+/// both lanes of a pair receive the same bits.
+__device__ inline float AddXor16(float x) {
+  const auto swapped = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x),
+                                                        false, false);
+  return __uint_as_float(swapped[0]) + __uint_as_float(swapped[1]);
+}
+
+/// x[l] + x[l ^ 32] by one v_permlane32_swap (the halves meet).
+__device__ inline float AddXor32(float x) {
+  const auto swapped = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x),
+                                                        false, false);
+  return __uint_as_float(swapped[0]) + __uint_as_float(swapped[1]);
+}
+
+/// Lane l receives x[l % 16] (`row0`) and x[16 + l % 16] (`row1`): the first
+/// two rows of 16 lanes broadcast over the wave by permlane swaps.
+__device__ inline void BroadcastRows01(float x, float& row0, float& row1) {
+  // [x0, x0, x2, x2] and [x1, x1, x3, x3] (rows of 16 lanes) ...
+  const auto rows = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x),
+                                                     false, false);
+  // ... then each one's low half over both halves.
+  const auto even = __builtin_amdgcn_permlane32_swap(rows[0], rows[0], false, false);
+  const auto odd = __builtin_amdgcn_permlane32_swap(rows[1], rows[1], false, false);
+  row0 = __uint_as_float(even[0]);
+  row1 = __uint_as_float(odd[0]);
+}
+
 /// Sum over a block of up to 1024 threads; `scratch` holds one float per
 /// wave. Every thread receives the total, added in wave order.
 __device__ inline float BlockSum(float value, float* scratch) {

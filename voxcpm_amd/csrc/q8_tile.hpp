@@ -105,6 +105,11 @@ struct TileArgs {
   // multiple of 8), on one compute die, whose L2 serves their weights.
   int row_blocks;
   int rows_per_block;
+  // Fragment-order sources with MT = 1 take tile-aligned row blocks
+  // instead: block b is part b % tile_blocks of the 16-row tile
+  // b / tile_blocks (row_blocks = tiles of m x tile_blocks), so that each
+  // workgroup loads and multiplies one 16-row tile.
+  int tile_blocks;
   // activations
   const Bf16* x;          // kRowMajor [m][k] / kFragBf16
   const float* h;         // kNormF32: float32 fragment order [32][k]
@@ -230,8 +235,11 @@ struct PairStage {
 /// Staged row-major sources load JR groups of 8 rows (8 JR >= m).
 template<int MT, int RG, ASource SRC, Output OUT, int PW = 1, int JR = 2 * MT>
 __device__ __forceinline__ void EngineBody(const TileArgs& a) {
+  // One 16-row tile of a fragment-order source per workgroup.
+  constexpr bool kOneTile = MT == 1 && SRC == ASource::kFragBf16;
   static_assert(SRC != ASource::kNormF32 || MT == 2, "norm source is 32 rows");
-  static_assert(OUT == Output::kStore || MT == 2, "fragment outputs are 32 rows");
+  static_assert(OUT == Output::kStore || MT == 2 || kOneTile,
+                "fragment outputs are 32 rows or one tile of them");
   static_assert(OUT != Output::kSwiGlu || RG == 2, "SwiGLU pairs two groups");
   extern __shared__ float lds[];
   const int lane = threadIdx.x % kWave;
@@ -241,8 +249,20 @@ __device__ __forceinline__ void EngineBody(const TileArgs& a) {
   const int octet = lane / 16;
   const int tiles = static_cast<int>(gridDim.x) / a.row_blocks;
   const int tile = static_cast<int>(blockIdx.x) % tiles;
-  const int row_lo = (static_cast<int>(blockIdx.x) / tiles) * a.rows_per_block;
-  const int row_hi = min(a.m, row_lo + a.rows_per_block);
+  const int block = static_cast<int>(blockIdx.x) / tiles;
+  int row_lo, row_hi;
+  int tile_base = 0;  // the workgroup's first 16-row tile
+  if constexpr (kOneTile) {
+    tile_base = block / a.tile_blocks;
+    const int first = 16 * tile_base;
+    const int count = min(16, a.m - first);
+    const int per = (count + a.tile_blocks - 1) / a.tile_blocks;
+    row_lo = first + (block % a.tile_blocks) * per;
+    row_hi = min(first + count, row_lo + per);
+  } else {
+    row_lo = block * a.rows_per_block;
+    row_hi = min(a.m, row_lo + a.rows_per_block);
+  }
   const auto in_rows = [&](int row) { return row >= row_lo && row < row_hi; };
   const int k_blocks = a.k / 32;
 
@@ -255,7 +275,7 @@ __device__ __forceinline__ void EngineBody(const TileArgs& a) {
   bool row_ok[MT];
 #pragma unroll
   for (int t = 0; t < MT; ++t)
-    row_ok[t] = in_rows(16 * t + r16);
+    row_ok[t] = in_rows(16 * (tile_base + t) + r16);
   // The activations as buffers: row-major [m][k] bf16, fragment-order bf16
   // (32 rows x pairs x 64 columns) or fragment-order float32.
   const __amdgpu_buffer_rsrc_t x_buffer = BufferOf(
@@ -275,7 +295,7 @@ __device__ __forceinline__ void EngineBody(const TileArgs& a) {
     const int l = e % 64;
     const int r = f / MT;
     const int t = f % MT;
-    row = 16 * t + 4 * (l / 16) + i;
+    row = 16 * (tile_base + t) + 4 * (l / 16) + i;
     const int group = RgGroup(tile, r, a.group_stride, RG);
     column = 16 * group + l % 16;
     return in_rows(row) && group < a.groups && column < a.n;
@@ -322,9 +342,10 @@ __device__ __forceinline__ void EngineBody(const TileArgs& a) {
                                                            32 * hf + 8 * octet),
                            ok && row_ok[t] && 2 * pair + hf < k_blocks);
         } else if constexpr (SRC == ASource::kFragBf16) {
-          v = BufferLoad16(x_buffer,
-                           16U * static_cast<std::uint32_t>(((pair * 2 + t) * 2 + hf) * 64 + lane),
-                           ok && row_ok[t]);
+          v = BufferLoad16(
+              x_buffer,
+              16U * static_cast<std::uint32_t>(((pair * 2 + tile_base + t) * 2 + hf) * 64 + lane),
+              ok && row_ok[t]);
         }
         s.a[t][hf] = v;
       }
@@ -449,12 +470,11 @@ __device__ __forceinline__ void EngineBody(const TileArgs& a) {
             partial[t] += v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
           }
     }
-    // The four octets of a row meet across lanes; waves meet in LDS.
+    // The four octets of a row meet across lanes (permlane swaps, no LDS
+    // round trip); waves meet in LDS.
 #pragma unroll
-    for (int t = 0; t < 2; ++t) {
-      partial[t] += __shfl_xor(partial[t], 16, kWave);
-      partial[t] += __shfl_xor(partial[t], 32, kWave);
-    }
+    for (int t = 0; t < 2; ++t)
+      partial[t] = AddXor32(AddXor16(partial[t]));
     if (octet == 0) {
       squares[wave * kSquaresStride + r16] = partial[0];
       squares[wave * kSquaresStride + 16 + r16] = partial[1];
@@ -469,11 +489,10 @@ __device__ __forceinline__ void EngineBody(const TileArgs& a) {
 #pragma unroll
     for (int w = 0; w < kHalf; ++w)
       total += squares[(first + w) * kSquaresStride + lane % 32];
-    total += __shfl_xor(total, 32, kWave);
+    total = AddXor32(total);
     const float row_inverse = rsqrtf(total / static_cast<float>(a.k) + a.eps);
     float inverse[2];
-    inverse[0] = __shfl(row_inverse, r16, kWave);
-    inverse[1] = __shfl(row_inverse, 16 + r16, kWave);
+    BroadcastRows01(row_inverse, inverse[0], inverse[1]);
 #pragma unroll
     for (int p = 0; p < PW; ++p) {
       const int pair = wave + p * waves;
