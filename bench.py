@@ -39,8 +39,8 @@ BF16_PEAK_TFLOPS = 2500.0
 # reading of a 256 MiB copy of known size) + WRITE_SIZE KiB (scale 1.0).
 # Measured, not computed: re-measure when the product kernel changes.
 FETCH_SCALE = 262144 / 131083.5
-TRAFFIC_KIB = {(1024, 3072): (1832.5, 264.0), (1024, 8192): (4558.5, 704.0),
-               (2048, 2048): (2552.5, 176.0), (2048, 16384): (17806.5, 1408.0)}
+TRAFFIC_KIB = {(1024, 3072): (1833.5, 264.0), (1024, 8192): (4553.0, 704.0),
+               (2048, 2048): (2553.5, 176.0), (2048, 16384): (17805.5, 1408.0)}
 PREFILL_M = [129, 256, 512, 1024]
 PREFILL_N = [2048, 6144, 16384]
 PREFILL_K = 2048
