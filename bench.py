@@ -325,30 +325,40 @@ def cpu_baseline(synth):
     sys.path.insert(0, os.path.join(ROOT, "tests"))
     import oracle_lib
     threads = max(1, min(16, os.cpu_count() or 1))
-    total_bytes = 0
-    total_seconds = 0.0
-    repeats = {}
+    inputs = []
     for k, n in SWEEP_SHAPES:
         rng = synth.Rng(0, k * 31 + n)
-        blocks = synth.q8_blocks(rng, n, k)
-        x = synth.activations(rng, ROWS, k)
-        count = 0
-        start = time.perf_counter()
-        while True:
-            oracle_lib.q8_linear(x, blocks, n, threads=threads)
-            count += 1
-            elapsed = time.perf_counter() - start
-            if elapsed > 2.5 or count >= 50:
-                break
-        total_seconds += elapsed
-        total_bytes += count * q8_bytes(k, n)
-        repeats[f"{k}x{n}"] = count
-    value = total_bytes / total_seconds / 1e9
+        inputs.append((k, n, synth.q8_blocks(rng, n, k), synth.activations(rng, ROWS, k)))
+
+    def rate(thread_count, seconds_per_shape, max_repeats):
+        total_bytes = 0
+        total_seconds = 0.0
+        repeats = {}
+        for k, n, blocks, x in inputs:
+            count = 0
+            start = time.perf_counter()
+            while True:
+                oracle_lib.q8_linear(x, blocks, n, threads=thread_count)
+                count += 1
+                elapsed = time.perf_counter() - start
+                if elapsed > seconds_per_shape or count >= max_repeats:
+                    break
+            total_seconds += elapsed
+            total_bytes += count * q8_bytes(k, n)
+            repeats[f"{k}x{n}"] = count
+        return total_bytes / total_seconds / 1e9, repeats, total_seconds
+
+    value, repeats, seconds = rate(threads, 2.5, 50)
     log(f"CPU oracle: {value:.2f} GB/s on {threads} threads")
+    single, single_repeats, single_seconds = rate(1, 1.0, 20)
+    log(f"CPU oracle: {single:.3f} GB/s on 1 thread")
     return {"value": round(value, 3), "unit": "GB/s", "cores": threads,
             "kind": "port",
             "sample": "oracle Q8_0 x bf16 products, M=22, the four sweep shapes, "
-                      f"repeats {repeats}, {total_seconds:.1f} s"}
+                      f"repeats {repeats}, {seconds:.1f} s",
+            "value_1_thread": round(single, 4),
+            "sample_1_thread": f"the same shapes on one thread, repeats {single_repeats}, "
+                               f"{single_seconds:.1f} s"}
 
 
 def cpu_patch(synth):
