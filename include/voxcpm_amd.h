@@ -110,6 +110,47 @@ int vx_q8_linear_bf16(const uint16_t* x, const void* packed, uint16_t* y,
                       void* stream);
 
 /* ------------------------------------------------------------------------
+ * bfloat16 weights (the HF checkpoint's format): the same products on bf16
+ * W, as panels (16 rows x 64 columns per 2048-byte unit, the two 32-column
+ * blocks' MFMA operands one after the other, zero past n and k) or as rows
+ * [n][k]. Each 32-column block's products are summed into the float32
+ * accumulators on the matrix cores in k order, as the reference's bf16
+ * products do (kernels/wmma_products.hip:210-213); there is no per-block
+ * scale.
+ * ---------------------------------------------------------------------- */
+
+/* Bytes of a packed bf16 [n][k] matrix (k a multiple of 32).
+ * Replaces kernels::Bf16TilesBytes (kernels/wmma_products.hpp:39-43). */
+size_t vx_bf16_packed_bytes(size_t n, size_t k);
+
+/* bf16 rows [n][k] -> panels (a byte shuffle).
+ * Replaces kernels::Bf16ToTiles (kernels/wmma_products.hpp:51-53). */
+int vx_bf16_pack(const uint16_t* rows, size_t n, size_t k, void* packed,
+                 void* stream);
+
+/* Panels -> bf16 rows [n][k], the exact inverse of vx_bf16_pack.
+ * Replaces kernels::Bf16TilesToRows (kernels/wmma_products.hpp:60-62). */
+int vx_bf16_unpack(const void* packed, size_t n, size_t k, uint16_t* rows,
+                   void* stream);
+
+/* y[m][n] (+)= x[m][k] . W[n][k]^T on bf16 panels, any m (k a multiple of
+ * 32). Replaces kernels::WmmaBf16 and Bf16Gemm::Linear on kBf16Tiles
+ * weights (kernels/wmma_products.hpp:95-99; gemm.cpp:259-303, where more
+ * than 128 rows unpack the tiles for hipBLASLt: here the same tiled
+ * kernel as the Q8_0 products takes them). */
+int vx_bf16_linear(const uint16_t* x, const void* packed, float* y, size_t m,
+                   size_t k, size_t n, int accumulate, vx_scratch* scratch,
+                   void* stream);
+
+/* The same on bf16 rows [n][k] as they come, m <= 32, k a multiple of 8
+ * (VX_UNSUPPORTED beyond 32 rows, where the reference hands the product to
+ * hipBLASLt). Replaces kernels::SkinnyGemm and Bf16Gemm::LinearRows
+ * (kernels/skinny_gemm.hpp:17-24; gemm.cpp:315-330). */
+int vx_bf16_linear_rows(const uint16_t* x, const uint16_t* w, float* y,
+                        size_t m, size_t k, size_t n, int accumulate,
+                        void* stream);
+
+/* ------------------------------------------------------------------------
  * Generator kernels: one entry per reference launcher on the path
  * (kernels/generator_kernels.hpp), same argument meaning, any head_dim that
  * is a multiple of 2 up to 256.

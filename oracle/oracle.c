@@ -206,6 +206,51 @@ double vo_q8_check(const float* y, const uint16_t* x, const uint8_t* blocks,
   return worst;
 }
 
+/* ---- bfloat16 weights --------------------------------------------------- */
+
+void vo_bf16_linear(const uint16_t* x, const uint16_t* w, float* y, size_t m,
+                    size_t k, size_t n, int accumulate) {
+  /* kernels/wmma_products.hip:210-213 (acc = Wmma(a0, b0, acc);
+   * acc = Wmma(a1, b1, acc) per 32-column block: 16 columns per step) */
+  for (size_t row = 0; row < m; ++row) {
+    for (size_t col = 0; col < n; ++col) {
+      float acc = 0.0f;
+      for (size_t c0 = 0; c0 < k; c0 += 16) {
+        float chunk = 0.0f;
+        const size_t c1 = c0 + 16 < k ? c0 + 16 : k;
+        for (size_t c = c0; c < c1; ++c)
+          chunk += vo_bf16_value(x[row * k + c]) * vo_bf16_value(w[col * k + c]);
+        acc += chunk;
+      }
+      float* target = y + row * n + col;
+      *target = accumulate ? *target + acc : acc;
+    }
+  }
+}
+
+double vo_bf16_check(const float* y, const uint16_t* x, const uint16_t* w,
+                     const float* before, size_t m, size_t k, size_t n) {
+  /* tests/products_test.cpp:117-145 */
+  double worst = 0.0;
+  for (size_t row = 0; row < m; ++row) {
+    for (size_t col = 0; col < n; ++col) {
+      double exact = before != NULL ? (double)before[row * n + col] : 0.0;
+      double magnitude = 0.0;
+      for (size_t c = 0; c < k; ++c) {
+        const double product =
+            (double)vo_bf16_value(x[row * k + c]) * (double)vo_bf16_value(w[col * k + c]);
+        exact += product;
+        magnitude += fabs(product);
+      }
+      const double error = fabs((double)y[row * n + col] - exact) /
+                           (magnitude > 1e-30 ? magnitude : 1e-30);
+      if (!(error <= worst))
+        worst = error; /* NaN propagates as the worst */
+    }
+  }
+  return worst;
+}
+
 /* ---- generator kernels -------------------------------------------------- */
 
 void vo_rms_norm(const float* input, const uint16_t* weight, uint16_t* output,

@@ -58,6 +58,23 @@ void vo_q8_linear(const uint16_t* x, const uint8_t* blocks, float* y, size_t m,
 double vo_q8_check(const float* y, const uint16_t* x, const uint8_t* blocks,
                    const float* before, size_t m, size_t k, size_t n);
 
+/* ---- bfloat16 weights --------------------------------------------------- */
+
+/* y[m][n] (+)= x[m][k] . W[n][k]^T for bf16 x and bf16 rows W, in the
+ * reference's bf16 order (kernels/wmma_products.hip:210-213): per
+ * 16-column chunk (one v_wmma_f32_16x16x16_bf16) a float32 sum of the
+ * products, added into the float32 accumulator in k order; the order
+ * inside a chunk is the hardware's. y = accumulate ? y + acc : acc.
+ * k a multiple of 8 (a last, short chunk is summed the same way). */
+void vo_bf16_linear(const uint16_t* x, const uint16_t* w, float* y, size_t m,
+                    size_t k, size_t n, int accumulate);
+
+/* Worst |y - exact| / sum|x*w| over all outputs for bf16 rows W, exact in
+ * double (tests/products_test.cpp:117-145, used with bf16 weights at
+ * :234-237). `before` is the y the product accumulated into, or NULL. */
+double vo_bf16_check(const float* y, const uint16_t* x, const uint16_t* w,
+                     const float* before, size_t m, size_t k, size_t n);
+
 /* ---- generator kernels (kernels/generator_kernels.hip) ---------------- */
 
 /* :91-108 */

@@ -54,6 +54,10 @@ _SIGNATURES = {
                       c_int, c_int], None),
     "vo_q8_check": ([c_void_p, c_void_p, c_void_p, c_void_p, c_size, c_size,
                      c_size], ctypes.c_double),
+    "vo_bf16_linear": ([c_void_p, c_void_p, c_void_p, c_size, c_size, c_size, c_int],
+                       None),
+    "vo_bf16_check": ([c_void_p, c_void_p, c_void_p, c_void_p, c_size, c_size,
+                       c_size], ctypes.c_double),
     "vo_rms_norm": ([c_void_p, c_void_p, c_void_p, c_void_p, c_size, c_size,
                      c_float], None),
     "vo_rope_table": ([ctypes.c_double, c_size, c_void_p, c_float, c_size,
@@ -141,6 +145,23 @@ def q8_check(y: np.ndarray, x: np.ndarray, blocks: np.ndarray,
     n = y.shape[1]
     y = np.ascontiguousarray(y, dtype=np.float32)
     return lib().vo_q8_check(ptr(y), ptr(x), ptr(blocks), ptr(before), m, k, n)
+
+
+def bf16_linear(x: np.ndarray, w: np.ndarray, before: np.ndarray | None = None) -> np.ndarray:
+    """x bf16 bits [m][k], w bf16 bits [n][k] -> float32 [m][n]."""
+    m, k = x.shape
+    n = w.shape[0]
+    y = np.zeros((m, n), dtype=np.float32) if before is None else before.copy()
+    lib().vo_bf16_linear(ptr(x), ptr(w), ptr(y), m, k, n, int(before is not None))
+    return y
+
+
+def bf16_check(y: np.ndarray, x: np.ndarray, w: np.ndarray,
+               before: np.ndarray | None = None) -> float:
+    m, k = x.shape
+    n = w.shape[0]
+    y = np.ascontiguousarray(y, dtype=np.float32)
+    return lib().vo_bf16_check(ptr(y), ptr(x), ptr(w), ptr(before), m, k, n)
 
 
 def euler_schedule(timesteps: int, sway: float, skip: bool):

@@ -131,6 +131,46 @@ def test_q8_linear_scales_after_block_sums(oracle):
     assert y[0, 0] == 0.0
 
 
+def test_bf16_linear_exact_on_integers(oracle):
+    """Small integer activations and weights in bf16: every float32 sum is
+    exact, so the product equals the integer matrix product bit for bit."""
+    rng = synth.Rng(6, 6)
+    m, k, n = 4, 96, 21
+    xi = ((rng.bits(m * k) % np.uint64(9)).astype(np.int64) - 4).reshape(m, k)
+    wi = ((rng.bits(n * k) % np.uint64(15)).astype(np.int64) - 7).reshape(n, k)
+    x = synth.bf16_bits(xi.astype(np.float32))
+    w = synth.bf16_bits(wi.astype(np.float32))
+    assert np.array_equal(oracle.bf16_linear(x, w), (xi @ wi.T).astype(np.float32))
+
+
+@pytest.mark.parametrize("k", [64, 40])
+def test_bf16_linear_against_float64(oracle, k):
+    """Against a float64 product (independent of the oracle's loops), a k
+    with a short last 16-column chunk, and the accumulate path; the checker
+    agrees and catches a planted error of 1e-4 |x w|."""
+    rng = synth.Rng(7, k)
+    m, n = 6, 19
+    x = synth.activations(rng, m, k)
+    w = synth.activations(rng, n, k)
+    xf = synth.bf16_values(x).astype(np.float64)
+    wf = synth.bf16_values(w).astype(np.float64)
+    exact = xf @ wf.T
+    magnitude = np.abs(xf) @ np.abs(wf).T
+    y = oracle.bf16_linear(x, w)
+    assert np.max(np.abs(y - exact) / magnitude) < 2e-6
+    before = f32(rng.normal(m * n).reshape(m, n))
+    y2 = oracle.bf16_linear(x, w, before=before)
+    assert np.max(np.abs(y2 - (exact + before)) / (magnitude + np.abs(before))) < 2e-6
+    assert oracle.bf16_check(y, x, w) < 2e-6
+    assert oracle.bf16_check(y2, x, w, before) < 2e-6
+    bad = y.copy()
+    bad[2, 5] += 1e-4 * magnitude[2, 5]
+    assert oracle.bf16_check(bad, x, w) > 5e-5
+    # A transposed weight (a plausible layout slip) fails the checker.
+    if k == 64:
+        assert oracle.bf16_check(oracle.bf16_linear(x, np.ascontiguousarray(w[::-1])), x, w) > 1e-2
+
+
 # ---- generator kernels -------------------------------------------------------
 
 def test_rms_norm(oracle):

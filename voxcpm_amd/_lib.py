@@ -77,6 +77,13 @@ _SIGNATURES = {
                               c_size, c_int, c_void_p, c_int, c_int, c_int,
                               c_void_p], c_int),
     "vx_q8_plan": ([c_size, c_size, c_size, c_void_p, c_void_p], c_int),
+    "vx_bf16_packed_bytes": ([c_size, c_size], c_size),
+    "vx_bf16_pack": ([c_void_p, c_size, c_size, c_void_p, c_void_p], c_int),
+    "vx_bf16_unpack": ([c_void_p, c_size, c_size, c_void_p, c_void_p], c_int),
+    "vx_bf16_linear": ([c_void_p, c_void_p, c_void_p, c_size, c_size, c_size,
+                        c_int, c_void_p, c_void_p], c_int),
+    "vx_bf16_linear_rows": ([c_void_p, c_void_p, c_void_p, c_size, c_size, c_size,
+                             c_int, c_void_p], c_int),
     "vx_test_pack_bf16": ([c_void_p, c_void_p, c_size, c_void_p], c_int),
     "vx_stream_read": ([c_void_p, c_size, ctypes.c_uint32, c_void_p, c_void_p], c_int),
     "vx_rms_norm": ([c_void_p, c_void_p, c_void_p, c_void_p, c_size, c_size,

@@ -101,9 +101,12 @@ int CheckProduct(const void* x, const void* w, const void* y, std::size_t m,
 
 int Product(const uint16_t* x, const void* packed, float* y, uint16_t* y_bf16,
             size_t m, size_t k, size_t n, int accumulate, vx_scratch* scratch,
-            int rg, int waves, int splits, void* stream) {
+            int rg, int waves, int splits, void* stream,
+            vx::q8::Weights kind = vx::q8::Weights::kQ8) {
   if (m > vx::kExactRows)
-    return vx::RunTiled(x, packed, y, y_bf16, m, k, n, accumulate != 0, false,
+    return vx::RunTiled(x, packed, y, y_bf16, m, k, n, accumulate != 0,
+                        kind == vx::q8::Weights::kQ8 ? vx::TiledMode::kQ8Expanded
+                                                     : vx::TiledMode::kBf16,
                         scratch != nullptr ? scratch->partials : nullptr,
                         scratch != nullptr ? scratch->partial_floats : 0,
                         vx::Stream(stream));
@@ -113,7 +116,7 @@ int Product(const uint16_t* x, const void* packed, float* y, uint16_t* y_bf16,
   return vx::RunSkinny(x, packed, y, y_bf16, m, k, n, accumulate != 0, plan,
                        scratch != nullptr ? scratch->partials : nullptr,
                        scratch != nullptr ? scratch->counters : nullptr,
-                       vx::Stream(stream));
+                       vx::Stream(stream), kind);
 }
 
 }  // namespace
@@ -177,6 +180,34 @@ int vx_q8_linear_bf16(const uint16_t* x, const void* packed, uint16_t* y,
                       void* stream) {
   VX_TRY(CheckProduct(x, packed, y, m, k, n, "vx_q8_linear_bf16"));
   return Product(x, packed, nullptr, y, m, k, n, 0, scratch, 0, 0, 0, stream);
+}
+
+int vx_bf16_linear(const uint16_t* x, const void* packed, float* y, size_t m, size_t k,
+                   size_t n, int accumulate, vx_scratch* scratch, void* stream) {
+  VX_TRY(CheckProduct(x, packed, y, m, k, n, "vx_bf16_linear"));
+  if (vx::q8::Bf16PackedBytes(n, k) > (1ULL << 31) - 16)
+    return vx::Fail(VX_BAD_ARG, "vx_bf16_linear: shape too large");
+  return Product(x, packed, y, nullptr, m, k, n, accumulate, scratch, 0, 0, 0, stream,
+                 vx::q8::Weights::kBf16);
+}
+
+int vx_bf16_linear_rows(const uint16_t* x, const uint16_t* w, float* y, size_t m, size_t k,
+                        size_t n, int accumulate, void* stream) {
+  if (x == nullptr || w == nullptr || y == nullptr)
+    return vx::Fail(VX_BAD_ARG, "vx_bf16_linear_rows: null pointer");
+  if (m == 0 || n == 0 || k == 0 || k % 8 != 0)
+    return vx::Fail(VX_BAD_ARG,
+                    "vx_bf16_linear_rows: m, n must be positive and k a positive multiple "
+                    "of 8");
+  if (m > 32)
+    return vx::Fail(VX_UNSUPPORTED, "vx_bf16_linear_rows: at most 32 rows");
+  // Byte offsets into x and w are 32-bit.
+  if (n > (1U << 24) || k > (1U << 22) || 2ULL * n * k > (1ULL << 31) - 16)
+    return vx::Fail(VX_BAD_ARG, "vx_bf16_linear_rows: shape too large");
+  if (!Aligned(x, 16) || !Aligned(w, 16))
+    return vx::Fail(VX_BAD_ARG, "vx_bf16_linear_rows: x and w must be 16-byte aligned");
+  return Product(x, w, y, nullptr, m, k, n, accumulate, nullptr, 0, 0, 0, stream,
+                 vx::q8::Weights::kBf16Rows);
 }
 
 /* Testing and tuning entry (declared in voxcpm_amd_internal.h): the product

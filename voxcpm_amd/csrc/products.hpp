@@ -8,6 +8,7 @@
 #include <cstddef>
 
 #include "common.hpp"
+#include "q8.hpp"
 
 namespace vx {
 
@@ -46,19 +47,24 @@ ProductPlan PlanSkinny(std::size_t m, std::size_t k, std::size_t n,
                        std::size_t scratch_floats, std::size_t scratch_counters,
                        int rg = 0, int waves = 0, int splits = 0);
 
-/// Launches the exact product (m <= 128) with `plan`.
+/// Launches the product (m <= 128) with `plan`: Q8_0 panels with the exact
+/// arithmetic, or bf16 weights (panels, or rows [n][k] for m <= 32) on the
+/// engine and tiled plans.
 int RunSkinny(const Bf16* x, const void* w, float* y, Bf16* y_bf16,
               std::size_t m, std::size_t k, std::size_t n, bool accumulate,
               const ProductPlan& plan, float* partials, unsigned* counters,
-              hipStream_t stream);
+              hipStream_t stream, q8::Weights kind = q8::Weights::kQ8);
 
-/// Launches the LDS-tiled product (q8_tiled.hip; meant for m > 32): the
-/// exact per-block arithmetic, or with `exact` false the expansion to
-/// bf16(scale * q) of products of more than 128 rows. Small grids split k
-/// over workgroups when `partials` holds partial_floats >= 2 m n floats
-/// (a second launch adds the splits in order).
+/// What the tiled kernel multiplies: Q8_0 panels with the exact per-block
+/// arithmetic, Q8_0 panels expanded to bf16(scale * q) (the reference's
+/// arithmetic beyond 128 rows), or bf16 panels.
+enum class TiledMode : int { kQ8Exact = 0, kQ8Expanded = 1, kBf16 = 2 };
+
+/// Launches the LDS-tiled product (q8_tiled.hip; meant for m > 32). Small
+/// grids split k over workgroups when `partials` holds partial_floats >=
+/// 2 m n floats (a second launch adds the splits in order).
 int RunTiled(const Bf16* x, const void* w, float* y, Bf16* y_bf16, std::size_t m,
-             std::size_t k, std::size_t n, bool accumulate, bool exact,
+             std::size_t k, std::size_t n, bool accumulate, TiledMode mode,
              float* partials, std::size_t partial_floats, hipStream_t stream);
 
 }  // namespace vx

@@ -43,6 +43,21 @@ inline std::size_t PackedBytes(std::size_t n, std::size_t k) {
   return Groups(n) * Pairs(k) * kUnitBytes;
 }
 
+// bfloat16 weights take the same units at 2048 bytes: two halves of 1024
+// bytes, one per 32-column block of the pair; in half h lane L owns bytes
+// [16 L, 16 L + 16) = w[r][64 p + 32 h + 8 j + 0..7] (bf16 bits) for
+// r = L % 16, j = L / 16. Rows past n and columns past k are zero. One
+// 16-byte load per lane and half is the MFMA B operand of one block.
+constexpr int kBf16UnitBytes = 2048;
+constexpr int kBf16HalfBytes = 1024;
+inline std::size_t Bf16PackedBytes(std::size_t n, std::size_t k) {
+  return Groups(n) * Pairs(k) * kBf16UnitBytes;
+}
+
+/// Weight formats the product kernels read: Q8_0 panels, bf16 panels, or
+/// bf16 rows [n][k] as they come (row-major, k a multiple of 8).
+enum class Weights : int { kQ8 = 0, kBf16 = 1, kBf16Rows = 2 };
+
 typedef __bf16 Bf16x8 __attribute__((ext_vector_type(8)));
 typedef float F32x4 __attribute__((ext_vector_type(4)));
 

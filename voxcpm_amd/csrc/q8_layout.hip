@@ -124,6 +124,48 @@ __global__ void UnpackBf16Kernel(const std::uint8_t* packed, int n, int k,
       word;
 }
 
+// bf16 panels (q8.hpp): one thread per (unit, half, lane) gathers 16 bytes
+// of one weight row.
+__global__ void PackBf16PanelsKernel(const Bf16* rows, int n, int k, std::uint8_t* packed,
+                                     int pairs, std::size_t threads) {
+  const std::size_t index =
+      static_cast<std::size_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (index >= threads)
+    return;
+  const int lane = static_cast<int>(index % 64);
+  const int half = static_cast<int>((index / 64) % 2);
+  const std::size_t unit = index / 128;
+  const int pair = static_cast<int>(unit % pairs);
+  const int group = static_cast<int>(unit / pairs);
+  const int row = group * 16 + lane % 16;
+  const int column = 64 * pair + 32 * half + 8 * (lane / 16);
+  uint4 word{0U, 0U, 0U, 0U};
+  if (row < n && column < k)
+    word = *reinterpret_cast<const uint4*>(rows + static_cast<std::size_t>(row) * k + column);
+  *reinterpret_cast<uint4*>(packed + unit * q8::kBf16UnitBytes + half * q8::kBf16HalfBytes +
+                            16 * lane) = word;
+}
+
+// One thread per 8 values of a row.
+__global__ void UnpackBf16PanelsKernel(const std::uint8_t* packed, int n, int k, Bf16* rows,
+                                       int pairs) {
+  const std::size_t index =
+      static_cast<std::size_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  const int octets = k / 8;
+  if (index >= static_cast<std::size_t>(n) * octets)
+    return;
+  const int row = static_cast<int>(index / octets);
+  const int column = static_cast<int>(index % octets) * 8;
+  const int pair = column / 64;
+  const int half = (column % 64) / 32;
+  const int lane = 16 * ((column % 32) / 8) + row % 16;
+  const std::uint8_t* source =
+      packed + (static_cast<std::size_t>(row / 16) * pairs + pair) * q8::kBf16UnitBytes +
+      half * q8::kBf16HalfBytes + 16 * lane;
+  *reinterpret_cast<uint4*>(rows + static_cast<std::size_t>(row) * k + column) =
+      *reinterpret_cast<const uint4*>(source);
+}
+
 int CheckShape(std::size_t n, std::size_t k, const char* what) {
   if (n == 0 || k == 0 || k % 32 != 0)
     return Fail(VX_BAD_ARG, std::string(what) +
@@ -190,6 +232,39 @@ int vx_q8_unpack_bf16(const void* packed, size_t n, size_t k, uint16_t* out,
       static_cast<const std::uint8_t*>(packed), static_cast<int>(n),
       static_cast<int>(k), out, pairs);
   return vx::LaunchStatus("vx_q8_unpack_bf16");
+}
+
+size_t vx_bf16_packed_bytes(size_t n, size_t k) {
+  return vx::q8::Bf16PackedBytes(n, k);
+}
+
+int vx_bf16_pack(const uint16_t* rows, size_t n, size_t k, void* packed, void* stream) {
+  VX_TRY(vx::CheckShape(n, k, "vx_bf16_pack"));
+  if (rows == nullptr || packed == nullptr)
+    return vx::Fail(VX_BAD_ARG, "vx_bf16_pack: null pointer");
+  if (reinterpret_cast<std::uintptr_t>(packed) % 16 != 0 ||
+      reinterpret_cast<std::uintptr_t>(rows) % 16 != 0)
+    return vx::Fail(VX_BAD_ARG, "vx_bf16_pack: pointers must be 16-byte aligned");
+  const int pairs = static_cast<int>(vx::q8::Pairs(k));
+  const std::size_t threads = vx::q8::Groups(n) * pairs * 128;
+  vx::PackBf16PanelsKernel<<<vx::Grid(threads, 256), 256, 0, vx::Stream(stream)>>>(
+      rows, static_cast<int>(n), static_cast<int>(k), static_cast<std::uint8_t*>(packed),
+      pairs, threads);
+  return vx::LaunchStatus("vx_bf16_pack");
+}
+
+int vx_bf16_unpack(const void* packed, size_t n, size_t k, uint16_t* rows, void* stream) {
+  VX_TRY(vx::CheckShape(n, k, "vx_bf16_unpack"));
+  if (rows == nullptr || packed == nullptr)
+    return vx::Fail(VX_BAD_ARG, "vx_bf16_unpack: null pointer");
+  if (reinterpret_cast<std::uintptr_t>(packed) % 16 != 0 ||
+      reinterpret_cast<std::uintptr_t>(rows) % 16 != 0)
+    return vx::Fail(VX_BAD_ARG, "vx_bf16_unpack: pointers must be 16-byte aligned");
+  const int pairs = static_cast<int>(vx::q8::Pairs(k));
+  vx::UnpackBf16PanelsKernel<<<vx::Grid(n * (k / 8), 256), 256, 0, vx::Stream(stream)>>>(
+      static_cast<const std::uint8_t*>(packed), static_cast<int>(n), static_cast<int>(k),
+      rows, pairs);
+  return vx::LaunchStatus("vx_bf16_unpack");
 }
 
 }  // extern "C"

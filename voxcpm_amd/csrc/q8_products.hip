@@ -305,12 +305,12 @@ Launcher PickLauncher(int mt, int rg) {
 
 // ---- the one-pass engine on row-major activations ---------------------------
 
-template<int MT, int RG, int PW, int JR>
+template<int MT, int RG, int PW, int JR, q8::Weights WK>
 void LaunchEngine(const q8::TileArgs& args, int tiles, int waves,
                   hipStream_t stream) {
   const std::size_t shared =
       q8::EngineShared(MT, RG, waves, q8::ASource::kRowMajor, PW);
-  q8::EngineKernel<MT, RG, q8::ASource::kRowMajor, q8::Output::kStore, PW, JR>
+  q8::EngineKernel<MT, RG, q8::ASource::kRowMajor, q8::Output::kStore, PW, JR, WK>
       <<<tiles, waves * kWave, shared, stream>>>(args);
 }
 
@@ -320,42 +320,58 @@ using EngineLauncher = void (*)(const q8::TileArgs&, int, int, hipStream_t);
 /// of 8 rows; more rows load straight into the operands. One pair per wave
 /// per pass measures fastest on MI355X at every sweep shape (deeper
 /// in-flight passes need more registers and LDS and lose).
-template<int MT, int RG>
+template<int MT, int RG, q8::Weights WK>
 EngineLauncher EngineJr(int m) {
   if constexpr (q8::StagesRows(q8::ASource::kRowMajor, MT)) {
     if (m <= 16 * MT - 8)
-      return LaunchEngine<MT, RG, 1, 2 * MT - 1>;
+      return LaunchEngine<MT, RG, 1, 2 * MT - 1, WK>;
   }
-  return LaunchEngine<MT, RG, 1, 2 * MT>;
+  return LaunchEngine<MT, RG, 1, 2 * MT, WK>;
 }
 
-template<int MT>
+template<int MT, q8::Weights WK>
 EngineLauncher EngineRg(int rg, int m) {
   if constexpr (MT * 4 <= 8) {
     if (rg == 4)
-      return EngineJr<MT, 4>(m);
+      return EngineJr<MT, 4, WK>(m);
   }
   if constexpr (MT * 2 <= 8) {
     if (rg == 2)
-      return EngineJr<MT, 2>(m);
+      return EngineJr<MT, 2, WK>(m);
   }
   if (rg == 1)
-    return EngineJr<MT, 1>(m);
+    return EngineJr<MT, 1, WK>(m);
   return nullptr;
 }
 
-EngineLauncher PickEngine(int mt, int rg, int m) {
+template<q8::Weights WK>
+EngineLauncher PickEngineFor(int mt, int rg, int m) {
   switch (mt) {
-    case 1: return EngineRg<1>(rg, m);
-    case 2: return EngineRg<2>(rg, m);
-    case 3: return EngineRg<3>(rg, m);
-    case 4: return EngineRg<4>(rg, m);
-    case 5: return EngineRg<5>(rg, m);
-    case 6: return EngineRg<6>(rg, m);
-    case 7: return EngineRg<7>(rg, m);
-    case 8: return EngineRg<8>(rg, m);
+    case 1: return EngineRg<1, WK>(rg, m);
+    case 2: return EngineRg<2, WK>(rg, m);
+    case 3: return EngineRg<3, WK>(rg, m);
+    case 4: return EngineRg<4, WK>(rg, m);
+    case 5: return EngineRg<5, WK>(rg, m);
+    case 6: return EngineRg<6, WK>(rg, m);
+    case 7: return EngineRg<7, WK>(rg, m);
+    case 8: return EngineRg<8, WK>(rg, m);
     default: return nullptr;
   }
+}
+
+/// bf16 rows [n][k] are read by the staged engine only (m <= 32).
+EngineLauncher PickEngine(int mt, int rg, int m, q8::Weights kind) {
+  switch (kind) {
+    case q8::Weights::kQ8: return PickEngineFor<q8::Weights::kQ8>(mt, rg, m);
+    case q8::Weights::kBf16: return PickEngineFor<q8::Weights::kBf16>(mt, rg, m);
+    case q8::Weights::kBf16Rows:
+      if (mt == 1)
+        return EngineRg<1, q8::Weights::kBf16Rows>(rg, m);
+      if (mt == 2)
+        return EngineRg<2, q8::Weights::kBf16Rows>(rg, m);
+      return nullptr;
+  }
+  return nullptr;
 }
 
 /// Engine plan: up to 256 row groups take one per workgroup; wider products
@@ -463,11 +479,16 @@ ProductPlan PlanSkinny(std::size_t m, std::size_t k, std::size_t n,
 int RunSkinny(const Bf16* x, const void* w, float* y, Bf16* y_bf16,
               std::size_t m, std::size_t k, std::size_t n, bool accumulate,
               const ProductPlan& plan, float* partials, unsigned* counters,
-              hipStream_t stream) {
-  if (plan.tiled)  // at least 256 tiles by the plan: no split over k
-    return RunTiled(x, w, y, y_bf16, m, k, n, accumulate, true, nullptr, 0, stream);
+              hipStream_t stream, q8::Weights kind) {
+  if (plan.tiled) {  // at least 256 tiles by the plan: no split over k
+    if (kind == q8::Weights::kBf16Rows)
+      return Fail(VX_UNSUPPORTED, "bf16 rows take at most 32 activation rows");
+    return RunTiled(x, w, y, y_bf16, m, k, n, accumulate,
+                    kind == q8::Weights::kQ8 ? TiledMode::kQ8Exact : TiledMode::kBf16,
+                    nullptr, 0, stream);
+  }
   if (plan.engine) {
-    const EngineLauncher launch = PickEngine(plan.mt, plan.rg, static_cast<int>(m));
+    const EngineLauncher launch = PickEngine(plan.mt, plan.rg, static_cast<int>(m), kind);
     if (launch == nullptr)
       return Fail(VX_UNSUPPORTED, "no product engine for this plan");
     q8::TileArgs args{};
@@ -485,8 +506,10 @@ int RunSkinny(const Bf16* x, const void* w, float* y, Bf16* y_bf16,
     args.y_bf16 = y_bf16;
     args.accumulate = accumulate ? 1 : 0;
     launch(args, plan.tiles * plan.row_blocks, plan.waves, stream);
-    return LaunchStatus("q8 product");
+    return LaunchStatus(kind == q8::Weights::kQ8 ? "q8 product" : "bf16 product");
   }
+  if (kind != q8::Weights::kQ8)
+    return Fail(VX_UNSUPPORTED, "split plans take Q8_0 panels only");
   const Launcher launch = PickLauncher(plan.mt, plan.rg);
   if (launch == nullptr)
     return Fail(VX_UNSUPPORTED, "no product kernel for this plan");

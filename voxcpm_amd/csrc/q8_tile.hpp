@@ -220,11 +220,13 @@ __device__ inline std::uint32_t BufferLoad4(__amdgpu_buffer_rsrc_t buffer, std::
       buffer, static_cast<int>(keep ? offset : kPastBuffer), 0, 0));
 }
 
-/// One pair's operands in flight: RG weight fragments with their scale
-/// pairs, and the MT x 2 activation fragments.
+/// One pair's operands in flight: RG weight fragments (Q8_0: both blocks'
+/// values and the scale pairs; bf16: `w` and `w2`, one block each), and
+/// the MT x 2 activation fragments.
 template<int MT, int RG>
 struct PairStage {
   uint4 w[RG];
+  uint4 w2[RG];
   std::uint32_t scales[RG];
   uint4 a[MT][2];
 };
@@ -232,8 +234,12 @@ struct PairStage {
 /// The engine. Grid: one workgroup per tile (RG row groups); blockDim.x =
 /// EngineThreads(MT, RG) (waves without pairs add zeros). PW pairs per wave
 /// per pass; kNormF32 needs every pair in one pass (pairs <= waves * PW).
-/// Staged row-major sources load JR groups of 8 rows (8 JR >= m).
-template<int MT, int RG, ASource SRC, Output OUT, int PW = 1, int JR = 2 * MT>
+/// Staged row-major sources load JR groups of 8 rows (8 JR >= m). WK: the
+/// weights' format; bf16 weights (panels or rows [n][k]) accumulate each
+/// block's MFMA straight into the sums, as the reference's bf16 products do
+/// (kernels/wmma_products.hip:210-213).
+template<int MT, int RG, ASource SRC, Output OUT, int PW = 1, int JR = 2 * MT,
+         Weights WK = Weights::kQ8>
 __device__ __forceinline__ void EngineBody(const TileArgs& a) {
   // One 16-row tile of a fragment-order source per workgroup.
   constexpr bool kOneTile = MT == 1 && SRC == ASource::kFragBf16;
@@ -266,11 +272,14 @@ __device__ __forceinline__ void EngineBody(const TileArgs& a) {
   const auto in_rows = [&](int row) { return row >= row_lo && row < row_hi; };
   const int k_blocks = a.k / 32;
 
+  constexpr int kUnit = WK == Weights::kQ8 ? kUnitBytes : kBf16UnitBytes;
   const std::uint8_t* unit[RG];
+  int first_row[RG];  // bf16 rows: the group's first weight row
 #pragma unroll
   for (int r = 0; r < RG; ++r) {
     const int g = min(RgGroup(tile, r, a.group_stride, RG), a.groups - 1);
-    unit[r] = a.w + static_cast<std::size_t>(g) * a.pairs * kUnitBytes;
+    unit[r] = a.w + static_cast<std::size_t>(g) * a.pairs * kUnit;
+    first_row[r] = 16 * g;
   }
   bool row_ok[MT];
 #pragma unroll
@@ -320,13 +329,30 @@ __device__ __forceinline__ void EngineBody(const TileArgs& a) {
 
   // Pairs past k load pair 0's unit, branch-free: their stages are never
   // multiplied.
+  // bf16 rows [n][k]: a buffer over the matrix, rows past n and columns
+  // past k masked.
+  const __amdgpu_buffer_rsrc_t row_buffer =
+      BufferOf(a.w, WK == Weights::kBf16Rows
+                        ? 2U * static_cast<std::uint32_t>(a.n) * static_cast<std::uint32_t>(a.k)
+                        : 0U);
   const auto load_weights = [&](int pair, PairStage<MT, RG>& s) {
     const bool ok = pair < a.pairs;
 #pragma unroll
     for (int r = 0; r < RG; ++r) {
-      const std::uint8_t* u = unit[r] + static_cast<std::size_t>(ok ? pair : 0) * kUnitBytes;
-      s.w[r] = *reinterpret_cast<const uint4*>(u + 16 * lane);
-      s.scales[r] = *reinterpret_cast<const std::uint32_t*>(u + kValueBytes + 4 * r16);
+      if constexpr (WK == Weights::kBf16Rows) {
+        const int row = first_row[r] + r16;
+        const int column = 64 * pair + 8 * octet;
+        const std::uint32_t at = 2U * static_cast<std::uint32_t>(row * a.k + column);
+        s.w[r] = BufferLoad16(row_buffer, at, ok && row < a.n && column < a.k);
+        s.w2[r] = BufferLoad16(row_buffer, at + 64U, ok && row < a.n && column + 32 < a.k);
+      } else {
+        const std::uint8_t* u = unit[r] + static_cast<std::size_t>(ok ? pair : 0) * kUnit;
+        s.w[r] = *reinterpret_cast<const uint4*>(u + 16 * lane);
+        if constexpr (WK == Weights::kQ8)
+          s.scales[r] = *reinterpret_cast<const std::uint32_t*>(u + kValueBytes + 4 * r16);
+        else
+          s.w2[r] = *reinterpret_cast<const uint4*>(u + kBf16HalfBytes + 16 * lane);
+      }
     }
   };
   const auto load_activations = [&](int pair, PairStage<MT, RG>& s) {
@@ -402,6 +428,16 @@ __device__ __forceinline__ void EngineBody(const TileArgs& a) {
 
   const auto multiply = [&](const PairStage<MT, RG>& s) {
     const F32x4 zero{0.0F, 0.0F, 0.0F, 0.0F};
+    if constexpr (WK != Weights::kQ8) {
+#pragma unroll
+      for (int r = 0; r < RG; ++r)
+#pragma unroll
+        for (int t = 0; t < MT; ++t) {
+          acc[r][t] = Mfma16x16x32(AsBf16x8(s.a[t][0]), AsBf16x8(s.w[r]), acc[r][t]);
+          acc[r][t] = Mfma16x16x32(AsBf16x8(s.a[t][1]), AsBf16x8(s.w2[r]), acc[r][t]);
+        }
+      return;
+    }
 #pragma unroll
     for (int r = 0; r < RG; ++r) {
       const Bf16x8 b0 = Int8x8ToBf16(s.w[r].x, s.w[r].y);
@@ -619,9 +655,10 @@ __device__ __forceinline__ void EngineBody(const TileArgs& a) {
   }
 }
 
-template<int MT, int RG, ASource SRC, Output OUT, int PW = 1, int JR = 2 * MT>
+template<int MT, int RG, ASource SRC, Output OUT, int PW = 1, int JR = 2 * MT,
+         Weights WK = Weights::kQ8>
 __global__ __launch_bounds__(EngineThreads(MT, RG)) void EngineKernel(TileArgs a) {
-  EngineBody<MT, RG, SRC, OUT, PW, JR>(a);
+  EngineBody<MT, RG, SRC, OUT, PW, JR, WK>(a);
 }
 
 }  // namespace vx::q8

@@ -1,5 +1,5 @@
-// Q8_0 x bfloat16 products of more than 32 activation rows on gfx950's
-// matrix cores: LDS-tiled, BM activation rows x 128 weight rows per
+// Q8_0 (or bf16) x bfloat16 products of more than 32 activation rows on
+// gfx950's matrix cores: LDS-tiled, BM activation rows x 128 weight rows per
 // workgroup, 64 columns (one panel pair, two Q8_0 blocks) per step.
 //
 // Two arithmetics, as the reference dispatches them (gemm.cpp:259-313):
@@ -11,6 +11,9 @@
 //    kernels/wmma_products.hip:94-112): every weight becomes
 //    bf16_rne(f32(f16 scale) * q) once per workgroup and step, and the MFMAs
 //    accumulate over all of k in float32.
+// bf16 panels (kernels/wmma_products.hip:210-213, the WmmaBf16 products)
+// take the expanded path's MFMA accumulation with the weights copied as
+// they are.
 //
 // Per step the threads load the step after next into registers (two
 // register sets, so a load has two steps of MFMAs to arrive), convert the
@@ -98,8 +101,13 @@ struct TileShape {
   static constexpr int kMinBlocks = MINB;
 };
 
-template<class T, bool EXACT>
+/// MODE: TiledMode (products.hpp) as an int: 0 Q8_0 exact, 1 Q8_0
+/// expanded, 2 bf16 panels.
+template<class T, int MODE>
 __global__ __launch_bounds__(T::kThreads, T::kMinBlocks) void TiledKernel(TiledArgs a) {
+  constexpr bool EXACT = MODE == 0;
+  constexpr bool BF16 = MODE == 2;
+  constexpr int kUnit = BF16 ? q8::kBf16UnitBytes : kUnitBytes;
   constexpr int BM = T::kBm;
   constexpr int kThreads = T::kThreads;
   constexpr int kAPieces = T::kAPieces;
@@ -125,7 +133,7 @@ __global__ __launch_bounds__(T::kThreads, T::kMinBlocks) void TiledKernel(TiledA
   const int first_pair = split * a.pairs_per_split;
   const int steps = min(a.pairs, first_pair + a.pairs_per_split) - first_pair;
   // The tile's panel groups as one buffer (under 2^31 bytes for k <= 2^22).
-  const std::uint32_t group_bytes = static_cast<std::uint32_t>(a.pairs) * kUnitBytes;
+  const std::uint32_t group_bytes = static_cast<std::uint32_t>(a.pairs) * kUnit;
   const __amdgpu_buffer_rsrc_t w_buffer =
       q8::BufferOf(a.w + static_cast<std::size_t>(group0) * group_bytes,
                    static_cast<std::uint32_t>(min(kTileN / 16, a.groups - group0)) * group_bytes);
@@ -133,6 +141,7 @@ __global__ __launch_bounds__(T::kThreads, T::kMinBlocks) void TiledKernel(TiledA
   struct Staging {
     uint4 x[kAPieces];
     uint4 w[kUnits];
+    uint4 w2[kUnits];  // bf16: the pair's second block
     std::uint32_t scales[kUnits];
   };
   // Every step issues the same loads, steps past the split's end included:
@@ -156,9 +165,12 @@ __global__ __launch_bounds__(T::kThreads, T::kMinBlocks) void TiledKernel(TiledA
       const int group = min(kUnits * wave + u, a.groups - 1 - group0);
       const std::uint32_t unit =
           static_cast<std::uint32_t>(group) * group_bytes +
-          static_cast<std::uint32_t>(live ? pair : 0) * kUnitBytes;
+          static_cast<std::uint32_t>(live ? pair : 0) * kUnit;
       s.w[u] = q8::BufferLoad16(w_buffer, unit + 16 * lane, live);
-      s.scales[u] = q8::BufferLoad4(w_buffer, unit + kValueBytes + 4 * r16, live);
+      if constexpr (BF16)
+        s.w2[u] = q8::BufferLoad16(w_buffer, unit + q8::kBf16HalfBytes + 16 * lane, live);
+      else
+        s.scales[u] = q8::BufferLoad4(w_buffer, unit + kValueBytes + 4 * r16, live);
     }
   };
   const auto store = [&](int buffer, const Staging& s) {
@@ -173,7 +185,10 @@ __global__ __launch_bounds__(T::kThreads, T::kMinBlocks) void TiledKernel(TiledA
       const float s0 = HalfValue(static_cast<std::uint16_t>(s.scales[u] & 0xFFFFU));
       const float s1 = HalfValue(static_cast<std::uint16_t>(s.scales[u] >> 16));
       uint4 first, second;
-      if constexpr (EXACT) {
+      if constexpr (BF16) {
+        first = s.w[u];
+        second = s.w2[u];
+      } else if constexpr (EXACT) {
         first = __builtin_bit_cast(uint4, Int8x8ToBf16(s.w[u].x, s.w[u].y));
         second = __builtin_bit_cast(uint4, Int8x8ToBf16(s.w[u].z, s.w[u].w));
         if (octet == 0) {
@@ -318,9 +333,9 @@ __global__ __launch_bounds__(256) void ReduceSplitsKernel(TiledArgs a) {
   }
 }
 
-template<class T, bool EXACT>
+template<class T, int MODE>
 void Launch(const TiledArgs& args, hipStream_t stream) {
-  TiledKernel<T, EXACT>
+  TiledKernel<T, MODE>
       <<<args.m_tiles * args.n_tiles * args.splits, T::kThreads, 0, stream>>>(args);
   if (args.splits > 1) {
     const std::size_t quads = (static_cast<std::size_t>(args.m) * args.n + 3) / 4;
@@ -334,7 +349,7 @@ using Large = TileShape<128, 4, 2, 1>;
 }  // namespace
 
 int RunTiled(const Bf16* x, const void* w, float* y, Bf16* y_bf16, std::size_t m,
-             std::size_t k, std::size_t n, bool accumulate, bool exact,
+             std::size_t k, std::size_t n, bool accumulate, TiledMode mode,
              float* partials, std::size_t partial_floats, hipStream_t stream) {
   TiledArgs args;
   args.x = x;
@@ -365,18 +380,18 @@ int RunTiled(const Bf16* x, const void* w, float* y, Bf16* y_bf16, std::size_t m
     args.splits *= 2;
   args.pairs_per_split = (args.pairs + args.splits - 1) / args.splits;
   args.partials = partials;
-  if (bm == 64) {
-    if (exact)
-      Launch<Small, true>(args, stream);
-    else
-      Launch<Small, false>(args, stream);
-  } else {
-    if (exact)
-      Launch<Large, true>(args, stream);
-    else
-      Launch<Large, false>(args, stream);
+  switch (mode) {
+    case TiledMode::kQ8Exact:
+      bm == 64 ? Launch<Small, 0>(args, stream) : Launch<Large, 0>(args, stream);
+      return LaunchStatus("q8 tiled product");
+    case TiledMode::kQ8Expanded:
+      bm == 64 ? Launch<Small, 1>(args, stream) : Launch<Large, 1>(args, stream);
+      return LaunchStatus("q8 expanded product");
+    case TiledMode::kBf16:
+      bm == 64 ? Launch<Small, 2>(args, stream) : Launch<Large, 2>(args, stream);
+      return LaunchStatus("bf16 tiled product");
   }
-  return LaunchStatus(exact ? "q8 tiled product" : "q8 expanded product");
+  return Fail(VX_BAD_ARG, "tiled product: unknown mode");
 }
 
 }  // namespace vx

@@ -16,7 +16,8 @@ from ._lib import DitLayer, DitProjection, DitShape, DitWeights, check, lib
 
 __all__ = [
     "Scratch", "Dit", "q8_pack", "q8_unpack_blocks", "q8_unpack_bf16",
-    "q8_linear", "q8_linear_bf16", "q8_plan", "stream_read", "euler_schedule", "rope_table",
+    "q8_linear", "q8_linear_bf16", "q8_plan", "bf16_pack", "bf16_unpack", "bf16_linear",
+    "bf16_linear_rows", "stream_read", "euler_schedule", "rope_table",
 ]
 
 
@@ -111,6 +112,48 @@ def q8_linear_bf16(x: torch.Tensor, packed: torch.Tensor, n: int,
     handle = scratch.handle if scratch is not None else None
     check(lib().vx_q8_linear_bf16(_ptr(x), _ptr(packed), _ptr(y), m, k, n,
                                   handle, _stream(stream)))
+    return y
+
+
+# ---- bf16 weights -----------------------------------------------------------
+
+def bf16_pack(rows: torch.Tensor, stream=None) -> torch.Tensor:
+    """bf16 weight rows [n][k] (on the device) -> panels."""
+    n, k = rows.shape
+    packed = torch.empty(lib().vx_bf16_packed_bytes(n, k), dtype=torch.uint8,
+                         device=rows.device)
+    check(lib().vx_bf16_pack(_ptr(rows), n, k, _ptr(packed), _stream(stream)))
+    return packed
+
+
+def bf16_unpack(packed: torch.Tensor, n: int, k: int, stream=None) -> torch.Tensor:
+    rows = torch.empty((n, k), dtype=torch.bfloat16, device=packed.device)
+    check(lib().vx_bf16_unpack(_ptr(packed), n, k, _ptr(rows), _stream(stream)))
+    return rows
+
+
+def bf16_linear(x: torch.Tensor, packed: torch.Tensor, n: int,
+                y: torch.Tensor | None = None, accumulate: bool = False,
+                scratch: Scratch | None = None, stream=None) -> torch.Tensor:
+    """y[m][n] (+)= x[m][k] W^T on bf16 panels; x bf16 [m][k], y float32."""
+    m, k = x.shape
+    if y is None:
+        y = torch.empty((m, n), dtype=torch.float32, device=x.device)
+    handle = scratch.handle if scratch is not None else None
+    check(lib().vx_bf16_linear(_ptr(x), _ptr(packed), _ptr(y), m, k, n,
+                               int(accumulate), handle, _stream(stream)))
+    return y
+
+
+def bf16_linear_rows(x: torch.Tensor, w: torch.Tensor, y: torch.Tensor | None = None,
+                     accumulate: bool = False, stream=None) -> torch.Tensor:
+    """y[m][n] (+)= x[m][k] W^T on bf16 rows W [n][k], m <= 32."""
+    m, k = x.shape
+    n = w.shape[0]
+    if y is None:
+        y = torch.empty((m, n), dtype=torch.float32, device=x.device)
+    check(lib().vx_bf16_linear_rows(_ptr(x), _ptr(w), _ptr(y), m, k, n,
+                                    int(accumulate), _stream(stream)))
     return y
 
 
