@@ -187,6 +187,43 @@ def gpu_products(args, torch, ops, synth, device, stream):
     return result
 
 
+def gpu_bf16(args, torch, ops, synth, device, stream):
+    """The sweep shapes at M=22 on bf16 weights (2 N K bytes): panels
+    (vx_bf16_linear) and rows as they come (vx_bf16_linear_rows), rotated
+    over >= 1 GiB per shape and replayed from HIP graphs."""
+    scratch = ops.Scratch(128, 16384)
+    rows = []
+    for k, n in SWEEP_SHAPES:
+        rng = synth.Rng(2, k * 31 + n)
+        w = torch.from_numpy(synth.bf16_bits(rng.normal(n * k).astype(np.float32))
+                             .view(np.int16).reshape(n, k)).to(device).view(torch.bfloat16)
+        x = torch.from_numpy(synth.activations(rng, ROWS, k).view(np.int16)).to(device) \
+            .view(torch.bfloat16)
+        y = torch.empty((ROWS, n), dtype=torch.float32, device=device)
+        weight_bytes = 2 * n * k
+        copies = max(8, int(np.ceil(ROTATION_BYTES / weight_bytes)))
+        entry = {"m": ROWS, "k": k, "n": n, "bytes": weight_bytes}
+        packed = ops.bf16_pack(w)
+        for name, pool, call in (
+                ("panels", packed.repeat(copies).view(copies, -1),
+                 lambda i, pool: ops.bf16_linear(x, pool[i % copies], n, y=y, scratch=scratch)),
+                ("rows", w.repeat(copies, 1).view(copies, n, k),
+                 lambda i, pool: ops.bf16_linear_rows(x, pool[i % copies], y=y))):
+            count = max(copies, 64)
+            g = graph_of(torch, stream, lambda i, pool=pool, call=call: call(i, pool), count)
+            g.replay()
+            us = time_graph(torch, stream, g) / count * 1e6
+            entry[f"us_{name}"] = round(us, 3)
+            entry[f"gbs_{name}"] = round(weight_bytes / us / 1e3, 1)
+            del g, pool
+            torch.cuda.empty_cache()
+        log(f"  bf16 M=22 K={k} N={n}: panels {entry['us_panels']} us "
+            f"({entry['gbs_panels']} GB/s), rows {entry['us_rows']} us "
+            f"({entry['gbs_rows']} GB/s)")
+        rows.append(entry)
+    return rows
+
+
 def gpu_prefill(args, torch, ops, synth, device, stream):
     """Prefill-sized Q8_0 products (m > 128, matrix-core bound): TFLOP/s of
     2 m n k per launch, launches replayed from a HIP graph over a few
@@ -392,6 +429,8 @@ def main() -> int:
                         help="skip the CPU baseline")
     parser.add_argument("--no-patch", action="store_true",
                         help="skip the DiT patch measurement")
+    parser.add_argument("--no-bf16", action="store_true",
+                        help="skip the bf16-weight products")
     parser.add_argument("--no-prefill", action="store_true",
                         help="skip the prefill-sized products")
     parser.add_argument("--pmc-workload", action="store_true",
@@ -421,6 +460,7 @@ def main() -> int:
     probe = read_probe(torch, device, stream)
     log(f"read probe {probe:.0f} GB/s")
     products = gpu_products(args, torch, ops, synth, device, stream)
+    bf16 = None if args.no_bf16 else gpu_bf16(args, torch, ops, synth, device, stream)
     prefill = None if args.no_prefill else gpu_prefill(args, torch, ops, synth, device, stream)
     patch = None if args.no_patch else gpu_patch(args, torch, ops, synth, device, stream)
     baseline = None
@@ -475,6 +515,7 @@ def main() -> int:
         "cpu_baseline": baseline,
         "read_probe_gbs": round(probe, 1),
         "sweep": products["sweep"],
+        "bf16_weights": bf16,
         "prefill": prefill,
         "patch": patch,
     }

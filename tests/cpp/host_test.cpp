@@ -192,12 +192,56 @@ void TestLinear(std::size_t in, std::size_t out, Random& rng,
   // A format this build does not serve throws GpuError.
   bool threw = false;
   try {
-    gemm.Linear(nullptr, vc::Matrix{vc::WeightFormat::kBf16, packed.get()},
+    gemm.Linear(nullptr, vc::Matrix{vc::WeightFormat::kBf16Tiles, packed.get()},
                 nullptr, 1, in, out, false);
   } catch (const vc::GpuError&) {
     threw = true;
   }
   Report(threw, "unsupported weight format throws GpuError");
+}
+
+/// Bf16Gemm::Linear on bf16 weights, as panels and as rows, at rows 1, 22,
+/// 40 and 130 (products_test.cpp:256-313 with kBf16Tiles): the bf16
+/// expansion of Q8_0 weights, error relative to sum |x w| <= 1e-5.
+void TestLinearBf16(std::size_t in, std::size_t out, Random& rng,
+                    hipStream_t stream) {
+  const auto blocks = Weights(out, in, rng);
+  std::vector<std::uint16_t> w(out * in);
+  vo_q8_dequant_bf16(blocks.data(), out, in, w.data());
+  const auto rows_w = Upload(w);
+  vc::DeviceBuffer<std::uint8_t> panels(vx_bf16_packed_bytes(out, in));
+  vc::CheckVx(vx_bf16_pack(rows_w.get(), out, in, panels.get(), nullptr), "pack");
+  vc::Check(hipDeviceSynchronize(), "sync");
+  vc::Bf16Gemm gemm(nullptr, stream);
+  for (const vc::WeightFormat format : {vc::WeightFormat::kBf16Panels, vc::WeightFormat::kBf16}) {
+    const vc::Matrix matrix{format, format == vc::WeightFormat::kBf16
+                                        ? static_cast<const void*>(rows_w.get())
+                                        : static_cast<const void*>(panels.get())};
+    for (const std::size_t rows : {1, 22, 40, 130}) {
+      const auto x = Activations(rows, in, rng, 2.0);
+      const auto x_device = Upload(x);
+      std::vector<float> before(rows * out);
+      for (auto& v : before)
+        v = static_cast<float>(rng.Normal());
+      vc::DeviceBuffer<float> y(rows * out);
+      for (const bool accumulate : {false, true}) {
+        vc::Check(hipMemcpy(y.get(), before.data(), before.size() * sizeof(float),
+                            hipMemcpyHostToDevice),
+                  "upload");
+        gemm.Linear(x_device.get(), matrix, y.get(), rows, in, out, accumulate);
+        vc::Check(hipStreamSynchronize(stream), "sync");
+        const auto result = Download(y.get(), y.size());
+        const double worst = vo_bf16_check(result.data(), x.data(), w.data(),
+                                           accumulate ? before.data() : nullptr, rows, in, out);
+        Report(worst <= 1e-5,
+               std::string("linear bf16 ") +
+                   (format == vc::WeightFormat::kBf16 ? "rows" : "panels") + " rows " +
+                   std::to_string(rows) + " in " + std::to_string(in) + " out " +
+                   std::to_string(out) + (accumulate ? " (accumulate)" : "") + ": worst " +
+                   Scientific(worst));
+      }
+    }
+  }
 }
 
 /// A small DiT of the released model's shape (GQA, head_dim 128, LongRoPE
@@ -390,6 +434,7 @@ int main() {
     Random rng(1234);
     TestLinear(1024, 2560, rng, stream);
     TestLinear(4096, 1024, rng, stream);
+    TestLinearBf16(1024, 2560, rng, stream);
     TestGenerator(rng);
     vc::Check(hipStreamDestroy(stream), "stream");
   } catch (const std::exception& failure) {

@@ -13,8 +13,28 @@ struct Bf16Gemm::State {
   vx_scratch* scratch = nullptr;
   std::size_t rows = 0;
   std::size_t out = 0;
+  // bf16 rows packed into panels for products of more than 32 rows (the
+  // reference's `unpacked` buffer, gemm.cpp:99).
+  void* panels = nullptr;
+  std::size_t panel_bytes = 0;
 
-  ~State() { vx_scratch_destroy(scratch); }
+  ~State() {
+    vx_scratch_destroy(scratch);
+    if (panels != nullptr)
+      (void)hipFree(panels);
+  }
+
+  void* Panels(std::size_t bytes) {
+    if (bytes > panel_bytes) {
+      if (panels != nullptr)
+        Check(hipFree(panels), "hipFree");
+      panels = nullptr;
+      panel_bytes = 0;
+      Check(hipMalloc(&panels, bytes), "hipMalloc");
+      panel_bytes = bytes;
+    }
+    return panels;
+  }
 
   vx_scratch* Reserve(std::size_t want_rows, std::size_t want_out) {
     if (want_rows > 128)
@@ -38,12 +58,36 @@ Bf16Gemm::~Bf16Gemm() = default;
 void Bf16Gemm::Linear(const void* x, const Matrix& w, float* y,
                       std::size_t rows, std::size_t in, std::size_t out,
                       bool accumulate) {
-  if (w.format != WeightFormat::kQ8Panels)
-    throw GpuError("Bf16Gemm::Linear: this build serves Q8_0 panels only");
-  vx_scratch* scratch = state_->Reserve(rows, out);
-  CheckVx(vx_q8_linear(static_cast<const std::uint16_t*>(x), w.data, y, rows,
-                       in, out, accumulate ? 1 : 0, scratch, stream_),
-          "Bf16Gemm::Linear");
+  const auto* activations = static_cast<const std::uint16_t*>(x);
+  switch (w.format) {
+    case WeightFormat::kQ8Panels:
+      CheckVx(vx_q8_linear(activations, w.data, y, rows, in, out, accumulate ? 1 : 0,
+                           state_->Reserve(rows, out), stream_),
+              "Bf16Gemm::Linear");
+      return;
+    case WeightFormat::kBf16Panels:
+      CheckVx(vx_bf16_linear(activations, w.data, y, rows, in, out, accumulate ? 1 : 0,
+                             state_->Reserve(rows, out), stream_),
+              "Bf16Gemm::Linear");
+      return;
+    case WeightFormat::kBf16: {
+      const auto* rows_w = static_cast<const std::uint16_t*>(w.data);
+      if (rows <= 32) {
+        CheckVx(vx_bf16_linear_rows(activations, rows_w, y, rows, in, out, accumulate ? 1 : 0,
+                                    stream_),
+                "Bf16Gemm::Linear");
+        return;
+      }
+      void* panels = state_->Panels(vx_bf16_packed_bytes(out, in));
+      CheckVx(vx_bf16_pack(rows_w, out, in, panels, stream_), "Bf16Gemm::Linear");
+      CheckVx(vx_bf16_linear(activations, panels, y, rows, in, out, accumulate ? 1 : 0,
+                             state_->Reserve(rows, out), stream_),
+              "Bf16Gemm::Linear");
+      return;
+    }
+    default:
+      throw GpuError("Bf16Gemm::Linear: the gfx11 tile formats are not served by this build");
+  }
 }
 
 }  // namespace gufo::models::voxcpm

@@ -17,8 +17,11 @@ namespace gufo::models::voxcpm {
 /// accumulation and output. Q8_0 panels up to 128 rows keep the Q8_0
 /// arithmetic exact (a float32 sum per block, scaled per block); more rows
 /// use bf16(scale * q) as the reference's expansion does, on the matrix
-/// cores without leaving Q8_0 in HBM. Other formats are not served by this
-/// build and throw GpuError.
+/// cores without leaving Q8_0 in HBM. bf16 panels and bf16 rows sum the
+/// blocks' products on the matrix cores (bf16 rows beyond 32 activation
+/// rows are packed into panels in the operator's scratch first, where the
+/// reference unpacks for hipBLASLt, gemm.cpp:296-303). The reference's gfx11
+/// tile formats are not served and throw GpuError.
 class Bf16Gemm {
 public:
   /// `fallback` is accepted for the reference's signature (gemm.hpp:51)

@@ -9,10 +9,11 @@ namespace gufo::models::voxcpm {
 
 /// How a weight matrix is stored on the device.
 enum class WeightFormat : std::uint8_t {
-  kBf16,       // bfloat16 [out][in], row-major (not served by this build)
-  kBf16Tiles,  // the reference's gfx11 bfloat16 tiles (not served)
-  kQ8Tiles,    // the reference's gfx11 Q8_0 tiles (not served)
-  kQ8Panels,   // GGML Q8_0 in gfx950 MFMA panels (vx_q8_pack)
+  kBf16,        // bfloat16 [out][in], row-major
+  kBf16Tiles,   // the reference's gfx11 bfloat16 tiles (not served)
+  kQ8Tiles,     // the reference's gfx11 Q8_0 tiles (not served)
+  kQ8Panels,    // GGML Q8_0 in gfx950 MFMA panels (vx_q8_pack)
+  kBf16Panels,  // bfloat16 in gfx950 MFMA panels (vx_bf16_pack)
 };
 
 /// A weight matrix [out][in] on the device.
