@@ -331,6 +331,20 @@ def gpu_patch(args, torch, ops, synth, device, stream):
     dit.status()
     persistent_us = start.elapsed_time(stop) * 1e3 / patches
     dit.set_path(_lib.DIT_PATH_AUTO)
+    dit.close()
+    # The same DiT on bf16 weights (bf16(scale q) panels, twice the bytes).
+    dit_bf16 = ops.Dit(weights, device, stream, bf16_weights=True)
+    for _ in range(2):
+        dit_bf16.patch(mu, cond, x, t, dt, evaluate, config.cfg, config.zero_star)
+    torch.cuda.synchronize()
+    start.record(stream)
+    for _ in range(patches):
+        dit_bf16.patch(mu, cond, x, t, dt, evaluate, config.cfg, config.zero_star)
+    stop.record(stream)
+    stop.synchronize()
+    dit_bf16.status()
+    bf16_us = start.elapsed_time(stop) * 1e3 / patches
+    dit_bf16.close()
     # Algorithmic bytes of a patch: 10 evaluations x 12 blocks of weights,
     # in/out projections per evaluation and cond_proj once; the time MLP is
     # cached per t and not counted.
@@ -341,11 +355,11 @@ def gpu_patch(args, torch, ops, synth, device, stream):
     patch_bytes = evaluations * (config.layers * block + io) + q8_bytes(config.feat, config.hidden)
     log(f"patch: {warm_us:.1f} us warm, {cold_us:.1f} us cold "
         f"({patch_bytes / 1e6:.1f} MB of weights per patch); "
-        f"persistent evaluation {persistent_us:.1f} us")
-    dit.close()
+        f"persistent evaluation {persistent_us:.1f} us; bf16 weights {bf16_us:.1f} us warm")
     gpu_patch.weights = weights
     return {"us_warm": round(warm_us, 2), "us_cold": round(cold_us, 2),
             "us_warm_persistent": round(persistent_us, 2),
+            "us_warm_bf16_weights": round(bf16_us, 2),
             "patches_timed": patches, "evaluations": evaluations,
             "bytes": patch_bytes,
             "gbs_warm": round(patch_bytes / warm_us / 1e3, 1),

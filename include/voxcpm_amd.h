@@ -214,7 +214,7 @@ typedef struct vx_dit_shape {
 } vx_dit_shape;
 
 typedef struct vx_dit_projection {
-  const void* weight;   /* Q8_0 panels [out][in] */
+  const void* weight;   /* panels [out][in] (Q8_0 or bf16, `format`) */
   const uint16_t* bias; /* bf16 [out], or NULL */
 } vx_dit_projection;
 
@@ -228,6 +228,14 @@ typedef struct vx_dit_layer {
   const void* down;           /* panels [hidden][ffn] */
 } vx_dit_layer;
 
+/* The format of every matrix of a DiT (vx_dit_weights.format): Q8_0
+ * panels (vx_q8_pack) or bf16 panels (vx_bf16_pack), as the reference's
+ * StackWeights hold kQ8Tiles or kBf16Tiles (weights.cpp:281-292). */
+typedef enum vx_weight_format {
+  VX_WEIGHTS_Q8_0 = 0,
+  VX_WEIGHTS_BF16 = 1
+} vx_weight_format;
+
 typedef struct vx_dit_weights {
   const vx_dit_layer* layers; /* host array of `layers` entries */
   const uint16_t* norm;       /* final norm, bf16 [hidden] */
@@ -240,6 +248,9 @@ typedef struct vx_dit_weights {
   vx_dit_projection time_2;   /* hidden -> hidden */
   vx_dit_projection delta_1;  /* time_in -> hidden (has_delta) */
   vx_dit_projection delta_2;  /* hidden -> hidden (has_delta) */
+  uint32_t format;            /* vx_weight_format of every matrix above (0:
+                                 Q8_0 panels; the persistent path takes
+                                 Q8_0 only) */
 } vx_dit_weights;
 
 typedef struct vx_dit vx_dit;

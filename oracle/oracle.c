@@ -111,13 +111,40 @@ void vo_q8_values(const uint8_t* blocks, size_t n, size_t k, double* output) {
 
 typedef struct linear_job {
   const uint16_t* x;
-  const uint8_t* blocks;
+  const uint8_t* blocks; /* Q8_0 blocks, or NULL for bf16 rows */
+  const uint16_t* w16;   /* bf16 rows [n][k] */
   float* y;
   size_t m, k, n, first, last;
   int accumulate;
 } linear_job;
 
+/* kernels/wmma_products.hip:210-213: a float32 sum per 16-column chunk
+ * (one WMMA step) added into the accumulator in k order. */
+static void bf16_columns(const linear_job* job) {
+  const size_t k = job->k;
+  for (size_t row = 0; row < job->m; ++row) {
+    const uint16_t* xr = job->x + row * k;
+    for (size_t col = job->first; col < job->last; ++col) {
+      const uint16_t* wr = job->w16 + col * k;
+      float acc = 0.0f;
+      for (size_t c0 = 0; c0 < k; c0 += 16) {
+        const size_t c1 = c0 + 16 < k ? c0 + 16 : k;
+        float chunk = 0.0f;
+        for (size_t c = c0; c < c1; ++c)
+          chunk += vo_bf16_value(xr[c]) * vo_bf16_value(wr[c]);
+        acc += chunk;
+      }
+      float* target = job->y + row * job->n + col;
+      *target = job->accumulate ? *target + acc : acc;
+    }
+  }
+}
+
 static void linear_columns(const linear_job* job) {
+  if (job->blocks == NULL) {
+    bf16_columns(job);
+    return;
+  }
   const size_t per_row = job->k / 32;
   float xs[32];
   for (size_t row = 0; row < job->m; ++row) {
@@ -146,8 +173,24 @@ static void* linear_thread(void* argument) {
   return NULL;
 }
 
+static void run_linear(linear_job base, int threads);
+
 void vo_q8_linear(const uint16_t* x, const uint8_t* blocks, float* y, size_t m,
                   size_t k, size_t n, int accumulate, int threads) {
+  const linear_job base = {x, blocks, NULL, y, m, k, n, 0, 0, accumulate};
+  run_linear(base, threads);
+}
+
+void vo_bf16_linear(const uint16_t* x, const uint16_t* w, float* y, size_t m,
+                    size_t k, size_t n, int accumulate, int threads) {
+  const linear_job base = {x, NULL, w, y, m, k, n, 0, 0, accumulate};
+  run_linear(base, threads);
+}
+
+/* Columns n split over `threads` POSIX threads: identical results for any
+ * count. */
+static void run_linear(linear_job base, int threads) {
+  const size_t n = base.n;
   if (threads < 1)
     threads = 1;
   if ((size_t)threads > n)
@@ -159,8 +202,9 @@ void vo_q8_linear(const uint16_t* x, const uint8_t* blocks, float* y, size_t m,
   const size_t chunk = (n + (size_t)threads - 1) / (size_t)threads;
   int started = 0;
   for (int t = 0; t < threads; ++t) {
-    linear_job job = {x, blocks, y, m, k, n, (size_t)t * chunk,
-                      (size_t)(t + 1) * chunk, accumulate};
+    linear_job job = base;
+    job.first = (size_t)t * chunk;
+    job.last = (size_t)(t + 1) * chunk;
     if (job.last > n)
       job.last = n;
     if (job.first >= job.last)
@@ -207,26 +251,6 @@ double vo_q8_check(const float* y, const uint16_t* x, const uint8_t* blocks,
 }
 
 /* ---- bfloat16 weights --------------------------------------------------- */
-
-void vo_bf16_linear(const uint16_t* x, const uint16_t* w, float* y, size_t m,
-                    size_t k, size_t n, int accumulate) {
-  /* kernels/wmma_products.hip:210-213 (acc = Wmma(a0, b0, acc);
-   * acc = Wmma(a1, b1, acc) per 32-column block: 16 columns per step) */
-  for (size_t row = 0; row < m; ++row) {
-    for (size_t col = 0; col < n; ++col) {
-      float acc = 0.0f;
-      for (size_t c0 = 0; c0 < k; c0 += 16) {
-        float chunk = 0.0f;
-        const size_t c1 = c0 + 16 < k ? c0 + 16 : k;
-        for (size_t c = c0; c < c1; ++c)
-          chunk += vo_bf16_value(x[row * k + c]) * vo_bf16_value(w[col * k + c]);
-        acc += chunk;
-      }
-      float* target = y + row * n + col;
-      *target = accumulate ? *target + acc : acc;
-    }
-  }
-}
 
 double vo_bf16_check(const float* y, const uint16_t* x, const uint16_t* w,
                      const float* before, size_t m, size_t k, size_t n) {
@@ -515,9 +539,22 @@ void vo_sinusoid(float t, size_t width, float* embedding) {
 /* ---- the local DiT ------------------------------------------------------ */
 
 /* Project (transformer.cpp:47-53): y = x W^T (+ b). */
-static void project(const vo_projection* p, const uint16_t* x, float* y,
-                    size_t rows, size_t in, size_t out, int threads) {
-  vo_q8_linear(x, p->weight, y, rows, in, out, 0, threads);
+/* A product on the DiT's matrices: Q8_0 blocks, or bf16 rows when
+ * `bf16_weights` is set (the reference's kBf16Tiles stacks). */
+static void dit_linear(const vo_dit* dit, const uint16_t* x, const uint8_t* w,
+                       float* y, size_t rows, size_t in, size_t out,
+                       int accumulate) {
+  if (dit->bf16_weights)
+    vo_bf16_linear(x, (const uint16_t*)w, y, rows, in, out, accumulate,
+                   dit->threads);
+  else
+    vo_q8_linear(x, w, y, rows, in, out, accumulate, dit->threads);
+}
+
+static void project(const vo_dit* dit, const vo_projection* p,
+                    const uint16_t* x, float* y, size_t rows, size_t in,
+                    size_t out) {
+  dit_linear(dit, x, p->weight, y, rows, in, out, 0);
   if (p->bias != NULL)
     vo_add_bias(y, p->bias, rows, out);
 }
@@ -533,19 +570,18 @@ void vo_dit_time_vector(const vo_dit* dit, float t, float* vector) {
   if (dit->has_delta) {
     vo_sinusoid(0.0f, in, embedding);
     vo_to_bf16(embedding, bf16, in, 0);
-    project(&dit->delta_1, bf16, middle, 1, in, width, dit->threads);
+    project(dit, &dit->delta_1, bf16, middle, 1, in, width);
     vo_to_bf16(middle, bf16, width, 1);
-    project(&dit->delta_2, bf16, vector, 1, width, width, dit->threads);
+    project(dit, &dit->delta_2, bf16, vector, 1, width, width);
   } else {
     memset(vector, 0, width * sizeof(float));
   }
   vo_sinusoid(t, in, embedding);
   vo_to_bf16(embedding, bf16, in, 0);
-  project(&dit->time_1, bf16, middle, 1, in, width, dit->threads);
+  project(dit, &dit->time_1, bf16, middle, 1, in, width);
   vo_to_bf16(middle, bf16, width, 1);
   /* vector (the delta term) += time_2 . silu(middle), then the bias */
-  vo_q8_linear(bf16, dit->time_2.weight, vector, 1, width, width, 1,
-               dit->threads);
+  dit_linear(dit, bf16, dit->time_2.weight, vector, 1, width, width, 1);
   if (dit->time_2.bias != NULL)
     vo_add_bias(vector, dit->time_2.bias, 1, width);
   free(embedding);
@@ -558,8 +594,8 @@ void vo_dit_cond_rows(const vo_dit* dit, const float* cond_latent,
   const size_t values = dit->patch * dit->feat;
   uint16_t* bf16 = (uint16_t*)malloc(values * sizeof(uint16_t));
   vo_to_bf16(cond_latent, bf16, values, 0);
-  project(&dit->cond_proj, bf16, cond_rows, dit->patch, dit->feat, dit->hidden,
-          dit->threads);
+  project(dit, &dit->cond_proj, bf16, cond_rows, dit->patch, dit->feat,
+          dit->hidden);
   free(bf16);
 }
 
@@ -573,7 +609,6 @@ void vo_dit_eval(const vo_dit* dit, const float* mu, const float* cond_rows,
   const size_t kv_width = dit->kv_heads * dit->head_dim;
   const size_t qkv_width = q_width + 2 * kv_width;
   const size_t ffn = dit->ffn;
-  const int threads = dit->threads;
   const size_t wide = ffn > qkv_width ? ffn : qkv_width;
   uint16_t* bf16 = (uint16_t*)malloc(rows * (wide > width ? wide : width) *
                                      sizeof(uint16_t));
@@ -597,27 +632,26 @@ void vo_dit_eval(const vo_dit* dit, const float* mu, const float* cond_rows,
       outputs[s * patch + i] = (int32_t)(s * length + 3 + patch + i);
 
   vo_to_bf16(x, bf16, patch * feat, 0);
-  project(&dit->in_proj, bf16, x_rows, patch, feat, width, threads);
+  project(dit, &dit->in_proj, bf16, x_rows, patch, feat, width);
   vo_assemble_dit(mu, time_vector, cond_rows, x_rows, hidden, patch, width);
   for (size_t l = 0; l < dit->layers; ++l) {
     const vo_layer* layer = &dit->layer[l];
     vo_rms_norm(hidden, layer->input_norm, bf16, NULL, rows, width, dit->eps);
-    vo_q8_linear(bf16, layer->qkv, qkv, rows, width, qkv_width, 0, threads);
+    dit_linear(dit, bf16, layer->qkv, qkv, rows, width, qkv_width, 0);
     vo_qkv_rope(qkv, dit->rope, positions, cache_rows, q, k_cache, v_cache,
                 rows, dit->heads, dit->kv_heads, dit->head_dim, rows);
     vo_attention(q, k_cache, v_cache, bf16, rows, length, length, 0, 0,
                  dit->heads, dit->kv_heads, dit->head_dim, rows);
-    vo_q8_linear(bf16, layer->o, hidden, rows, q_width, width, 1, threads);
+    dit_linear(dit, bf16, layer->o, hidden, rows, q_width, width, 1);
     vo_rms_norm(hidden, layer->post_norm, bf16, NULL, rows, width, dit->eps);
-    vo_q8_linear(bf16, layer->gate_up, gate_up, rows, width, 2 * ffn, 0,
-                 threads);
+    dit_linear(dit, bf16, layer->gate_up, gate_up, rows, width, 2 * ffn, 0);
     vo_swiglu(gate_up, bf16, rows, ffn);
-    vo_q8_linear(bf16, layer->down, hidden, rows, ffn, width, 1, threads);
+    dit_linear(dit, bf16, layer->down, hidden, rows, ffn, width, 1);
   }
   vo_rms_norm(hidden, dit->norm, bf16, output, rows, width, dit->eps);
   vo_gather_rows(output, outputs, hidden, 2 * patch, width);
   vo_to_bf16(hidden, bf16, 2 * patch * width, 0);
-  project(&dit->out_proj, bf16, velocity, 2 * patch, width, feat, threads);
+  project(dit, &dit->out_proj, bf16, velocity, 2 * patch, width, feat);
 
   free(bf16);
   free(x_rows);

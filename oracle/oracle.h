@@ -65,9 +65,10 @@ double vo_q8_check(const float* y, const uint16_t* x, const uint8_t* blocks,
  * 16-column chunk (one v_wmma_f32_16x16x16_bf16) a float32 sum of the
  * products, added into the float32 accumulator in k order; the order
  * inside a chunk is the hardware's. y = accumulate ? y + acc : acc.
- * k a multiple of 8 (a last, short chunk is summed the same way). */
+ * k a multiple of 8 (a last, short chunk is summed the same way).
+ * `threads` splits the columns n (identical results for any count). */
 void vo_bf16_linear(const uint16_t* x, const uint16_t* w, float* y, size_t m,
-                    size_t k, size_t n, int accumulate);
+                    size_t k, size_t n, int accumulate, int threads);
 
 /* Worst |y - exact| / sum|x*w| over all outputs for bf16 rows W, exact in
  * double (tests/products_test.cpp:117-145, used with bf16 weights at
@@ -130,7 +131,8 @@ void vo_sinusoid(float t, size_t width, float* embedding);
 /* ---- the local DiT ------------------------------------------------------ */
 
 typedef struct vo_projection {
-  const uint8_t* weight; /* GGML Q8_0 blocks [out][in/32] */
+  const uint8_t* weight; /* GGML Q8_0 blocks [out][in/32], or bf16 rows
+                            [out][in] (vo_dit.bf16_weights) */
   const uint16_t* bias;  /* bf16 [out] or NULL */
 } vo_projection;
 
@@ -154,6 +156,8 @@ typedef struct vo_dit {
   vo_projection in_proj, cond_proj, out_proj;
   vo_projection time_1, time_2, delta_1, delta_2;
   int threads; /* for the products */
+  int bf16_weights; /* every matrix is bf16 rows [out][in] instead of Q8_0
+                       blocks (weights.cpp:281-282, kBf16Tiles stacks) */
 } vo_dit;
 
 /* TimeVector (generator.cpp:212-237, 150-167): [hidden]. */

@@ -39,7 +39,7 @@ class Dit(ctypes.Structure):
         ("in_proj", Projection), ("cond_proj", Projection),
         ("out_proj", Projection), ("time_1", Projection),
         ("time_2", Projection), ("delta_1", Projection),
-        ("delta_2", Projection), ("threads", c_int)]
+        ("delta_2", Projection), ("threads", c_int), ("bf16_weights", c_int)]
 
 
 _SIGNATURES = {
@@ -54,8 +54,8 @@ _SIGNATURES = {
                       c_int, c_int], None),
     "vo_q8_check": ([c_void_p, c_void_p, c_void_p, c_void_p, c_size, c_size,
                      c_size], ctypes.c_double),
-    "vo_bf16_linear": ([c_void_p, c_void_p, c_void_p, c_size, c_size, c_size, c_int],
-                       None),
+    "vo_bf16_linear": ([c_void_p, c_void_p, c_void_p, c_size, c_size, c_size, c_int,
+                        c_int], None),
     "vo_bf16_check": ([c_void_p, c_void_p, c_void_p, c_void_p, c_size, c_size,
                        c_size], ctypes.c_double),
     "vo_rms_norm": ([c_void_p, c_void_p, c_void_p, c_void_p, c_size, c_size,
@@ -147,12 +147,13 @@ def q8_check(y: np.ndarray, x: np.ndarray, blocks: np.ndarray,
     return lib().vo_q8_check(ptr(y), ptr(x), ptr(blocks), ptr(before), m, k, n)
 
 
-def bf16_linear(x: np.ndarray, w: np.ndarray, before: np.ndarray | None = None) -> np.ndarray:
+def bf16_linear(x: np.ndarray, w: np.ndarray, before: np.ndarray | None = None,
+                threads: int = 8) -> np.ndarray:
     """x bf16 bits [m][k], w bf16 bits [n][k] -> float32 [m][n]."""
     m, k = x.shape
     n = w.shape[0]
     y = np.zeros((m, n), dtype=np.float32) if before is None else before.copy()
-    lib().vo_bf16_linear(ptr(x), ptr(w), ptr(y), m, k, n, int(before is not None))
+    lib().vo_bf16_linear(ptr(x), ptr(w), ptr(y), m, k, n, int(before is not None), threads)
     return y
 
 
@@ -183,13 +184,18 @@ def rope_table(theta: float, dim: int, factors, scaling: float,
 class OracleDit:
     """A vo_dit over host copies of synthetic weights."""
 
-    def __init__(self, weights, threads: int = 8):
+    def __init__(self, weights, threads: int = 8, bf16_weights: bool = False):
+        """`bf16_weights`: every matrix as the bf16 expansion bf16(scale q)
+        of its Q8_0 blocks (the reference's bf16 tiles of the same weights)."""
         config = weights.config
         self.config = config
         self._keep = []
 
         def keep(array):
             array = np.ascontiguousarray(array)
+            if bf16_weights and array.ndim == 3 and array.shape[-1] == 34:
+                n, blocks, _ = array.shape
+                array = q8_dequant_bf16(array, n, blocks * 32)
             self._keep.append(array)
             return array.ctypes.data
 
@@ -213,7 +219,8 @@ class OracleDit:
             config.hidden, config.heads, config.kv_heads, config.head_dim,
             config.ffn, config.layers, config.patch, config.feat,
             config.time_in, config.eps, int(config.has_delta), rope, layers,
-            keep(weights.norm), threads=threads, **projections)
+            keep(weights.norm), threads=threads, bf16_weights=int(bf16_weights),
+            **projections)
 
     def time_vector(self, t: float) -> np.ndarray:
         out = np.zeros(self.config.hidden, dtype=np.float32)

@@ -395,3 +395,67 @@ def test_dit_patch_full(vx, oracle, cuda, stream, config):
     error, cos = rel_max(got, ref), cosine(got, ref)
     print(f"patch rel-max {error:.2e} cosine {cos:.8f}")
     assert error <= 1e-2 and cos >= 0.9999
+
+
+# ---- the DiT on bf16 weights -------------------------------------------------
+
+def make_bf16_dit(config, seed, vx, oracle, cuda):
+    """The same synthetic DiT with every matrix as bf16(scale q) panels, and
+    the oracle on the same bf16 matrices."""
+    length = 3 + 2 * config.patch
+    rope = oracle.rope_table(config.rope_theta, config.head_dim, config.rope_factors,
+                             config.rope_scaling, length)
+    weights = synth.dit_weights(config, seed, rope)
+    return (weights, vx.Dit(weights, cuda, bf16_weights=True),
+            oracle.OracleDit(weights, threads=16, bf16_weights=True))
+
+
+@pytest.mark.parametrize("config", [
+    synth.DitConfig(layers=1),
+    SMALL_REAL,
+    synth.DitConfig(layers=2, hidden=512, head_dim=32, ffn=1536, patch=3),
+], ids=["synthetic-block", "voxcpm2-2layers", "narrow-heads"])
+def test_bf16_dit_velocity_paths(vx, oracle, cuda, stream, config):
+    """Velocity on bf16 weights through the fused kernels and the
+    per-kernel path; the persistent path takes Q8_0 only and says so."""
+    from voxcpm_amd import _lib
+    weights, dit, odit = make_bf16_dit(config, 44, vx, oracle, cuda)
+    inputs = synth.patch_inputs(config, 45)
+    mu, cond, x = (dev(a, cuda) for a in (inputs.mu, inputs.cond_latent, inputs.noise))
+    ref = odit.velocity(inputs.mu, inputs.cond_latent, inputs.noise, 0.63)
+    for path in (_lib.DIT_PATH_FUSED, _lib.DIT_PATH_UNFUSED):
+        dit.set_path(path)
+        got = dit.velocity(mu, cond, x, 0.63).cpu().numpy()
+        dit.status()
+        error, cos = rel_max(got, ref), cosine(got, ref)
+        print(f"bf16 weights path {path}: velocity rel-max {error:.2e} cosine {cos:.8f}",
+              flush=True)
+        assert error <= 1e-2 and cos >= 0.9999, path
+        assert np.array_equal(got, dit.velocity(mu, cond, x, 0.63).cpu().numpy())
+    with pytest.raises(_lib.VxError) as info:
+        dit.set_path(_lib.DIT_PATH_PERSISTENT)
+    assert info.value.status == _lib.VX_UNSUPPORTED
+
+
+def test_bf16_dit_patch_full(vx, oracle, cuda, stream):
+    """The synthetic workload's full patch (12 blocks, 10 Euler steps) on
+    bf16 weights, replayed as a HIP graph."""
+    config = synth.SYNTHETIC_DIT
+    weights, dit, odit = make_bf16_dit(config, 46, vx, oracle, cuda)
+    inputs = synth.patch_inputs(config, 47)
+    from voxcpm_amd import ops
+    t, dt, ev = ops.euler_schedule(config.steps, config.sway, config.skip)
+    mu, cond = dev(inputs.mu, cuda), dev(inputs.cond_latent, cuda)
+    x = dev(inputs.noise, cuda)
+    dit.patch(mu, cond, x, t, dt, ev, config.cfg, config.zero_star)
+    got = x.cpu().numpy()
+    x.copy_(dev(inputs.noise, cuda))
+    dit.patch(mu, cond, x, t, dt, ev, config.cfg, config.zero_star)
+    torch.cuda.synchronize()
+    dit.status()
+    assert np.array_equal(x.cpu().numpy(), got)
+    ref = odit.patch(inputs.mu, inputs.cond_latent, inputs.noise, t, dt, ev,
+                     config.cfg, config.zero_star)
+    error, cos = rel_max(got, ref), cosine(got, ref)
+    print(f"bf16 weights patch rel-max {error:.2e} cosine {cos:.8f}")
+    assert error <= 1e-2 and cos >= 0.9999

@@ -381,15 +381,20 @@ def test_sinusoid(oracle):
 
 # ---- the DiT against a float64 torch formulation --------------------------------
 
-def torch_dit_velocity(weights, oracle, mu, cond_latent, x, t):
+def torch_dit_velocity(weights, oracle, mu, cond_latent, x, t, bf16_weights=False):
     """The local DiT in float64 torch from its description (no bf16 rounding,
-    torch's attention), for comparison at tolerance."""
+    torch's attention), for comparison at tolerance. `bf16_weights` takes
+    every matrix as bf16(scale q) (numpy's rounding of the float64 value)."""
     c = weights.config
     td = torch.float64
 
     def W(blocks):
         n, kb, _ = blocks.shape
-        return torch.from_numpy(oracle.q8_values(np.ascontiguousarray(blocks), n, kb * 32))
+        values = oracle.q8_values(np.ascontiguousarray(blocks), n, kb * 32)
+        if bf16_weights:
+            values = synth.bf16_values(synth.bf16_bits(values.astype(np.float32))) \
+                .astype(np.float64)
+        return torch.from_numpy(values)
 
     def vec(bits):
         return torch.from_numpy(synth.bf16_values(bits).astype(np.float64))
@@ -459,20 +464,28 @@ def torch_dit_velocity(weights, oracle, mu, cond_latent, x, t):
                     layers=2, time_in=256, has_delta=True, eps=1e-5,
                     rope_factors=synth.VOXCPM2_SHORT_FACTORS),
 ], ids=["mha-hd64", "gqa-hd128-delta"])
-def test_dit_velocity_against_float64_torch(oracle, config):
+@pytest.mark.parametrize("bf16_weights", [False, True], ids=["q8", "bf16-weights"])
+def test_dit_velocity_against_float64_torch(oracle, config, bf16_weights):
     rope = oracle.rope_table(config.rope_theta, config.head_dim, config.rope_factors,
                              config.rope_scaling, 3 + 2 * config.patch)
     weights = synth.dit_weights(config, 11, rope)
     inputs = synth.patch_inputs(config, 12)
-    dit = oracle.OracleDit(weights)
+    dit = oracle.OracleDit(weights, bf16_weights=bf16_weights)
     got = dit.velocity(inputs.mu, inputs.cond_latent, inputs.noise, 0.63)
     ref = torch_dit_velocity(weights, oracle, inputs.mu, inputs.cond_latent,
-                             inputs.noise, 0.63)
+                             inputs.noise, 0.63, bf16_weights=bf16_weights)
     error = np.linalg.norm(got - ref) / np.linalg.norm(ref)
     assert error < 1e-2, error  # bf16 activations against float64
     # A planted slip in the oracle's composition (swapping the CFG branches)
     # fails the same bound.
     assert np.linalg.norm(got[::-1] - ref) / np.linalg.norm(ref) > 5e-2
+    if bf16_weights:
+        # The bf16 matrices are really the ones multiplied: the result moves
+        # off the Q8_0 one by the weights' rounding, and only by that.
+        q8 = oracle.OracleDit(weights).velocity(inputs.mu, inputs.cond_latent,
+                                                inputs.noise, 0.63)
+        moved = np.linalg.norm(got - q8) / np.linalg.norm(q8)
+        assert 1e-6 < moved < 2e-2, moved
 
 
 def test_dit_patch_composes_evaluations(oracle):

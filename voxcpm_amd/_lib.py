@@ -56,7 +56,12 @@ class DitWeights(ctypes.Structure):
                 ("rope", c_void_p), ("in_proj", DitProjection),
                 ("cond_proj", DitProjection), ("out_proj", DitProjection),
                 ("time_1", DitProjection), ("time_2", DitProjection),
-                ("delta_1", DitProjection), ("delta_2", DitProjection)]
+                ("delta_1", DitProjection), ("delta_2", DitProjection),
+                ("format", ctypes.c_uint32)]
+
+
+VX_WEIGHTS_Q8_0 = 0
+VX_WEIGHTS_BF16 = 1
 
 
 _SIGNATURES = {

@@ -164,14 +164,19 @@ struct vx_dit {
         (void)hipFree(pointer);
   }
 
-  /// y[m][n] (+)= x W^T on Q8_0 panels.
+  /// The weights' format (every matrix).
+  vx::q8::Weights Kind() const {
+    return weights.format == VX_WEIGHTS_BF16 ? vx::q8::Weights::kBf16 : vx::q8::Weights::kQ8;
+  }
+
+  /// y[m][n] (+)= x W^T on the panels.
   int Linear(const Bf16* x, const void* w, float* y, std::size_t m,
              std::size_t k, std::size_t n, bool accumulate,
              hipStream_t stream) {
     const vx::ProductPlan plan =
         vx::PlanSkinny(m, k, n, partial_floats, counter_count);
     return vx::RunSkinny(x, w, y, nullptr, m, k, n, accumulate, plan,
-                         partials, counters, stream);
+                         partials, counters, stream, Kind());
   }
 
   /// Project (transformer.cpp:47-53): y = x W^T + b.
@@ -379,6 +384,8 @@ int CheckShape(const vx_dit_shape& s) {
 }
 
 int CheckWeights(const vx_dit_shape& s, const vx_dit_weights& w) {
+  if (w.format != VX_WEIGHTS_Q8_0 && w.format != VX_WEIGHTS_BF16)
+    return vx::Fail(VX_BAD_ARG, "vx_dit_create: unknown weight format");
   if (w.layers == nullptr || w.norm == nullptr || w.in_proj.weight == nullptr ||
       w.cond_proj.weight == nullptr || w.out_proj.weight == nullptr ||
       w.time_1.weight == nullptr || w.time_2.weight == nullptr)
@@ -439,6 +446,7 @@ int Create(vx_dit* dit) {
   fs.ffn = static_cast<int>(s.ffn);
   fs.feat = static_cast<int>(s.feat);
   fs.eps = s.eps;
+  fs.weights = dit->Kind();
   dit->fused = vx::fused::Supported(fs);
   if (dit->fused) {
     const std::size_t h_count = vx::q8::FragElements(s.hidden);
@@ -457,7 +465,9 @@ int Create(vx_dit* dit) {
 
     dit->grid = vx::persistent::GridSize();
     const int layers = static_cast<int>(s.layers);
-    dit->persistent = vx::persistent::Supported(fs, layers, dit->grid) &&
+    // The persistent kernel reads Q8_0 panels only.
+    dit->persistent = fs.weights == vx::q8::Weights::kQ8 &&
+                      vx::persistent::Supported(fs, layers, dit->grid) &&
                       vx::persistent::Prepare(fs);
   }
   if (dit->persistent) {

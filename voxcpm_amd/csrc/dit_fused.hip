@@ -49,23 +49,28 @@ struct InArgs {
 };
 
 // One wave per 16 hidden columns: in_proj of the patch rows (x rounded to
-// bf16, the exact Q8_0 product, then the bias), written to both branches'
-// x rows, and the mu / time / condition rows of those columns.
+// bf16, the exact Q8_0 product or the bf16 one, then the bias), written to
+// both branches' x rows, and the mu / time / condition rows of those
+// columns.
+template<q8::Weights WK>
 __global__ __launch_bounds__(kWave) void InAssembleKernel(InArgs a) {
+  constexpr int kUnit = WK == q8::Weights::kQ8 ? kUnitBytes : q8::kBf16UnitBytes;
   const int lane = threadIdx.x;
   const int r16 = lane % 16;
   const int octet = lane / 16;
   const int group = static_cast<int>(blockIdx.x);
   const int pairs = PairsOf(a.feat);
   const std::uint8_t* unit =
-      a.w + static_cast<std::size_t>(group) * pairs * kUnitBytes;
+      a.w + static_cast<std::size_t>(group) * pairs * kUnit;
   F32x4 acc{0.0F, 0.0F, 0.0F, 0.0F};
   const F32x4 zero{0.0F, 0.0F, 0.0F, 0.0F};
   for (int pair = 0; pair < pairs; ++pair) {
-    const std::uint8_t* u = unit + static_cast<std::size_t>(pair) * kUnitBytes;
+    const std::uint8_t* u = unit + static_cast<std::size_t>(pair) * kUnit;
     const uint4 wv = *reinterpret_cast<const uint4*>(u + 16 * lane);
     const std::uint32_t scales =
-        *reinterpret_cast<const std::uint32_t*>(u + kValueBytes + 4 * r16);
+        WK == q8::Weights::kQ8
+            ? *reinterpret_cast<const std::uint32_t*>(u + kValueBytes + 4 * r16)
+            : 0U;
     uint4 xa[2];
 #pragma unroll
     for (int hf = 0; hf < 2; ++hf) {
@@ -80,6 +85,13 @@ __global__ __launch_bounds__(kWave) void InAssembleKernel(InArgs a) {
         v[4] = hi.x; v[5] = hi.y; v[6] = hi.z; v[7] = hi.w;
       }
       xa[hf] = q8::PackBf16x8(v);
+    }
+    if constexpr (WK != q8::Weights::kQ8) {
+      // bf16 panels: each block's products accumulate straight into the sums.
+      const uint4 wv2 = *reinterpret_cast<const uint4*>(u + q8::kBf16HalfBytes + 16 * lane);
+      acc = Mfma16x16x32(AsBf16x8(xa[0]), AsBf16x8(wv), acc);
+      acc = Mfma16x16x32(AsBf16x8(xa[1]), AsBf16x8(wv2), acc);
+      continue;
     }
     const F32x4 sum0 = Mfma16x16x32(AsBf16x8(xa[0]), Int8x8ToBf16(wv.x, wv.y), zero);
     const F32x4 sum1 = Mfma16x16x32(AsBf16x8(xa[1]), Int8x8ToBf16(wv.z, wv.w), zero);
@@ -292,9 +304,12 @@ constexpr int kOutGroups = 4;  // feat <= 64
 
 // One workgroup: the 2 patch output rows of both branches normalised with
 // the final norm (bf16 after the float32 scale, as RmsNorm then ToBf16),
-// the out_proj product split over the waves by pairs, the bias, and with x
-// given the guided Euler step over the whole velocity.
+// the out_proj product (Q8_0 or bf16 panels) split over the waves by pairs,
+// the bias, and with x given the guided Euler step over the whole velocity.
+template<q8::Weights WK>
 __global__ __launch_bounds__(1024) void OutEulerKernel(OutArgs a) {
+  constexpr bool kBf16 = WK != q8::Weights::kQ8;
+  constexpr int kUnit = kBf16 ? q8::kBf16UnitBytes : kUnitBytes;
   __shared__ float squares[kMaxWaves][16];
   __shared__ float reduce[kMaxWaves][kOutGroups][4][kWave];
   __shared__ float velocity[2 * 8 * 64];
@@ -312,6 +327,7 @@ __global__ __launch_bounds__(1024) void OutEulerKernel(OutArgs a) {
   const int h_row = row_ok ? (r16 / a.patch) * a.length + 3 + a.patch + r16 % a.patch : 0;
   constexpr int kPw = 2;  // pairs per wave: hidden <= 2048
   uint4 wv[kPw][kOutGroups];
+  uint4 wv2[kPw][kOutGroups];  // bf16: the pair's second block
   std::uint32_t sc[kPw][kOutGroups];
   float4 hv[kPw][2][2];
 #pragma unroll
@@ -322,9 +338,16 @@ __global__ __launch_bounds__(1024) void OutEulerKernel(OutArgs a) {
     for (int g = 0; g < kOutGroups; ++g) {
       const bool use = ok && g < groups;
       const std::uint8_t* u =
-          a.w + (static_cast<std::size_t>(use ? g : 0) * pairs + (use ? pair : 0)) * kUnitBytes;
+          a.w + (static_cast<std::size_t>(use ? g : 0) * pairs + (use ? pair : 0)) * kUnit;
       wv[p][g] = use ? *reinterpret_cast<const uint4*>(u + 16 * lane) : uint4{0U, 0U, 0U, 0U};
-      sc[p][g] = use ? *reinterpret_cast<const std::uint32_t*>(u + kValueBytes + 4 * r16) : 0U;
+      if constexpr (kBf16) {
+        wv2[p][g] = use ? *reinterpret_cast<const uint4*>(u + q8::kBf16HalfBytes + 16 * lane)
+                        : uint4{0U, 0U, 0U, 0U};
+        sc[p][g] = 0U;
+      } else {
+        sc[p][g] =
+            use ? *reinterpret_cast<const std::uint32_t*>(u + kValueBytes + 4 * r16) : 0U;
+      }
     }
 #pragma unroll
     for (int hf = 0; hf < 2; ++hf)
@@ -385,6 +408,11 @@ __global__ __launch_bounds__(1024) void OutEulerKernel(OutArgs a) {
     for (int g = 0; g < kOutGroups; ++g) {
       if (g >= groups)
         continue;
+      if constexpr (kBf16) {
+        acc[g] = Mfma16x16x32(AsBf16x8(xa[0]), AsBf16x8(wv[p][g]), acc[g]);
+        acc[g] = Mfma16x16x32(AsBf16x8(xa[1]), AsBf16x8(wv2[p][g]), acc[g]);
+        continue;
+      }
       const float s0 = HalfValue(static_cast<std::uint16_t>(sc[p][g] & 0xFFFFU));
       const float s1 = HalfValue(static_cast<std::uint16_t>(sc[p][g] >> 16));
       const F32x4 sum0 =
@@ -449,11 +477,15 @@ __global__ __launch_bounds__(1024) void OutEulerKernel(OutArgs a) {
 // ---- the engine's fused instantiations -------------------------------------
 
 template<q8::ASource SRC, q8::Output OUT, int RG, int PW, int MT = 2>
-void LaunchEngine(const q8::TileArgs& args, int tiles, int waves,
+void LaunchEngine(const q8::TileArgs& args, int tiles, int waves, q8::Weights kind,
                   hipStream_t stream) {
   const std::size_t shared = q8::EngineShared(MT, RG, waves, SRC);
-  q8::EngineKernel<MT, RG, SRC, OUT, PW>
-      <<<tiles, waves * kWave, shared, stream>>>(args);
+  if (kind == q8::Weights::kQ8)
+    q8::EngineKernel<MT, RG, SRC, OUT, PW, 2 * MT, q8::Weights::kQ8>
+        <<<tiles, waves * kWave, shared, stream>>>(args);
+  else
+    q8::EngineKernel<MT, RG, SRC, OUT, PW, 2 * MT, q8::Weights::kBf16>
+        <<<tiles, waves * kWave, shared, stream>>>(args);
 }
 
 q8::TileArgs BaseArgs(const void* weight, int m, int k, int n) {
@@ -522,7 +554,10 @@ void InAssemble(const float* x, const void* in_weight, const Bf16* in_bias,
   a.feat = s.feat;
   a.hidden = s.hidden;
   a.length = s.length;
-  InAssembleKernel<<<s.hidden / 16, kWave, 0, stream>>>(a);
+  if (s.weights == q8::Weights::kQ8)
+    InAssembleKernel<q8::Weights::kQ8><<<s.hidden / 16, kWave, 0, stream>>>(a);
+  else
+    InAssembleKernel<q8::Weights::kBf16><<<s.hidden / 16, kWave, 0, stream>>>(a);
 }
 
 void Qkv(const float* h, const Bf16* norm, const void* weight, float* qkv,
@@ -535,10 +570,10 @@ void Qkv(const float* h, const Bf16* norm, const void* weight, float* qkv,
   args.y = qkv;
   if (args.pairs <= kMaxWaves)
     LaunchEngine<q8::ASource::kNormF32, q8::Output::kStore, 1, 1>(
-        args, args.groups, kMaxWaves, stream);
+        args, args.groups, kMaxWaves, s.weights, stream);
   else
     LaunchEngine<q8::ASource::kNormF32, q8::Output::kStore, 1, 2>(
-        args, args.groups, kMaxWaves, stream);
+        args, args.groups, kMaxWaves, s.weights, stream);
 }
 
 void Attention(const float* qkv, const float* rope, Bf16* out, const Shape& s,
@@ -574,11 +609,11 @@ void Residual(const Bf16* act, const void* weight, int k, int n, float* h,
   if (args.pairs > 2 * kMaxWaves) {  // two pairs per wave per pass
     SetTileBlocks(args, args.groups, s.rows);
     LaunchEngine<q8::ASource::kFragBf16, q8::Output::kResidual, 1, 2, 1>(
-        args, args.groups * args.row_blocks, kMaxWaves, stream);
+        args, args.groups * args.row_blocks, kMaxWaves, s.weights, stream);
   } else {
     SetRowBlocks(args, args.groups, s.rows);
     LaunchEngine<q8::ASource::kFragBf16, q8::Output::kResidual, 1, 1>(
-        args, args.groups * args.row_blocks, kMaxWaves, stream);
+        args, args.groups * args.row_blocks, kMaxWaves, s.weights, stream);
   }
 }
 
@@ -593,10 +628,10 @@ void GateUp(const float* h, const Bf16* norm, const void* weight, Bf16* out,
   const int tiles = s.ffn / 16;
   if (args.pairs <= kMaxWaves)
     LaunchEngine<q8::ASource::kNormF32, q8::Output::kSwiGlu, 2, 1>(
-        args, tiles, kMaxWaves, stream);
+        args, tiles, kMaxWaves, s.weights, stream);
   else
     LaunchEngine<q8::ASource::kNormF32, q8::Output::kSwiGlu, 2, 2>(
-        args, tiles, kMaxWaves, stream);
+        args, tiles, kMaxWaves, s.weights, stream);
 }
 
 void OutEuler(const float* h, const Bf16* norm, const void* out_weight,
@@ -619,7 +654,10 @@ void OutEuler(const float* h, const Bf16* norm, const void* out_weight,
   a.length = s.length;
   const int pairs = PairsOf(s.hidden);
   const int waves = std::min(kMaxWaves, pairs);
-  OutEulerKernel<<<1, waves * kWave, 0, stream>>>(a);
+  if (s.weights == q8::Weights::kQ8)
+    OutEulerKernel<q8::Weights::kQ8><<<1, waves * kWave, 0, stream>>>(a);
+  else
+    OutEulerKernel<q8::Weights::kBf16><<<1, waves * kWave, 0, stream>>>(a);
 }
 
 }  // namespace vx::fused

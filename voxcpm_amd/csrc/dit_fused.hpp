@@ -13,6 +13,7 @@
 #include <cstdint>
 
 #include "common.hpp"
+#include "q8.hpp"
 
 namespace vx::fused {
 
@@ -27,6 +28,7 @@ struct Shape {
   int ffn;
   int feat;
   float eps;
+  q8::Weights weights = q8::Weights::kQ8;  // Q8_0 or bf16 panels, every matrix
 };
 
 /// Whether the fused kernels take this shape: at most 32 rows (patch <= 6),

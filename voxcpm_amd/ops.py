@@ -12,7 +12,8 @@ import numpy as np
 import torch
 
 from . import synth
-from ._lib import DitLayer, DitProjection, DitShape, DitWeights, check, lib
+from ._lib import (VX_WEIGHTS_BF16, VX_WEIGHTS_Q8_0, DitLayer, DitProjection, DitShape,
+                   DitWeights, check, lib)
 
 __all__ = [
     "Scratch", "Dit", "q8_pack", "q8_unpack_blocks", "q8_unpack_bf16",
@@ -203,7 +204,9 @@ class Dit:
     """vx_dit over device copies of synthetic (or given) host weights."""
 
     def __init__(self, weights: synth.DitWeightsHost, device=None,
-                 stream=None):
+                 stream=None, bf16_weights: bool = False):
+        """`bf16_weights`: every matrix as bf16 panels of bf16(scale q), the
+        bf16 expansion of its Q8_0 blocks (the DiT on bf16 weights)."""
         self.config = config = weights.config
         device = _device(device)
         self._keep = []
@@ -212,6 +215,8 @@ class Dit:
             n, kb, _ = blocks.shape
             raw = torch.from_numpy(np.ascontiguousarray(blocks)).to(device)
             packed = q8_pack(raw, n, kb * 32, stream)
+            if bf16_weights:
+                packed = bf16_pack(q8_unpack_bf16(packed, n, kb * 32, stream), stream)
             self._keep.append(packed)
             return packed
 
@@ -246,7 +251,7 @@ class Dit:
         self._layers = layer_array
         self._weights = DitWeights(
             layer_array, upload_bf16(weights.norm).data_ptr(), rope_ptr,
-            **projections)
+            **projections, format=VX_WEIGHTS_BF16 if bf16_weights else VX_WEIGHTS_Q8_0)
         self._shape = DitShape(
             config.hidden, config.heads, config.kv_heads, config.head_dim,
             config.ffn, config.layers, config.patch, config.feat,
