@@ -41,6 +41,14 @@ BF16_PEAK_TFLOPS = 2500.0
 FETCH_SCALE = 262144 / 131083.5
 TRAFFIC_KIB = {(1024, 3072): (1833.5, 264.0), (1024, 8192): (4553.0, 704.0),
                (2048, 2048): (2553.5, 176.0), (2048, 16384): (17805.5, 1408.0)}
+# The decode steps' products (tools/bench/gemm_bench.cpp:34-38): the base and
+# residual LMs (hidden 2048, 16 + 2 x 2 heads of 128, MLP 6144) and the
+# local encoder/DiT shapes, at one row (an LM step) and five (the encoder's
+# patch + special row).
+LM_SHAPES = [("lm qkv", 2048, 2560), ("lm o", 2048, 2048), ("lm gate_up", 2048, 12288),
+             ("lm down", 6144, 2048), ("local qkv", 1024, 2560), ("local o", 2048, 1024),
+             ("local gate_up", 1024, 8192), ("local down", 4096, 1024)]
+LM_ROWS = [1, 5]
 PREFILL_M = [129, 256, 512, 1024]
 PREFILL_N = [2048, 6144, 16384]
 PREFILL_K = 2048
@@ -58,7 +66,8 @@ def q8_bytes(k: int, n: int) -> int:
 class Product:
     """One sweep shape on the GPU: a pool of rotating weight copies."""
 
-    def __init__(self, ops, synth, torch, device, k: int, n: int, seed: int):
+    def __init__(self, ops, synth, torch, device, k: int, n: int, seed: int,
+                 rows=SWEEP_ROWS):
         self.k, self.n = k, n
         rng = synth.Rng(seed, k * 31 + n)
         blocks = torch.from_numpy(synth.q8_blocks(rng, n, k)).to(device)
@@ -68,7 +77,7 @@ class Product:
         self.copies = max(8, int(np.ceil(ROTATION_BYTES / self.bytes)))
         self.pool = packed.repeat(self.copies).view(self.copies, -1)
         self.inputs = {}
-        for m in SWEEP_ROWS:
+        for m in rows:
             x = synth.activations(rng, m, k)
             self.inputs[m] = (
                 torch.from_numpy(x.view(np.int16)).to(device).view(torch.bfloat16),
@@ -185,6 +194,43 @@ def gpu_products(args, torch, ops, synth, device, stream):
     del products
     torch.cuda.empty_cache()
     return result
+
+
+def gpu_lm(args, torch, ops, synth, device, stream):
+    """The decode shapes at 1 and 5 rows, MALL-cold (rotated copies),
+    graph-replayed like the sweep; beside each the plain-read ceiling."""
+    scratch = ops.Scratch(128, 16384)
+    sink = torch.zeros(1, dtype=torch.int32, device=device)
+    rows_out = []
+    for name, k, n in LM_SHAPES:
+        p = Product(ops, synth, torch, device, k, n, seed=1, rows=LM_ROWS)
+        count = max(p.copies, 64)
+        g = graph_of(torch, stream,
+                     lambda i, p=p: ops.stream_read(p.pool[i % p.copies], sink), count)
+        g.replay()
+        read_us = time_graph(torch, stream, g) / count * 1e6
+        del g
+        for m in LM_ROWS:
+            g = graph_of(torch, stream, lambda _i, p=p, m=m: p.launch(ops, scratch, m), count)
+            g.replay()
+            us = time_graph(torch, stream, g) / count * 1e6
+            del g
+            rows_out.append({"name": name, "m": m, "k": k, "n": n, "us": round(us, 3),
+                             "gbs": round(p.bytes / us / 1e3, 1),
+                             "hbm_frac": round(p.bytes / us / 1e3 / HBM_PEAK_GBS, 4),
+                             "read_ceiling_us": round(read_us, 3)})
+            log(f"  {name} M={m}: {us:.3f} us, {p.bytes / us / 1e3:.1f} GB/s "
+                f"(read ceiling {read_us:.3f} us)")
+        del p
+        torch.cuda.empty_cache()
+    # Product time of one base-LM step (28 layers) and one residual-LM step
+    # (8 layers) at one row, from the per-shape figures.
+    layer_us = sum(r["us"] for r in rows_out if r["m"] == 1 and r["name"].startswith("lm "))
+    layer_bytes = sum(q8_bytes(k, n) for name, k, n in LM_SHAPES if name.startswith("lm "))
+    return {"shapes": rows_out, "lm_layer_us_m1": round(layer_us, 3),
+            "lm_layer_gbs_m1": round(layer_bytes / layer_us / 1e3, 1),
+            "base_lm_products_us_m1": round(28 * layer_us, 1),
+            "residual_lm_products_us_m1": round(8 * layer_us, 1)}
 
 
 def gpu_bf16(args, torch, ops, synth, device, stream):
@@ -445,6 +491,8 @@ def main() -> int:
                         help="skip the DiT patch measurement")
     parser.add_argument("--no-bf16", action="store_true",
                         help="skip the bf16-weight products")
+    parser.add_argument("--no-lm", action="store_true",
+                        help="skip the LM decode shapes")
     parser.add_argument("--no-prefill", action="store_true",
                         help="skip the prefill-sized products")
     parser.add_argument("--pmc-workload", action="store_true",
@@ -474,6 +522,7 @@ def main() -> int:
     probe = read_probe(torch, device, stream)
     log(f"read probe {probe:.0f} GB/s")
     products = gpu_products(args, torch, ops, synth, device, stream)
+    lm = None if args.no_lm else gpu_lm(args, torch, ops, synth, device, stream)
     bf16 = None if args.no_bf16 else gpu_bf16(args, torch, ops, synth, device, stream)
     prefill = None if args.no_prefill else gpu_prefill(args, torch, ops, synth, device, stream)
     patch = None if args.no_patch else gpu_patch(args, torch, ops, synth, device, stream)
@@ -529,6 +578,7 @@ def main() -> int:
         "cpu_baseline": baseline,
         "read_probe_gbs": round(probe, 1),
         "sweep": products["sweep"],
+        "lm_decode": lm,
         "bf16_weights": bf16,
         "prefill": prefill,
         "patch": patch,

@@ -25,7 +25,10 @@ SHAPES = [
     (2048, 1024, [1, 5, 22]),
     (4096, 1024, [1, 5, 22]),
     (2048, 2048, [1, 5]),
-    (6144, 2048, [1, 3]),
+    (6144, 2048, [1, 3, 5]),
+    # the LM decode step's qkv and gate_up (tools/bench/gemm_bench.cpp:35-36)
+    (2048, 2560, [1, 5]),
+    (2048, 12288, [1, 5]),
     (8192, 512, [1, 22]),
     (1024, 72, [3, 22]),  # rows not a multiple of 16
     (2048, 2, [1]),

@@ -33,6 +33,7 @@ struct ProductPlan {
   int pairs_per_split = 0;
   int pairs_per_wave = 0;
   int row_blocks = 1;  // engine plans: activation-row blocks per tile
+  int pw = 1;          // engine plans: pairs per wave in flight per pass
 };
 
 /// Largest row-group count per workgroup the kernels have for `mt` tiles.

@@ -308,8 +308,7 @@ Launcher PickLauncher(int mt, int rg) {
 template<int MT, int RG, int PW, int JR, q8::Weights WK>
 void LaunchEngine(const q8::TileArgs& args, int tiles, int waves,
                   hipStream_t stream) {
-  const std::size_t shared =
-      q8::EngineShared(MT, RG, waves, q8::ASource::kRowMajor, PW);
+  const std::size_t shared = q8::EngineShared(MT, RG, waves, q8::ASource::kRowMajor);
   q8::EngineKernel<MT, RG, q8::ASource::kRowMajor, q8::Output::kStore, PW, JR, WK>
       <<<tiles, waves * kWave, shared, stream>>>(args);
 }
@@ -317,62 +316,80 @@ void LaunchEngine(const q8::TileArgs& args, int tiles, int waves,
 using EngineLauncher = void (*)(const q8::TileArgs&, int, int, hipStream_t);
 
 /// Up to 32 rows the engine stages the rows through LDS in JR load groups
-/// of 8 rows; more rows load straight into the operands. One pair per wave
-/// per pass measures fastest on MI355X at every sweep shape (deeper
-/// in-flight passes need more registers and LDS and lose).
-template<int MT, int RG, q8::Weights WK>
+/// of 8 rows; more rows load straight into the operands.
+template<int MT, int RG, int PW, q8::Weights WK>
 EngineLauncher EngineJr(int m) {
   if constexpr (q8::StagesRows(q8::ASource::kRowMajor, MT)) {
     if (m <= 16 * MT - 8)
-      return LaunchEngine<MT, RG, 1, 2 * MT - 1, WK>;
+      return LaunchEngine<MT, RG, PW, 2 * MT - 1, WK>;
   }
-  return LaunchEngine<MT, RG, 1, 2 * MT, WK>;
+  return LaunchEngine<MT, RG, PW, 2 * MT, WK>;
+}
+
+/// Pairs in flight per wave (`pw`, kMaxPairsInFlight): one 16-row tile
+/// (m <= 16) takes up to four, so that the decode shapes' long reductions
+/// (k = 6144: 96 pairs over 16 waves) need few memory round trips; 32 rows
+/// take one at most (measured fastest on MI355X at the M = 22 sweep shapes,
+/// where more pairs in flight cost registers).
+template<int MT, int RG, q8::Weights WK>
+EngineLauncher EnginePw(int pw, int m) {
+  if constexpr (MT == 1) {
+    switch (pw) {
+      case 2: return EngineJr<MT, RG, 2, WK>(m);
+      case 3: return EngineJr<MT, RG, 3, WK>(m);
+      case 4: return EngineJr<MT, RG, 4, WK>(m);
+      default: break;
+    }
+  }
+  return pw == 1 ? EngineJr<MT, RG, 1, WK>(m) : nullptr;
 }
 
 template<int MT, q8::Weights WK>
-EngineLauncher EngineRg(int rg, int m) {
+EngineLauncher EngineRg(int rg, int pw, int m) {
   if constexpr (MT * 4 <= 8) {
     if (rg == 4)
-      return EngineJr<MT, 4, WK>(m);
+      return EnginePw<MT, 4, WK>(pw, m);
   }
   if constexpr (MT * 2 <= 8) {
     if (rg == 2)
-      return EngineJr<MT, 2, WK>(m);
+      return EnginePw<MT, 2, WK>(pw, m);
   }
   if (rg == 1)
-    return EngineJr<MT, 1, WK>(m);
+    return EnginePw<MT, 1, WK>(pw, m);
   return nullptr;
 }
 
 template<q8::Weights WK>
-EngineLauncher PickEngineFor(int mt, int rg, int m) {
+EngineLauncher PickEngineFor(int mt, int rg, int pw, int m) {
   switch (mt) {
-    case 1: return EngineRg<1, WK>(rg, m);
-    case 2: return EngineRg<2, WK>(rg, m);
-    case 3: return EngineRg<3, WK>(rg, m);
-    case 4: return EngineRg<4, WK>(rg, m);
-    case 5: return EngineRg<5, WK>(rg, m);
-    case 6: return EngineRg<6, WK>(rg, m);
-    case 7: return EngineRg<7, WK>(rg, m);
-    case 8: return EngineRg<8, WK>(rg, m);
+    case 1: return EngineRg<1, WK>(rg, pw, m);
+    case 2: return EngineRg<2, WK>(rg, pw, m);
+    case 3: return EngineRg<3, WK>(rg, pw, m);
+    case 4: return EngineRg<4, WK>(rg, pw, m);
+    case 5: return EngineRg<5, WK>(rg, pw, m);
+    case 6: return EngineRg<6, WK>(rg, pw, m);
+    case 7: return EngineRg<7, WK>(rg, pw, m);
+    case 8: return EngineRg<8, WK>(rg, pw, m);
     default: return nullptr;
   }
 }
 
 /// bf16 rows [n][k] are read by the staged engine only (m <= 32).
-EngineLauncher PickEngine(int mt, int rg, int m, q8::Weights kind) {
+EngineLauncher PickEngine(int mt, int rg, int pw, int m, q8::Weights kind) {
   switch (kind) {
-    case q8::Weights::kQ8: return PickEngineFor<q8::Weights::kQ8>(mt, rg, m);
-    case q8::Weights::kBf16: return PickEngineFor<q8::Weights::kBf16>(mt, rg, m);
+    case q8::Weights::kQ8: return PickEngineFor<q8::Weights::kQ8>(mt, rg, pw, m);
+    case q8::Weights::kBf16: return PickEngineFor<q8::Weights::kBf16>(mt, rg, pw, m);
     case q8::Weights::kBf16Rows:
       if (mt == 1)
-        return EngineRg<1, q8::Weights::kBf16Rows>(rg, m);
+        return EngineRg<1, q8::Weights::kBf16Rows>(rg, pw, m);
       if (mt == 2)
-        return EngineRg<2, q8::Weights::kBf16Rows>(rg, m);
+        return EngineRg<2, q8::Weights::kBf16Rows>(rg, pw, m);
       return nullptr;
   }
   return nullptr;
 }
+
+constexpr int kMaxPairsInFlight = 4;
 
 /// Engine plan: up to 256 row groups take one per workgroup; wider products
 /// share each activation fragment over 2 or 4 row groups (fewer workgroups
@@ -396,7 +413,10 @@ ProductPlan PlanEngine(std::size_t m, std::size_t k, std::size_t n) {
   plan.engine = true;
   const int groups = static_cast<int>(q8::Groups(n));
   const int pairs = static_cast<int>(q8::Pairs(k));
-  int rg = groups <= 256 ? 1 : groups <= 512 ? 2 : 4;
+  // Up to 8 rows (one staged load group) the activations cost little to
+  // re-read: one row group per workgroup spreads wide products over more
+  // compute units (measured on MI355X at 1 and 5 rows, n 12288 and 16384).
+  int rg = (m <= 8 || groups <= 256) ? 1 : groups <= 512 ? 2 : 4;
   while (rg > 1 && rg * plan.mt > 8)
     rg /= 2;
   plan.rg = rg;
@@ -412,6 +432,13 @@ ProductPlan PlanEngine(std::size_t m, std::size_t k, std::size_t n) {
   plan.splits = 1;
   plan.pairs_per_split = pairs;
   plan.pairs_per_wave = (pairs + plan.waves - 1) / plan.waves;
+  if (plan.mt == 1) {
+    // Passes of equal length, at most four pairs (two with four row groups)
+    // in flight per wave.
+    const int most = std::min(kMaxPairsInFlight, 8 / rg);
+    const int passes = (plan.pairs_per_wave + most - 1) / most;
+    plan.pw = (plan.pairs_per_wave + passes - 1) / passes;
+  }
   return plan;
 }
 
@@ -488,7 +515,8 @@ int RunSkinny(const Bf16* x, const void* w, float* y, Bf16* y_bf16,
                     nullptr, 0, stream);
   }
   if (plan.engine) {
-    const EngineLauncher launch = PickEngine(plan.mt, plan.rg, static_cast<int>(m), kind);
+    const EngineLauncher launch =
+        PickEngine(plan.mt, plan.rg, plan.pw, static_cast<int>(m), kind);
     if (launch == nullptr)
       return Fail(VX_UNSUPPORTED, "no product engine for this plan");
     q8::TileArgs args{};

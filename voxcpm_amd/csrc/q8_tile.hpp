@@ -143,18 +143,20 @@ __host__ __device__ constexpr bool StagesRows(ASource source, int mt) {
 
 /// Floats of one wave's private row-staging region: PW pairs of 16 MT rows
 /// x 128 bytes.
-__host__ __device__ constexpr int StageFloats(int mt, int pw) {
-  return pw * mt * 16 * 32;
+/// Floats of a wave's row-staging region: one pair's 16 MT rows x 64
+/// columns of bf16 (the pairs of a pass are staged one after another).
+__host__ __device__ constexpr int StageFloats(int mt) {
+  return mt * 16 * 32;
 }
 
 /// LDS bytes the engine needs for `waves` waves. The row-staging regions
 /// and the waves' partial sums share the same bytes (a barrier separates
 /// them).
 __host__ __device__ constexpr std::size_t EngineShared(int mt, int rg, int waves,
-                                                      ASource source, int pw = 1) {
+                                                      ASource source) {
   std::size_t per_wave = static_cast<std::size_t>(rg) * mt * 256;
-  if (StagesRows(source, mt) && static_cast<std::size_t>(StageFloats(mt, pw)) > per_wave)
-    per_wave = static_cast<std::size_t>(StageFloats(mt, pw));
+  if (StagesRows(source, mt) && static_cast<std::size_t>(StageFloats(mt)) > per_wave)
+    per_wave = static_cast<std::size_t>(StageFloats(mt));
   std::size_t floats = static_cast<std::size_t>(waves) * per_wave;
   if (source == ASource::kNormF32)
     floats += static_cast<std::size_t>(waves) * kSquaresStride;
@@ -400,8 +402,11 @@ __device__ __forceinline__ void EngineBody(const TileArgs& a) {
                               column_ok && in_rows(row));
     }
   };
-  const auto stage_rows = [&](int p, const RawRows& raw, PairStage<MT, RG>& s) {
-    uint4* region = reinterpret_cast<uint4*>(lds + wave * StageFloats(MT, PW)) + p * MT * 128;
+  // The pairs of a pass go through the one region in turn: a wave's LDS
+  // accesses complete in order, so a pair's writes follow the previous
+  // pair's reads without a wait.
+  uint4* const region = reinterpret_cast<uint4*>(lds + wave * StageFloats(MT));
+  const auto stage_rows = [&](const RawRows& raw, PairStage<MT, RG>& s) {
 #pragma unroll
     for (int j = 0; j < JR; ++j) {
       // Rows outside the block were loaded as zero; writing them keeps the
@@ -557,8 +562,8 @@ __device__ __forceinline__ void EngineBody(const TileArgs& a) {
         multiply(stage[p]);
   } else if constexpr (StagesRows(SRC, MT)) {
     // Passes of PW pairs per wave (pair base + p waves + wave), every load
-    // of a pass issued before its first product; plans pick PW so that one
-    // pass covers k.
+    // of a pass issued before its first product, so that PW pairs per wave
+    // are in flight; plans pick PW so that few passes cover k.
     for (int base = 0; base < a.pairs; base += waves * PW) {
       PairStage<MT, RG> stage[PW];
       RawRows raw[PW];
@@ -569,7 +574,7 @@ __device__ __forceinline__ void EngineBody(const TileArgs& a) {
       }
 #pragma unroll
       for (int p = 0; p < PW; ++p) {
-        stage_rows(p, raw[p], stage[p]);
+        stage_rows(raw[p], stage[p]);
         if (base + p * waves + wave < a.pairs)
           multiply(stage[p]);
       }
