@@ -300,6 +300,61 @@ int vx_dit_status(vx_dit* dit);
 int vx_euler_schedule(size_t timesteps, float sway, int skip, float* t,
                       float* dt, int32_t* evaluate);
 
+/* ---- one MiniCPM4 stack with a key/value cache --------------------------
+ *
+ * ForwardStack (transformer.cpp:55-100) as one call: VoxCPM2's base LM and
+ * residual LM (one row per decode step, generator.cpp:482-510) and the
+ * local encoder (patch + 1 rows per patch, generator.cpp:252-295). */
+
+typedef struct vx_stack_shape {
+  size_t hidden;   /* TransformerConfig (config.hpp:15-31) */
+  size_t heads;
+  size_t kv_heads;
+  size_t head_dim;
+  size_t ffn;      /* intermediate */
+  size_t layers;
+  float eps;
+  int rope;        /* 1: rotary embedding from vx_stack_weights.rope;
+                      0: none (the residual LM, config.rope = false) */
+} vx_stack_shape;
+
+typedef struct vx_stack_weights {
+  const vx_dit_layer* layers; /* host array of `layers` entries
+                                 (StackWeights, weights.hpp:28-41) */
+  const uint16_t* norm;       /* final norm, bf16 [hidden] */
+  const float* rope;          /* device table [positions][head_dim]
+                                 (vx_rope_table), or NULL without rope */
+  uint32_t format;            /* vx_weight_format of every matrix */
+} vx_stack_weights;
+
+typedef struct vx_stack vx_stack;
+
+/* Creates a stack over caller-owned device weights (the handle keeps the
+ * pointers); scratch grows with the rows and cache lengths it is given. */
+int vx_stack_create(vx_stack** stack, const vx_stack_shape* shape,
+                    const vx_stack_weights* weights);
+void vx_stack_destroy(vx_stack* stack);
+
+/* ForwardStack (transformer.cpp:55-100, transformer.hpp:69-72): `rows`
+ * rows of the float32 residual stream hidden [rows][hidden] (updated in
+ * place) through every layer; the final norm's float32 output to
+ * output [rows][hidden]. The cache is the reference's KvCache
+ * (transformer.hpp:18-36): k_cache and v_cache [layers][kv_heads]
+ * [capacity][head_dim] float32, caller-owned; each layer writes its rows'
+ * keys and values at cache_rows [rows] (device) and rotates them at
+ * positions [rows] (device), then row r of sequence r / rows_per_sequence
+ * attends to keys s keys_per_sequence + 0 .. past + (causal ? r % rows_per_
+ * sequence + 1 : rows_per_sequence) - 1 (AttentionLayout,
+ * transformer.hpp:41-48). VX_BAD_ARG when rows is not a multiple of
+ * rows_per_sequence or the attended keys pass the capacity; positions and
+ * cache_rows must index the rotary table and the cache. */
+int vx_stack_forward(vx_stack* stack, float* hidden, float* output,
+                     size_t rows, const int32_t* positions,
+                     const int32_t* cache_rows, size_t rows_per_sequence,
+                     size_t keys_per_sequence, size_t past, int causal,
+                     float* k_cache, float* v_cache, size_t capacity,
+                     void* stream);
+
 /* The rotary table of MiniCPM's LongRoPE on the host, float32 as the
  * reference computes it (transformer.cpp:20-45): [positions][dim], cos in
  * the first half, sin in the second. factors: dim/2 values or NULL. */

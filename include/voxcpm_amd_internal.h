@@ -76,6 +76,35 @@ int vx_dit_path(const vx_dit* dit);
 int vx_dit_set_trace(vx_dit* dit, void* buffer, size_t bytes);
 size_t vx_dit_trace_bytes(const vx_dit* dit);
 
+/* The stack's paths: AUTO takes FUSED up to 32 rows (the DiT's fused layer
+ * kernels on fragment-order rows around the rotary/cache kernel and the
+ * split attention), else UNFUSED (transformer.cpp:55-100's launch
+ * sequence). */
+#define VX_STACK_PATH_AUTO 0
+#define VX_STACK_PATH_FUSED 2
+#define VX_STACK_PATH_UNFUSED 3
+
+/* Selects the path of later vx_stack_forward calls (VX_UNSUPPORTED when the
+ * shape has no fused kernels). */
+int vx_stack_set_path(vx_stack* stack, int path);
+/* The path a call of `rows` rows takes now, or -1 for a null handle. */
+int vx_stack_path(const vx_stack* stack, size_t rows);
+
+/* The stack's attention on one layer's cache (the arguments of
+ * vx_attention, kernels/generator_kernels.hpp): the keys of each (row, KV
+ * head) in chunks of 64 scored by separate workgroups, a second launch
+ * merging the chunks' statistics in chunk order when there are several;
+ * output bf16 [rows][heads][head_dim]. `partials` holds
+ * vx_split_attention_floats(...) floats (NULL when that is 0). */
+int vx_split_attention(const float* q, const float* k_cache,
+                       const float* v_cache, uint16_t* output, size_t rows,
+                       size_t rows_per_sequence, size_t keys_per_sequence,
+                       size_t past, int causal, size_t heads, size_t kv_heads,
+                       size_t head_dim, size_t capacity, float* partials,
+                       size_t partial_floats, void* stream);
+size_t vx_split_attention_floats(size_t rows, size_t heads, size_t head_dim,
+                                 size_t past, size_t rows_per_sequence);
+
 #ifdef __cplusplus
 }
 #endif

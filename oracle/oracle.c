@@ -701,3 +701,58 @@ void vo_dit_patch(const vo_dit* dit, const float* mu, const float* cond_latent,
   free(time);
   free(velocity);
 }
+
+/* ---- one MiniCPM4 stack with a key/value cache --------------------------- */
+
+static void stack_linear(const vo_stack* stack, const uint16_t* x,
+                         const uint8_t* w, float* y, size_t rows, size_t in,
+                         size_t out, int accumulate) {
+  if (stack->bf16_weights)
+    vo_bf16_linear(x, (const uint16_t*)w, y, rows, in, out, accumulate,
+                   stack->threads);
+  else
+    vo_q8_linear(x, w, y, rows, in, out, accumulate, stack->threads);
+}
+
+void vo_stack_forward(const vo_stack* stack, float* hidden, float* output,
+                      size_t rows, const int32_t* positions,
+                      const int32_t* cache_rows, size_t rows_per_sequence,
+                      size_t keys_per_sequence, size_t past, int causal,
+                      float* k_cache, float* v_cache, size_t capacity) {
+  /* transformer.cpp:55-100 */
+  const size_t width = stack->hidden;
+  const size_t q_width = stack->heads * stack->head_dim;
+  const size_t kv_width = stack->kv_heads * stack->head_dim;
+  const size_t qkv_width = q_width + 2 * kv_width;
+  const size_t ffn = stack->ffn;
+  const size_t layer_stride = stack->kv_heads * capacity * stack->head_dim;
+  size_t wide = ffn > qkv_width ? ffn : qkv_width;
+  if (width > wide)
+    wide = width;
+  uint16_t* bf16 = (uint16_t*)malloc(rows * wide * sizeof(uint16_t));
+  float* qkv = (float*)malloc(rows * qkv_width * sizeof(float));
+  float* q = (float*)malloc(rows * q_width * sizeof(float));
+  float* gate_up = (float*)malloc(rows * 2 * ffn * sizeof(float));
+  for (size_t l = 0; l < stack->layers; ++l) {
+    const vo_layer* layer = &stack->layer[l];
+    float* keys = k_cache + l * layer_stride;
+    float* values = v_cache + l * layer_stride;
+    vo_rms_norm(hidden, layer->input_norm, bf16, NULL, rows, width, stack->eps);
+    stack_linear(stack, bf16, layer->qkv, qkv, rows, width, qkv_width, 0);
+    vo_qkv_rope(qkv, stack->rope, positions, cache_rows, q, keys, values, rows,
+                stack->heads, stack->kv_heads, stack->head_dim, capacity);
+    vo_attention(q, keys, values, bf16, rows, rows_per_sequence,
+                 keys_per_sequence, past, causal, stack->heads,
+                 stack->kv_heads, stack->head_dim, capacity);
+    stack_linear(stack, bf16, layer->o, hidden, rows, q_width, width, 1);
+    vo_rms_norm(hidden, layer->post_norm, bf16, NULL, rows, width, stack->eps);
+    stack_linear(stack, bf16, layer->gate_up, gate_up, rows, width, 2 * ffn, 0);
+    vo_swiglu(gate_up, bf16, rows, ffn);
+    stack_linear(stack, bf16, layer->down, hidden, rows, ffn, width, 1);
+  }
+  vo_rms_norm(hidden, stack->norm, bf16, output, rows, width, stack->eps);
+  free(bf16);
+  free(qkv);
+  free(q);
+  free(gate_up);
+}

@@ -180,6 +180,31 @@ void vo_dit_patch(const vo_dit* dit, const float* mu, const float* cond_latent,
                   const int32_t* evaluate, size_t steps, float cfg,
                   int zero_star);
 
+/* ---- one MiniCPM4 stack with a key/value cache (the LMs, the encoder) -- */
+
+typedef struct vo_stack {
+  size_t hidden, heads, kv_heads, head_dim, ffn, layers;
+  float eps;
+  const float* rope; /* rotary table [positions][head_dim], or NULL for a
+                        stack without rotary embedding (the residual LM) */
+  const vo_layer* layer;
+  const uint16_t* norm; /* final norm, bf16 [hidden] */
+  int threads;          /* for the products */
+  int bf16_weights;     /* bf16 rows [out][in] instead of Q8_0 blocks */
+} vo_stack;
+
+/* ForwardStack (transformer.cpp:55-100): `rows` rows of the float32
+ * residual stream hidden [rows][hidden] (updated in place) through every
+ * layer, the final norm's float32 output to output [rows][hidden]. Each
+ * layer writes its rows' keys and values into k_cache / v_cache
+ * [layer][kv_head][capacity][head_dim] at cache_rows and attends as
+ * vo_attention does (rows_per_sequence, keys_per_sequence, past, causal). */
+void vo_stack_forward(const vo_stack* stack, float* hidden, float* output,
+                      size_t rows, const int32_t* positions,
+                      const int32_t* cache_rows, size_t rows_per_sequence,
+                      size_t keys_per_sequence, size_t past, int causal,
+                      float* k_cache, float* v_cache, size_t capacity);
+
 #ifdef __cplusplus
 }
 #endif

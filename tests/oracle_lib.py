@@ -84,6 +84,11 @@ _SIGNATURES = {
     "vo_dit_patch": ([ctypes.POINTER(Dit), c_void_p, c_void_p, c_void_p,
                       c_void_p, c_void_p, c_void_p, c_size, c_float, c_int],
                      None),
+    # (vo_stack*, hidden, output, rows, positions, cache_rows,
+    #  rows_per_sequence, keys_per_sequence, past, causal, k, v, capacity)
+    "vo_stack_forward": ([c_void_p, c_void_p, c_void_p, c_size, c_void_p, c_void_p,
+                          c_size, c_size, c_size, c_int, c_void_p, c_void_p, c_size],
+                         None),
 }
 
 _lib = None
@@ -181,6 +186,13 @@ def rope_table(theta: float, dim: int, factors, scaling: float,
     return table
 
 
+class Stack(ctypes.Structure):
+    _fields_ = [(name, c_size) for name in (
+        "hidden", "heads", "kv_heads", "head_dim", "ffn", "layers")] + [
+        ("eps", ctypes.c_float), ("rope", c_void_p), ("layer", ctypes.POINTER(Layer)),
+        ("norm", c_void_p), ("threads", ctypes.c_int), ("bf16_weights", ctypes.c_int)]
+
+
 class OracleDit:
     """A vo_dit over host copies of synthetic weights."""
 
@@ -260,3 +272,51 @@ class OracleDit:
                            ptr(x), ptr(t), ptr(dt), ptr(evaluate), len(t), cfg,
                            int(zero_star))
         return x
+
+
+class OracleStack:
+    """A vo_stack over host copies of synthetic stack weights."""
+
+    def __init__(self, weights, rope: np.ndarray | None, threads: int = 8,
+                 bf16_weights: bool = False):
+        config = weights.config
+        self.config = config
+        self._keep = []
+
+        def keep(array):
+            array = np.ascontiguousarray(array)
+            if bf16_weights and array.ndim == 3 and array.shape[-1] == 34:
+                n, blocks, _ = array.shape
+                array = q8_dequant_bf16(array, n, blocks * 32)
+            self._keep.append(array)
+            return array.ctypes.data
+
+        layers = (Layer * config.layers)()
+        for index, layer in enumerate(weights.layers):
+            layers[index] = Layer(keep(layer["input_norm"]), keep(layer["qkv"]),
+                                  keep(layer["o"]), keep(layer["post_norm"]),
+                                  keep(layer["gate_up"]), keep(layer["down"]))
+        self._layers = layers
+        table = None if rope is None else keep(np.asarray(rope, dtype=np.float32))
+        self.struct = Stack(config.hidden, config.heads, config.kv_heads, config.head_dim,
+                            config.ffn, config.layers, config.eps, table, layers,
+                            keep(weights.norm), threads, int(bf16_weights))
+
+    def forward(self, hidden, positions, cache_rows, rows_per_sequence: int,
+                keys_per_sequence: int, past: int, causal: bool, k_cache, v_cache):
+        """ForwardStack: returns (hidden after the layers, the final norm's
+        output); k_cache / v_cache [layers][kv_heads][capacity][head_dim]
+        float32 are updated in place."""
+        hidden = np.array(hidden, dtype=np.float32, copy=True)
+        rows = hidden.shape[0]
+        output = np.zeros_like(hidden)
+        positions = np.ascontiguousarray(positions, dtype=np.int32)
+        cache_rows = np.ascontiguousarray(cache_rows, dtype=np.int32)
+        assert k_cache.dtype == np.float32 and k_cache.flags.c_contiguous
+        assert v_cache.dtype == np.float32 and v_cache.flags.c_contiguous
+        capacity = k_cache.shape[2]
+        lib().vo_stack_forward(ctypes.addressof(self.struct), ptr(hidden), ptr(output), rows,
+                               ptr(positions), ptr(cache_rows), rows_per_sequence,
+                               keys_per_sequence, past, int(causal), ptr(k_cache),
+                               ptr(v_cache), capacity)
+        return hidden, output

@@ -509,3 +509,120 @@ def test_dit_patch_composes_evaluations(oracle):
         oracle.lib().vo_guided_euler(oracle.ptr(flat), oracle.ptr(x), x.size, 2.0,
                                      float(dt[step]), 1)
     assert np.array_equal(got, x)
+
+
+# ---- a stack with a key/value cache against a float64 torch formulation ----
+
+def torch_stack(weights, oracle, rope, hidden, sequences, causal):
+    """The MiniCPM4 stack in float64 torch from its description over whole
+    sequences (no cache: every key of a sequence at once, torch's attention
+    with its own causal mask). hidden [S][T][hidden] float; returns
+    (residual stream after the layers, final norm's output)."""
+    c = weights.config
+    td = torch.float64
+
+    def W(blocks):
+        n, kb, _ = blocks.shape
+        return torch.from_numpy(oracle.q8_values(np.ascontiguousarray(blocks), n, kb * 32))
+
+    def vec(bits):
+        return torch.from_numpy(synth.bf16_values(bits).astype(np.float64))
+
+    def rms(h, g):
+        return h / torch.sqrt((h * h).mean(-1, keepdim=True) + c.eps) * vec(g)
+
+    h = torch.from_numpy(hidden.astype(np.float64)).reshape(sequences, -1, c.hidden)
+    length = h.shape[1]
+    half = c.head_dim // 2
+    if rope is not None:
+        table = torch.from_numpy(rope[:length].astype(np.float64))
+        cos, sin = table[:, :half], table[:, half:]
+
+    def rotate(v):
+        if rope is None:
+            return v
+        a, b = v[..., :half], v[..., half:]
+        return torch.cat([a * cos - b * sin, b * cos + a * sin], -1)
+
+    for layer in weights.layers:
+        qkv = rms(h, layer["input_norm"]) @ W(layer["qkv"]).T
+        qw, kw = c.q_width, c.kv_heads * c.head_dim
+        q = qkv[..., :qw].reshape(sequences, length, c.heads, c.head_dim).transpose(1, 2)
+        k = qkv[..., qw:qw + kw].reshape(sequences, length, c.kv_heads, c.head_dim).transpose(1, 2)
+        v = qkv[..., qw + kw:].reshape(sequences, length, c.kv_heads, c.head_dim).transpose(1, 2)
+        q, k = rotate(q), rotate(k)
+        g = c.heads // c.kv_heads
+        k, v = k.repeat_interleave(g, 1), v.repeat_interleave(g, 1)
+        a = torch.nn.functional.scaled_dot_product_attention(q, k, v, is_causal=causal)
+        h = h + a.transpose(1, 2).reshape(sequences, length, qw) @ W(layer["o"]).T
+        gu = rms(h, layer["post_norm"]) @ W(layer["gate_up"]).T
+        h = h + (torch.nn.functional.silu(gu[..., :c.ffn]) * gu[..., c.ffn:]) @ W(layer["down"]).T
+    return h.reshape(-1, c.hidden).numpy(), rms(h, weights.norm).reshape(-1, c.hidden).numpy()
+
+
+def relative(a, b):
+    return float(np.linalg.norm(np.asarray(a, np.float64) - b) / np.linalg.norm(b))
+
+
+STACK_CONFIGS = [
+    synth.StackConfig(hidden=256, heads=4, kv_heads=2, head_dim=64, ffn=512, layers=2,
+                      rope_factors=tuple(1.0 + 0.1 * i for i in range(32))),
+    synth.StackConfig(hidden=128, heads=2, kv_heads=1, head_dim=64, ffn=256, layers=2,
+                      rope=False),
+]
+
+
+@pytest.mark.parametrize("config", STACK_CONFIGS, ids=["gqa-rope", "no-rope"])
+def test_stack_incremental_decode_equals_full_causal_forward(oracle, config):
+    """A causal prefill of 6 rows, then 3 one-row steps through the cache
+    (the LM's decode: positions = cache rows = past), equal row for row the
+    whole 9-row causal sequence in float64 torch."""
+    rope = oracle.rope_table(config.rope_theta, config.head_dim, config.rope_factors,
+                             config.rope_scaling, 16) if config.rope else None
+    weights = synth.stack_weights(config, 21)
+    stack = oracle.OracleStack(weights, rope, threads=4)
+    rng = synth.Rng(22, 1)
+    total, prefix, capacity = 9, 6, 12
+    h0 = rng.normal(total * config.hidden).astype(np.float32).reshape(total, config.hidden)
+    ref_h, ref_out = torch_stack(weights, oracle, rope, h0, 1, True)
+    shape = (config.layers, config.kv_heads, capacity, config.head_dim)
+    k_cache, v_cache = np.zeros(shape, np.float32), np.zeros(shape, np.float32)
+    rows = np.arange(prefix, dtype=np.int32)
+    h, out = stack.forward(h0[:prefix], rows, rows, prefix, prefix, 0, True, k_cache, v_cache)
+    assert relative(out, ref_out[:prefix]) < 5e-4
+    assert relative(h, ref_h[:prefix]) < 5e-4
+    for position in range(prefix, total):
+        at = np.array([position], np.int32)
+        h, out = stack.forward(h0[position:position + 1], at, at, 1, 1, position, True,
+                               k_cache, v_cache)
+        assert relative(out, ref_out[position:position + 1]) < 5e-4, position
+        assert relative(h, ref_h[position:position + 1]) < 5e-4, position
+    # A planted slip: the last step attending one key short (past - 1)
+    # moves the output well past the bound (bf16 activations against
+    # float64 stay near 1e-4).
+    kc, vc = k_cache.copy(), v_cache.copy()
+    at = np.array([total - 1], np.int32)
+    _, bad = stack.forward(h0[total - 1:], at, at, 1, 1, total - 2, True, kc, vc)
+    assert relative(bad, ref_out[total - 1:]) > 2e-3
+
+
+def test_stack_bidirectional_sequences(oracle):
+    """The local encoder's layout: two 5-row sequences attending within
+    themselves, non-causal, rotary positions row % 5, against float64 torch;
+    swapping the two sequences' rows moves every output."""
+    config = STACK_CONFIGS[0]
+    rope = oracle.rope_table(config.rope_theta, config.head_dim, config.rope_factors,
+                             config.rope_scaling, 8)
+    weights = synth.stack_weights(config, 23)
+    stack = oracle.OracleStack(weights, rope, threads=4)
+    rng = synth.Rng(24, 1)
+    h0 = rng.normal(10 * config.hidden).astype(np.float32).reshape(10, config.hidden)
+    ref_h, ref_out = torch_stack(weights, oracle, rope, h0, 2, False)
+    shape = (config.layers, config.kv_heads, 10, config.head_dim)
+    k_cache, v_cache = np.zeros(shape, np.float32), np.zeros(shape, np.float32)
+    positions = (np.arange(10) % 5).astype(np.int32)
+    h, out = stack.forward(h0, positions, np.arange(10, dtype=np.int32), 5, 5, 0, False,
+                           k_cache, v_cache)
+    assert relative(out, ref_out) < 5e-4
+    assert relative(h, ref_h) < 5e-4
+    assert relative(out[::-1], ref_out) > 5e-2

@@ -63,6 +63,22 @@ class DitWeights(ctypes.Structure):
 VX_WEIGHTS_Q8_0 = 0
 VX_WEIGHTS_BF16 = 1
 
+# Stack paths (voxcpm_amd_internal.h).
+STACK_PATH_AUTO = 0
+STACK_PATH_FUSED = 2
+STACK_PATH_UNFUSED = 3
+
+
+class StackShape(ctypes.Structure):
+    _fields_ = [(name, c_size) for name in (
+        "hidden", "heads", "kv_heads", "head_dim", "ffn", "layers")] + [
+        ("eps", ctypes.c_float), ("rope", c_int)]
+
+
+class StackWeights(ctypes.Structure):
+    _fields_ = [("layers", ctypes.POINTER(DitLayer)), ("norm", c_void_p),
+                ("rope", c_void_p), ("format", ctypes.c_uint32)]
+
 
 _SIGNATURES = {
     "vx_last_error": ([], ctypes.c_char_p),
@@ -117,6 +133,19 @@ _SIGNATURES = {
     "vx_dit_path": ([c_void_p], c_int),
     "vx_dit_set_trace": ([c_void_p, c_void_p, c_size], c_int),
     "vx_dit_trace_bytes": ([c_void_p], c_size),
+    "vx_stack_create": ([ctypes.POINTER(c_void_p), ctypes.POINTER(StackShape),
+                         ctypes.POINTER(StackWeights)], c_int),
+    "vx_stack_destroy": ([c_void_p], None),
+    # (stack, hidden, output, rows, positions, cache_rows, rows_per_sequence,
+    #  keys_per_sequence, past, causal, k_cache, v_cache, capacity, stream)
+    "vx_stack_forward": ([c_void_p, c_void_p, c_void_p, c_size, c_void_p, c_void_p,
+                          c_size, c_size, c_size, c_int, c_void_p, c_void_p, c_size,
+                          c_void_p], c_int),
+    "vx_stack_set_path": ([c_void_p, c_int], c_int),
+    "vx_stack_path": ([c_void_p, c_size], c_int),
+    "vx_split_attention": ([c_void_p] * 4 + [c_size] * 4 + [c_int] + [c_size] * 4
+                           + [c_void_p, c_size, c_void_p], c_int),
+    "vx_split_attention_floats": ([c_size] * 5, c_size),
     "vx_euler_schedule": ([c_size, c_float, c_int, c_void_p, c_void_p,
                            c_void_p], c_int),
     "vx_rope_table": ([ctypes.c_double, c_size, c_void_p, c_float, c_size,

@@ -539,6 +539,11 @@ bool Supported(const Shape& s) {
          s.head_dim <= 256 && s.heads % s.kv_heads == 0;
 }
 
+bool StackSupported(const Shape& s) {
+  return s.rows <= q8::kFragRows && s.hidden % 64 == 0 && s.hidden <= 2 * 64 * kMaxWaves &&
+         (s.heads * s.head_dim) % 64 == 0 && s.ffn % 64 == 0 && s.heads % s.kv_heads == 0;
+}
+
 void InAssemble(const float* x, const void* in_weight, const Bf16* in_bias,
                 const float* mu, const float* time, const float* cond_rows,
                 float* h, const Shape& s, hipStream_t stream) {

@@ -36,6 +36,11 @@ struct Shape {
 /// feat <= 64, head_dim even and <= 256.
 bool Supported(const Shape& s);
 
+/// Whether the layer kernels (Qkv, Residual, GateUp) take a stack of this
+/// shape, the DiT's input and output kernels aside: up to 32 rows, widths
+/// multiples of 64, hidden <= 2048.
+bool StackSupported(const Shape& s);
+
 /// Residual stream rows (float32 fragment order [32][hidden]) from in_proj
 /// of x [patch][feat] (bf16 conversion, product, bias) and the assembly of
 /// mu, the time vector and the condition rows (generator.cpp:297-316;

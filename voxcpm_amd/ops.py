@@ -13,12 +13,13 @@ import torch
 
 from . import synth
 from ._lib import (VX_WEIGHTS_BF16, VX_WEIGHTS_Q8_0, DitLayer, DitProjection, DitShape,
-                   DitWeights, check, lib)
+                   DitWeights, StackShape, StackWeights, check, lib)
 
 __all__ = [
     "Scratch", "Dit", "q8_pack", "q8_unpack_blocks", "q8_unpack_bf16",
     "q8_linear", "q8_linear_bf16", "q8_plan", "bf16_pack", "bf16_unpack", "bf16_linear",
-    "bf16_linear_rows", "stream_read", "euler_schedule", "rope_table",
+    "bf16_linear_rows", "stream_read", "euler_schedule", "rope_table", "Stack",
+    "split_attention",
 ]
 
 
@@ -338,3 +339,108 @@ class Dit:
             dt.ctypes.data, evaluate.ctypes.data, len(t), cfg, int(zero_star),
             _stream(stream)))
         return x
+
+
+def split_attention(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
+                    rows_per_sequence: int, keys_per_sequence: int, past: int,
+                    causal: bool, heads: int, kv_heads: int, stream=None) -> torch.Tensor:
+    """The stack's attention on one layer's cache: q float32 [rows][heads][D],
+    k_cache / v_cache float32 [kv_heads][capacity][D] -> bf16 [rows][heads][D]."""
+    rows, _, head_dim = q.shape
+    capacity = k_cache.shape[1]
+    out = torch.empty((rows, heads, head_dim), dtype=torch.bfloat16, device=q.device)
+    floats = lib().vx_split_attention_floats(rows, heads, head_dim, past, rows_per_sequence)
+    partials = torch.empty(max(floats, 1), dtype=torch.float32, device=q.device)
+    check(lib().vx_split_attention(_ptr(q), _ptr(k_cache), _ptr(v_cache), _ptr(out), rows,
+                                   rows_per_sequence, keys_per_sequence, past, int(causal),
+                                   heads, kv_heads, head_dim, capacity,
+                                   _ptr(partials) if floats else None, floats,
+                                   _stream(stream)))
+    return out
+
+
+class Stack:
+    """vx_stack (ForwardStack with a key/value cache) over device copies of
+    synthetic stack weights."""
+
+    def __init__(self, weights: synth.StackWeightsHost, rope: np.ndarray | None,
+                 device=None, stream=None, bf16_weights: bool = False):
+        self.config = config = weights.config
+        device = _device(device)
+        self._keep = []
+
+        def upload_q8(blocks: np.ndarray) -> torch.Tensor:
+            n, kb, _ = blocks.shape
+            raw = torch.from_numpy(np.ascontiguousarray(blocks)).to(device)
+            packed = q8_pack(raw, n, kb * 32, stream)
+            if bf16_weights:
+                packed = bf16_pack(q8_unpack_bf16(packed, n, kb * 32, stream), stream)
+            self._keep.append(packed)
+            return packed
+
+        def upload_bf16(bits: np.ndarray) -> torch.Tensor:
+            tensor = torch.from_numpy(bits.view(np.int16).copy()).to(device)
+            self._keep.append(tensor)
+            return tensor
+
+        layer_array = (DitLayer * config.layers)()
+        for index, layer in enumerate(weights.layers):
+            layer_array[index] = DitLayer(
+                upload_bf16(layer["input_norm"]).data_ptr(),
+                upload_q8(layer["qkv"]).data_ptr(),
+                upload_q8(layer["o"]).data_ptr(),
+                upload_bf16(layer["post_norm"]).data_ptr(),
+                upload_q8(layer["gate_up"]).data_ptr(),
+                upload_q8(layer["down"]).data_ptr())
+        rope_ptr = None
+        if config.rope:
+            table = torch.from_numpy(np.ascontiguousarray(rope, dtype=np.float32)).to(device)
+            self._keep.append(table)
+            rope_ptr = table.data_ptr()
+        self._layers = layer_array
+        self._weights = StackWeights(layer_array, upload_bf16(weights.norm).data_ptr(),
+                                     rope_ptr,
+                                     VX_WEIGHTS_BF16 if bf16_weights else VX_WEIGHTS_Q8_0)
+        self._shape = StackShape(config.hidden, config.heads, config.kv_heads,
+                                 config.head_dim, config.ffn, config.layers, config.eps,
+                                 int(config.rope))
+        torch.cuda.synchronize(device)
+        handle = ctypes.c_void_p()
+        check(lib().vx_stack_create(ctypes.byref(handle), ctypes.byref(self._shape),
+                                    ctypes.byref(self._weights)))
+        self.handle = handle
+        self.device = device
+
+    def close(self) -> None:
+        if getattr(self, "handle", None):
+            lib().vx_stack_destroy(self.handle)
+            self.handle = ctypes.c_void_p()
+
+    def __del__(self):
+        self.close()
+
+    def set_path(self, path: int) -> None:
+        """Selects the path (voxcpm_amd._lib.STACK_PATH_*)."""
+        check(lib().vx_stack_set_path(self.handle, path))
+
+    def path(self, rows: int) -> int:
+        return lib().vx_stack_path(self.handle, rows)
+
+    def cache(self, capacity: int) -> tuple[torch.Tensor, torch.Tensor]:
+        """A zeroed key/value cache [layers][kv_heads][capacity][head_dim]."""
+        c = self.config
+        shape = (c.layers, c.kv_heads, capacity, c.head_dim)
+        return (torch.zeros(shape, dtype=torch.float32, device=self.device),
+                torch.zeros(shape, dtype=torch.float32, device=self.device))
+
+    def forward(self, hidden: torch.Tensor, output: torch.Tensor, positions: torch.Tensor,
+                cache_rows: torch.Tensor, rows_per_sequence: int, keys_per_sequence: int,
+                past: int, causal: bool, k_cache: torch.Tensor, v_cache: torch.Tensor,
+                stream=None) -> None:
+        """ForwardStack: hidden float32 [rows][hidden] (in place), output
+        float32 [rows][hidden], positions / cache_rows int32 [rows]."""
+        rows = hidden.shape[0]
+        check(lib().vx_stack_forward(self.handle, _ptr(hidden), _ptr(output), rows,
+                                     _ptr(positions), _ptr(cache_rows), rows_per_sequence,
+                                     keys_per_sequence, past, int(causal), _ptr(k_cache),
+                                     _ptr(v_cache), k_cache.shape[2], _stream(stream)))

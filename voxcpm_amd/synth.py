@@ -242,3 +242,62 @@ def patch_inputs(config: DitConfig, seed: int) -> PatchInputs:
     noise = rng.normal(config.patch * config.feat).astype(np.float32)
     return PatchInputs(mu.copy(), cond.reshape(config.patch, config.feat).copy(),
                        noise.reshape(config.patch, config.feat))
+
+
+@dataclasses.dataclass(frozen=True)
+class StackConfig:
+    """A MiniCPM4 stack with a key/value cache (vx_stack_shape): the LMs
+    and the local encoder (config.hpp:15-31)."""
+    hidden: int = 2048
+    heads: int = 16
+    kv_heads: int = 2
+    head_dim: int = 128
+    ffn: int = 6144
+    layers: int = 28
+    eps: float = 1e-5
+    rope: bool = True
+    rope_theta: float = 10000.0
+    rope_factors: tuple | None = None
+    rope_scaling: float = 1.0
+
+    @property
+    def q_width(self) -> int:
+        return self.heads * self.head_dim
+
+    @property
+    def qkv_width(self) -> int:
+        return (self.heads + 2 * self.kv_heads) * self.head_dim
+
+
+# VoxCPM2's stacks (tests/config_samples.hpp of the reference): the base LM
+# (28 layers, hidden 2048, MLP 6144, 16 q heads x 128 with 2 KV heads,
+# LongRoPE), the residual LM (8 layers, no rotary embedding) and the local
+# encoder (12 layers, hidden 1024, MLP 4096, heads as the LM's).
+VOXCPM2_BASE_LM = StackConfig(rope_factors=VOXCPM2_SHORT_FACTORS)
+VOXCPM2_RESIDUAL_LM = StackConfig(layers=8, rope=False)
+VOXCPM2_ENCODER = StackConfig(hidden=1024, ffn=4096, layers=12,
+                              rope_factors=VOXCPM2_SHORT_FACTORS)
+
+
+@dataclasses.dataclass
+class StackWeightsHost:
+    """Host copies of a stack's weights: GGML Q8_0 blocks and bf16 vectors."""
+    config: StackConfig
+    layers: list  # dicts: input_norm, qkv, o, post_norm, gate_up, down
+    norm: np.ndarray
+
+
+def stack_weights(config: StackConfig, seed: int) -> StackWeightsHost:
+    rng = Rng(seed, 3)
+    layers = []
+    h = config.hidden
+    for _ in range(config.layers):
+        layers.append({
+            "input_norm": bf16_vector(rng, h, 1.0, 0.02),
+            "qkv": q8_blocks(rng, config.qkv_width, h),
+            "o": q8_blocks(rng, h, config.q_width),
+            "post_norm": bf16_vector(rng, h, 1.0, 0.02),
+            "gate_up": q8_blocks(rng, 2 * config.ffn, h),
+            "down": q8_blocks(rng, h, config.ffn),
+        })
+    return StackWeightsHost(config, layers, bf16_vector(rng, h, 1.0, 0.02))
