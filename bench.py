@@ -233,6 +233,108 @@ def gpu_lm(args, torch, ops, synth, device, stream):
             "residual_lm_products_us_m1": round(8 * layer_us, 1)}
 
 
+def device_stack_weights(torch, synth, config, device, seed: int):
+    """Random weights of a stack's shape made on the device (GGML Q8_0
+    blocks: int8 uniform in [-127, 127], float16 scales |N(0, 0.02)| / 127;
+    norms bf16(1 + N(0, 0.02))): the decode benchmark's 28 distinct layers
+    (1.4 GB) without host generation."""
+    gen = torch.Generator(device=device)
+    gen.manual_seed(seed)
+
+    def blocks(n, k):
+        kb = k // 32
+        q = torch.randint(-127, 128, (n, kb, 32), dtype=torch.int8, device=device,
+                          generator=gen)
+        scale = (torch.randn((n, kb), device=device, generator=gen).abs() * (0.02 / 127))
+        out = torch.empty((n, kb, 34), dtype=torch.uint8, device=device)
+        out[..., :2] = scale.to(torch.float16).view(torch.uint8).view(n, kb, 2)
+        out[..., 2:] = q.view(torch.uint8)
+        return out
+
+    def norm(width):
+        values = 1.0 + 0.02 * torch.randn(width, device=device, generator=gen)
+        return values.to(torch.bfloat16).view(torch.int16)
+
+    h = config.hidden
+    layers = [{"input_norm": norm(h), "qkv": blocks(config.qkv_width, h),
+               "o": blocks(h, config.q_width), "post_norm": norm(h),
+               "gate_up": blocks(2 * config.ffn, h), "down": blocks(h, config.ffn)}
+              for _ in range(config.layers)]
+    return synth.StackWeightsHost(config, layers, norm(h))
+
+
+def stack_bytes(config, rows_keys: int) -> int:
+    """Algorithmic bytes of one forward: every layer's Q8_0 weights read
+    once, plus the float32 keys and values the rows attend to."""
+    layer = (q8_bytes(config.hidden, config.qkv_width) + q8_bytes(config.q_width, config.hidden)
+             + q8_bytes(config.hidden, 2 * config.ffn) + q8_bytes(config.ffn, config.hidden))
+    cache = 2 * config.kv_heads * rows_keys * config.head_dim * 4
+    return config.layers * (layer + cache)
+
+
+def gpu_lm_step(args, torch, ops, synth, device, stream):
+    """One decode step of VoxCPM2's base LM (28 layers, one row at `past`
+    cached positions), of the residual LM (8 layers, no rotary embedding)
+    and one encoder call (12 layers, one 5-row patch), each on its fused and
+    per-kernel paths; eager launches, inputs and caches resident."""
+    from voxcpm_amd import _lib
+    rope = ops.rope_table(10000.0, 128, synth.VOXCPM2_SHORT_FACTORS, 1.0, 8192)
+    start = torch.cuda.Event(enable_timing=True)
+    stop = torch.cuda.Event(enable_timing=True)
+    out = {}
+    cases = [("base_lm", synth.VOXCPM2_BASE_LM, 1, [128, 1024, 4096]),
+             ("residual_lm", synth.VOXCPM2_RESIDUAL_LM, 1, [1024]),
+             ("encoder", synth.VOXCPM2_ENCODER, 5, [0])]
+    for name, config, rows, pasts in cases:
+        weights = device_stack_weights(torch, synth, config, device, 7)
+        stack = ops.Stack(weights, rope if config.rope else None, device, stream)
+        del weights
+        capacity = max(pasts) + rows + 1
+        k, v = stack.cache(capacity)
+        k.normal_()
+        v.normal_()
+        hidden0 = torch.randn((rows, config.hidden), dtype=torch.float32, device=device)
+        hidden = hidden0.clone()
+        output = torch.empty_like(hidden)
+        entry = {}
+        for past in pasts:
+            causal = rows == 1
+            positions = torch.arange(past, past + rows, dtype=torch.int32, device=device) \
+                if causal else torch.arange(rows, dtype=torch.int32, device=device)
+            for path_name, path in (("fused", _lib.STACK_PATH_AUTO),
+                                    ("unfused", _lib.STACK_PATH_UNFUSED)):
+                stack.set_path(path)
+
+                def once():
+                    hidden.copy_(hidden0)
+                    stack.forward(hidden, output, positions, positions, rows, rows, past,
+                                  causal, k, v, stream)
+
+                for _ in range(3):
+                    once()
+                torch.cuda.synchronize()
+                steps = max(10, args.steps // 2)
+                start.record(stream)
+                for _ in range(steps):
+                    once()
+                stop.record(stream)
+                stop.synchronize()
+                us = start.elapsed_time(stop) * 1e3 / steps
+                keys = past + (1 if causal else rows)
+                nbytes = stack_bytes(config, rows * keys)
+                entry[f"{path_name}_past{past}"] = {
+                    "us": round(us, 1), "bytes": nbytes,
+                    "gbs": round(nbytes / us / 1e3, 1),
+                    "hbm_frac": round(nbytes / us / 1e3 / HBM_PEAK_GBS, 4)}
+                log(f"  {name} rows {rows} past {past} {path_name}: {us:.1f} us "
+                    f"({nbytes / us / 1e3:.0f} GB/s of weights + cache)")
+        out[name] = {"layers": config.layers, "rows": rows, **entry}
+        stack.close()
+        del stack, k, v
+        torch.cuda.empty_cache()
+    return out
+
+
 def gpu_bf16(args, torch, ops, synth, device, stream):
     """The sweep shapes at M=22 on bf16 weights (2 N K bytes): panels
     (vx_bf16_linear) and rows as they come (vx_bf16_linear_rows), rotated
@@ -523,6 +625,8 @@ def main() -> int:
     log(f"read probe {probe:.0f} GB/s")
     products = gpu_products(args, torch, ops, synth, device, stream)
     lm = None if args.no_lm else gpu_lm(args, torch, ops, synth, device, stream)
+    if lm is not None:
+        lm["steps"] = gpu_lm_step(args, torch, ops, synth, device, stream)
     bf16 = None if args.no_bf16 else gpu_bf16(args, torch, ops, synth, device, stream)
     prefill = None if args.no_prefill else gpu_prefill(args, torch, ops, synth, device, stream)
     patch = None if args.no_patch else gpu_patch(args, torch, ops, synth, device, stream)

@@ -76,13 +76,17 @@ int vx_dit_path(const vx_dit* dit);
 int vx_dit_set_trace(vx_dit* dit, void* buffer, size_t bytes);
 size_t vx_dit_trace_bytes(const vx_dit* dit);
 
-/* The stack's paths: AUTO takes FUSED up to 32 rows (the DiT's fused layer
- * kernels on fragment-order rows around the rotary/cache kernel and the
- * split attention), else UNFUSED (transformer.cpp:55-100's launch
- * sequence). */
+/* The stack's paths: AUTO takes ROWS up to 8 rows (one-tile products on
+ * the row-major residual stream, the norms folded into qkv and gate_up,
+ * SwiGLU into gate_up's epilogue, the residual adds into o and down), FUSED
+ * up to 32 rows (the DiT's fused layer kernels on fragment-order rows),
+ * else UNFUSED (transformer.cpp:55-100's launch sequence); every path
+ * shares the rotary/cache kernel and the split attention. A path that
+ * cannot take a call's rows runs UNFUSED. */
 #define VX_STACK_PATH_AUTO 0
 #define VX_STACK_PATH_FUSED 2
 #define VX_STACK_PATH_UNFUSED 3
+#define VX_STACK_PATH_ROWS 4
 
 /* Selects the path of later vx_stack_forward calls (VX_UNSUPPORTED when the
  * shape has no fused kernels). */

@@ -106,17 +106,22 @@ STACKS = {
 }
 
 
+PATHS = {"auto": (_lib.STACK_PATH_AUTO, _lib.STACK_PATH_ROWS),
+         "fragments": (_lib.STACK_PATH_FUSED, _lib.STACK_PATH_FUSED),
+         "unfused": (_lib.STACK_PATH_UNFUSED, _lib.STACK_PATH_UNFUSED)}
+
+
 @pytest.mark.parametrize("name", list(STACKS))
-@pytest.mark.parametrize("path", [_lib.STACK_PATH_AUTO, _lib.STACK_PATH_UNFUSED],
-                         ids=["fused", "unfused"])
+@pytest.mark.parametrize("path", list(PATHS))
 def test_stack_prefill_then_decode(vx, oracle, cuda, stream, name, path):
     """A causal prefill of 7 rows, then one-row decode steps (positions =
     cache rows = past) through a cache long enough to split the attention
-    into several chunks; the caches match too."""
+    into several chunks; the caches match too. AUTO takes the one-tile
+    row-major kernels at these row counts."""
     config = STACKS[name]
     run = Run(vx, oracle, cuda, config, 41, capacity=160)
-    run.gpu.set_path(path)
-    expected = _lib.STACK_PATH_FUSED if path == _lib.STACK_PATH_AUTO else path
+    selected, expected = PATHS[path]
+    run.gpu.set_path(selected)
     assert run.gpu.path(1) == expected
     rng = synth.Rng(42, 1)
     prefix = 7
@@ -141,13 +146,16 @@ def test_stack_prefill_then_decode(vx, oracle, cuda, stream, name, path):
 def test_stack_encoder_layout(vx, oracle, cuda, stream):
     """The local encoder's call (generator.cpp:252-295): patches of 5 rows
     attending within themselves, rotary positions row % 5, cache rows in
-    order; three patches at once and one alone."""
+    order; three and four patches at once (15 and 20 rows: the
+    fragment-order kernels) and one alone (the one-tile kernels)."""
     config = synth.StackConfig(hidden=1024, ffn=4096, layers=2,
                                rope_factors=synth.VOXCPM2_SHORT_FACTORS)
     run = Run(vx, oracle, cuda, config, 43, capacity=64)
     rng = synth.Rng(44, 1)
-    for patches in (3, 1):
+    for patches in (3, 4, 1):
         rows = 5 * patches
+        expected = _lib.STACK_PATH_ROWS if rows <= 8 else _lib.STACK_PATH_FUSED
+        assert run.gpu.path(rows) == expected
         h0 = rng.normal(rows * config.hidden).astype(np.float32).reshape(rows, config.hidden)
         run.step(h0, np.arange(rows) % 5, np.arange(rows), 5, 5, 0, False,
                  f"encoder {patches} patches")
@@ -195,3 +203,30 @@ def test_stack_argument_errors(vx, cuda, stream):
     with pytest.raises(_lib.VxError) as info:  # two sequences 10 keys apart
         stack.forward(hidden, out, rows, rows, 2, 10, 5, False, k, v)
     assert info.value.status == _lib.VX_BAD_ARG
+
+
+def test_stack_decode_replays(vx, oracle, cuda, stream):
+    """Decode steps through the same buffers replay one captured graph
+    whose attention reads each call's past from the device: every step
+    matches the oracle, across chunk boundaries (63 -> 64 -> 65 keys), and a
+    per-kernel call and a fragment-order call in between (other paths, the
+    graph dropped and captured again) change nothing."""
+    config = STACKS["gqa-hd64"]
+    run = Run(vx, oracle, cuda, config, 51, capacity=200)
+    rng = synth.Rng(52, 1)
+    hidden = torch.empty((1, config.hidden), dtype=torch.float32, device=cuda)
+    output = torch.empty_like(hidden)
+    position = torch.empty(1, dtype=torch.int32, device=cuda)
+    for past in (61, 62, 63, 64, 65, 129, 130):
+        h = rng.normal(config.hidden).astype(np.float32).reshape(1, config.hidden)
+        hidden.copy_(torch.from_numpy(h))
+        position.fill_(past)
+        run.gpu.set_path(_lib.STACK_PATH_UNFUSED if past == 64 else
+                         _lib.STACK_PATH_FUSED if past == 129 else _lib.STACK_PATH_AUTO)
+        run.gpu.forward(hidden, output, position, position, 1, 1, past, True, run.k_gpu,
+                        run.v_gpu)
+        torch.cuda.synchronize()
+        at = np.array([past], np.int32)
+        ref_h, ref_out = run.cpu.forward(h, at, at, 1, 1, past, True, run.k_cpu, run.v_cpu)
+        check_close(output.cpu().numpy(), ref_out, f"replay past {past} output")
+        check_close(hidden.cpu().numpy(), ref_h, f"replay past {past} hidden")

@@ -67,6 +67,7 @@ VX_WEIGHTS_BF16 = 1
 STACK_PATH_AUTO = 0
 STACK_PATH_FUSED = 2
 STACK_PATH_UNFUSED = 3
+STACK_PATH_ROWS = 4
 
 
 class StackShape(ctypes.Structure):

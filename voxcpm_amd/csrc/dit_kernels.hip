@@ -5,6 +5,7 @@
 // launcher; reductions use 64-lane waves.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cmath>
 #include <cstdint>
 
@@ -43,29 +44,36 @@ __global__ void RmsNormKernel(const float* input, const Bf16* weight,
   }
 }
 
+/// One workgroup per (row, head of q | k | v), one thread per rotated pair
+/// (i, i + head_dim / 2): every load of a pair is issued at once. q and k
+/// heads rotate (when a table is given) into q and the key cache; v heads
+/// copy into the value cache.
 __global__ void QkvRopeKernel(const float* qkv, const float* cos_sin,
                               const std::int32_t* positions,
                               const std::int32_t* cache_rows, float* q,
                               float* k_cache, float* v_cache, int heads,
                               int kv_heads, int head_dim, int capacity) {
   const std::size_t row = blockIdx.x;
+  const int head = static_cast<int>(blockIdx.y);
   const int half = head_dim / 2;
   const int width = (heads + 2 * kv_heads) * head_dim;
-  const float* source = qkv + row * width;
-  const float* table =
-      cos_sin == nullptr
-          ? nullptr
-          : cos_sin + static_cast<std::size_t>(positions[row]) * head_dim;
+  const float* source = qkv + row * width + static_cast<std::size_t>(head) * head_dim;
   const std::size_t cache_row = static_cast<std::size_t>(cache_rows[row]);
-  const int pairs = (heads + kv_heads) * half;
-  for (int index = threadIdx.x; index < pairs; index += blockDim.x) {
-    const int head = index / half;
-    const int i = index % half;
-    const float a = source[head * head_dim + i];
-    const float b = source[head * head_dim + half + i];
+  for (int i = threadIdx.x; i < half; i += blockDim.x) {
+    const float a = source[i];
+    const float b = source[half + i];
+    if (head >= heads + kv_heads) {  // a value head
+      float* target = v_cache +
+                      (static_cast<std::size_t>(head - heads - kv_heads) * capacity + cache_row) *
+                          head_dim;
+      target[i] = a;
+      target[half + i] = b;
+      continue;
+    }
     float first = a;
     float second = b;
-    if (table != nullptr) {
+    if (cos_sin != nullptr) {
+      const float* table = cos_sin + static_cast<std::size_t>(positions[row]) * head_dim;
       const float c = table[i];
       const float s = table[half + i];
       first = a * c - b * s;
@@ -74,18 +82,10 @@ __global__ void QkvRopeKernel(const float* qkv, const float* cos_sin,
     float* target =
         head < heads
             ? q + (row * heads + head) * head_dim
-            : k_cache + ((static_cast<std::size_t>(head - heads) * capacity) +
-                         cache_row) *
+            : k_cache + ((static_cast<std::size_t>(head - heads) * capacity) + cache_row) *
                             head_dim;
     target[i] = first;
     target[half + i] = second;
-  }
-  const float* v = source + (heads + kv_heads) * head_dim;
-  for (int index = threadIdx.x; index < kv_heads * head_dim;
-       index += blockDim.x) {
-    const int head = index / head_dim;
-    v_cache[(static_cast<std::size_t>(head) * capacity + cache_row) * head_dim +
-            index % head_dim] = v[index];
   }
 }
 
@@ -269,7 +269,10 @@ void QkvRope(const float* qkv, const float* cos_sin,
              std::size_t capacity, hipStream_t stream) {
   if (rows == 0)
     return;
-  QkvRopeKernel<<<static_cast<unsigned>(rows), kThreads, 0, stream>>>(
+  const unsigned threads = static_cast<unsigned>(
+      std::min<std::size_t>(256, (head_dim / 2 + kWave - 1) / kWave * kWave));
+  QkvRopeKernel<<<dim3(static_cast<unsigned>(rows), static_cast<unsigned>(heads + 2 * kv_heads)),
+                  threads, 0, stream>>>(
       qkv, cos_sin, positions, cache_rows, q, k_cache, v_cache,
       static_cast<int>(heads), static_cast<int>(kv_heads),
       static_cast<int>(head_dim), static_cast<int>(capacity));

@@ -20,14 +20,17 @@
 //    on the fly (kernels/generator_kernels.hip:91-108): each wave loads its
 //    pairs' values, the per-row sums of squares meet in LDS, and the operand
 //    is bf16((x * rsqrt(mean + eps)) * gamma), exactly the reference's
-//    normalised bf16 activations.
+//    normalised bf16 activations;
+//  - kNormRows: the same from a row-major float32 residual stream of up to
+//    16 rows (one tile: the stacks' decode steps and encoder patches).
 //
 // and leave through one of three epilogues:
 //  - kStore: float32 [m][n] row-major (optionally accumulated) or bf16;
 //  - kResidual: added into the float32 fragment-order residual stream;
 //  - kSwiGlu: RG = 2 with the up rows `group_stride` row groups after the
 //    gate rows; bf16(silu(gate) * up) in bf16 fragment order
-//    (kernels/generator_kernels.hip:243-254).
+//    (kernels/generator_kernels.hip:243-254);
+//  - kSwiGluRows: the same into bf16 [m][n / 2] row-major (y_bf16).
 #ifndef VOXCPM_AMD_Q8_TILE_HPP_
 #define VOXCPM_AMD_Q8_TILE_HPP_
 
@@ -86,8 +89,8 @@ inline std::size_t FragElements(std::size_t columns) {
   return static_cast<std::size_t>(kFragRows) * ((columns + 63) / 64) * 64;
 }
 
-enum class ASource : int { kRowMajor = 0, kFragBf16 = 1, kNormF32 = 2 };
-enum class Output : int { kStore = 0, kResidual = 1, kSwiGlu = 2 };
+enum class ASource : int { kRowMajor = 0, kFragBf16 = 1, kNormF32 = 2, kNormRows = 3 };
+enum class Output : int { kStore = 0, kResidual = 1, kSwiGlu = 2, kSwiGluRows = 3 };
 
 struct TileArgs {
   const std::uint8_t* w;  // panels [groups][pairs] units
@@ -112,12 +115,14 @@ struct TileArgs {
   int tile_blocks;
   // activations
   const Bf16* x;          // kRowMajor [m][k] / kFragBf16
-  const float* h;         // kNormF32: float32 fragment order [32][k]
-  const Bf16* gamma;      // kNormF32: [k]
-  float eps;              // kNormF32
+  const float* h;         // kNormF32: float32 fragment order [32][k];
+                          // kNormRows: float32 [m][k] row-major
+  const Bf16* gamma;      // kNormF32, kNormRows: [k]
+  float eps;              // kNormF32, kNormRows
   // outputs
   float* y;               // kStore float32 [m][n]
-  Bf16* y_bf16;           // kStore bf16 [m][n] (used when y is null)
+  Bf16* y_bf16;           // kStore bf16 [m][n] (used when y is null);
+                          // kSwiGluRows bf16 [m][n / 2]
   int accumulate;         // kStore float32: y += product
   float* residual;        // kResidual: float32 fragment order [32][n]
   Bf16* frag_out;         // kSwiGlu: bf16 fragment order [32][n / 2]
@@ -147,6 +152,22 @@ __host__ __device__ constexpr bool StagesRows(ASource source, int mt) {
 /// columns of bf16 (the pairs of a pass are staged one after another).
 __host__ __device__ constexpr int StageFloats(int mt) {
   return mt * 16 * 32;
+}
+
+/// Floats of the normalised bf16 rows [m][k + 8] of the kNormRows source
+/// (a multiple of 4: the sums behind them stay 16-byte aligned).
+__host__ __device__ constexpr std::size_t NormRowsFloats(int m, int k) {
+  return ((static_cast<std::size_t>(m) * (k + 8) + 7) / 8) * 4;
+}
+
+/// LDS bytes of the kNormRows source for m rows of k (k a multiple of 64,
+/// at most 8 times the threads): the normalised rows and the row sums,
+/// later the waves' partial sums over the same bytes.
+__host__ __device__ constexpr std::size_t NormRowsShared(int mt, int rg, int m, int k) {
+  const int threads = EngineThreads(mt, rg);
+  const std::size_t rows = NormRowsFloats(m, k) + threads + 16;
+  const std::size_t reduce = static_cast<std::size_t>(threads / 64) * rg * mt * 256;
+  return (rows > reduce ? rows : reduce) * sizeof(float);
 }
 
 /// LDS bytes the engine needs for `waves` waves. The row-staging regions
@@ -245,10 +266,13 @@ template<int MT, int RG, ASource SRC, Output OUT, int PW = 1, int JR = 2 * MT,
 __device__ __forceinline__ void EngineBody(const TileArgs& a) {
   // One 16-row tile of a fragment-order source per workgroup.
   constexpr bool kOneTile = MT == 1 && SRC == ASource::kFragBf16;
+  constexpr bool kNorm = SRC == ASource::kNormF32 || SRC == ASource::kNormRows;
+  constexpr bool kSwish = OUT == Output::kSwiGlu || OUT == Output::kSwiGluRows;
   static_assert(SRC != ASource::kNormF32 || MT == 2, "norm source is 32 rows");
-  static_assert(OUT == Output::kStore || MT == 2 || kOneTile,
+  static_assert(SRC != ASource::kNormRows || MT == 1, "row-major norm source is one tile");
+  static_assert(OUT == Output::kStore || OUT == Output::kSwiGluRows || MT == 2 || kOneTile,
                 "fragment outputs are 32 rows or one tile of them");
-  static_assert(OUT != Output::kSwiGlu || RG == 2, "SwiGLU pairs two groups");
+  static_assert(!kSwish || RG == 2, "SwiGLU pairs two groups");
   extern __shared__ float lds[];
   const int lane = threadIdx.x % kWave;
   const int wave = threadIdx.x / kWave;
@@ -288,13 +312,16 @@ __device__ __forceinline__ void EngineBody(const TileArgs& a) {
   for (int t = 0; t < MT; ++t)
     row_ok[t] = in_rows(16 * (tile_base + t) + r16);
   // The activations as buffers: row-major [m][k] bf16, fragment-order bf16
-  // (32 rows x pairs x 64 columns) or fragment-order float32.
+  // (32 rows x pairs x 64 columns), fragment-order float32 or row-major
+  // float32 [m][k].
   const __amdgpu_buffer_rsrc_t x_buffer = BufferOf(
       a.x, SRC == ASource::kRowMajor
                ? 2U * static_cast<std::uint32_t>(a.m) * static_cast<std::uint32_t>(a.k)
                : 4096U * static_cast<std::uint32_t>(a.pairs));
-  const __amdgpu_buffer_rsrc_t h_buffer =
-      BufferOf(a.h, 8192U * static_cast<std::uint32_t>(a.pairs));
+  const __amdgpu_buffer_rsrc_t h_buffer = BufferOf(
+      a.h, SRC == ASource::kNormRows
+               ? 4U * static_cast<std::uint32_t>(a.m) * static_cast<std::uint32_t>(a.k)
+               : 8192U * static_cast<std::uint32_t>(a.pairs));
 
   // Output element e of the tile (thread e, e + threads, ...): fragment
   // f = r MT + t, accumulator i, lane l -> (row, column); false past m / n.
@@ -464,11 +491,81 @@ __device__ __forceinline__ void EngineBody(const TileArgs& a) {
   };
 
   float* reduce = lds;
-  if constexpr (SRC == ASource::kNormF32) {
+  if constexpr (SRC == ASource::kNormRows) {
+    // The workgroup's m rows, RMS-normalised once into LDS as bf16 (rows
+    // k + 8 values apart, which spreads their banks), are every wave's
+    // operands: only the weights are held in registers, so two workgroups
+    // fit a compute unit. Threads take 8 consecutive values of a row, the
+    // rows of a pass side by side; each row's sum of squares is added by
+    // one wave in a fixed order.
+    const int stride = a.k + 8;
+    Bf16* xs = reinterpret_cast<Bf16*>(lds);
+    float* sums = lds + NormRowsFloats(a.m, a.k);  // [threads] partials, [16] inverses
+    PairStage<MT, RG> stage[PW];
+#pragma unroll
+    for (int p = 0; p < PW; ++p)
+      load_weights(wave + p * waves, stage[p]);
+    __builtin_amdgcn_sched_barrier(0);
+    const int t = static_cast<int>(threadIdx.x);
+    const int per_row = a.k / 8;
+    // A wave adds each row's sums: at most one row per wave per pass.
+    const int rows_per_pass = min(kThreads / per_row, waves);
+    const int c = t % per_row;
+    const uint4 g = *reinterpret_cast<const uint4*>(a.gamma + 8 * c);
+    const float gamma[8] = {Bf16Lo(g.x), Bf16Hi(g.x), Bf16Lo(g.y), Bf16Hi(g.y),
+                            Bf16Lo(g.z), Bf16Hi(g.z), Bf16Lo(g.w), Bf16Hi(g.w)};
+    for (int first = 0; first < a.m; first += rows_per_pass) {
+      const int r = first + t / per_row;
+      const bool live = t < rows_per_pass * per_row && r < a.m;
+      const std::uint32_t at = 4U * static_cast<std::uint32_t>(r * a.k + 8 * c);
+      const float4 lo = __builtin_bit_cast(float4, BufferLoad16(h_buffer, at, live));
+      const float4 hi = __builtin_bit_cast(float4, BufferLoad16(h_buffer, at + 16U, live));
+      const float x[8] = {lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
+      float square = 0.0F;
+#pragma unroll
+      for (int i = 0; i < 8; ++i)
+        square += x[i] * x[i];
+      sums[t] = square;
+      __syncthreads();
+      if (wave < rows_per_pass && first + wave < a.m) {
+        float total = 0.0F;
+        for (int j = lane; j < per_row; j += kWave)
+          total += sums[wave * per_row + j];
+        total = AddXor32(AddXor16(RowSum16(total)));
+        if (lane == 0)
+          sums[kThreads + wave] = rsqrtf(total / static_cast<float>(a.k) + a.eps);
+      }
+      __syncthreads();
+      if (live) {
+        const float inverse = sums[kThreads + t / per_row];
+        float v[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i)
+          v[i] = x[i] * inverse * gamma[i];
+        *reinterpret_cast<uint4*>(xs + r * stride + 8 * c) = PackBf16x8(v);
+      }
+      __syncthreads();
+    }
+#pragma unroll
+    for (int p = 0; p < PW; ++p) {
+      const int pair = wave + p * waves;
+#pragma unroll
+      for (int hf = 0; hf < 2; ++hf)
+        stage[p].a[0][hf] =
+            row_ok[0] ? *reinterpret_cast<const uint4*>(xs + r16 * stride +
+                                                         64 * (pair < a.pairs ? pair : 0) +
+                                                         32 * hf + 8 * octet)
+                      : uint4{0U, 0U, 0U, 0U};
+      if (pair < a.pairs)
+        multiply(stage[p]);
+    }
+    // The partial sums below reuse the rows' bytes.
+    __syncthreads();
+  } else if constexpr (kNorm) {
     // Every pair in this pass: wave w owns pairs w, w + waves, ...
     float* squares = lds + static_cast<std::size_t>(waves) * RG * MT * 256;
     PairStage<MT, RG> stage[PW];
-    float4 hv[PW][2][2][2];  // [pair][t][half][quarter]
+    float4 hv[PW][MT][2][2];  // [pair][t][half][quarter]
     uint4 gamma_bits[PW][2];  // [pair][half]: 8 bf16 norm weights
 #pragma unroll
     for (int p = 0; p < PW; ++p)
@@ -490,7 +587,7 @@ __device__ __forceinline__ void EngineBody(const TileArgs& a) {
       const int pair = wave + p * waves;
       const bool ok = pair < a.pairs;
 #pragma unroll
-      for (int t = 0; t < 2; ++t)
+      for (int t = 0; t < MT; ++t)
 #pragma unroll
         for (int hf = 0; hf < 2; ++hf)
 #pragma unroll
@@ -501,8 +598,11 @@ __device__ __forceinline__ void EngineBody(const TileArgs& a) {
                                                (((pair * 2 + t) * 2 + hf) * 2 + q) * 64 + lane),
                                      ok && row_ok[t]));
           }
+    }
 #pragma unroll
-      for (int t = 0; t < 2; ++t)
+    for (int p = 0; p < PW; ++p) {
+#pragma unroll
+      for (int t = 0; t < MT; ++t)
 #pragma unroll
         for (int hf = 0; hf < 2; ++hf)
 #pragma unroll
@@ -514,7 +614,7 @@ __device__ __forceinline__ void EngineBody(const TileArgs& a) {
     // The four octets of a row meet across lanes (permlane swaps, no LDS
     // round trip); waves meet in LDS.
 #pragma unroll
-    for (int t = 0; t < 2; ++t)
+    for (int t = 0; t < MT; ++t)
       partial[t] = AddXor32(AddXor16(partial[t]));
     if (octet == 0) {
       squares[wave * kSquaresStride + r16] = partial[0];
@@ -544,7 +644,7 @@ __device__ __forceinline__ void EngineBody(const TileArgs& a) {
         const float gamma[8] = {Bf16Lo(g.x), Bf16Hi(g.x), Bf16Lo(g.y), Bf16Hi(g.y),
                                 Bf16Lo(g.z), Bf16Hi(g.z), Bf16Lo(g.w), Bf16Hi(g.w)};
 #pragma unroll
-        for (int t = 0; t < 2; ++t) {
+        for (int t = 0; t < MT; ++t) {
           const float4 lo = hv[p][t][hf][0];
           const float4 hi = hv[p][t][hf][1];
           const float x[8] = {lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
@@ -637,7 +737,7 @@ __device__ __forceinline__ void EngineBody(const TileArgs& a) {
       total += parts[w];
     return total;
   };
-  const int outputs = OUT == Output::kSwiGlu ? MT * 256 : kFragmentFloats;
+  const int outputs = kSwish ? MT * 256 : kFragmentFloats;
 #pragma unroll
   for (int u = 0; u < kOutputsPerThread; ++u) {
     const int e = static_cast<int>(threadIdx.x) + u * kThreads;
@@ -653,9 +753,12 @@ __device__ __forceinline__ void EngineBody(const TileArgs& a) {
         a.y_bf16[at] = Bf16Fast(v);
     } else if constexpr (OUT == Output::kResidual) {
       a.residual[F32FragIndex(row, column)] = before[u] + v;
-    } else {
+    } else if constexpr (OUT == Output::kSwiGlu) {
       const float up = total_of(e + MT * 256);
       a.frag_out[BfFragIndex(row, column)] = Bf16Fast(Silu(v) * up);
+    } else {
+      const float up = total_of(e + MT * 256);
+      a.y_bf16[static_cast<std::size_t>(row) * (a.n / 2) + column] = Bf16Fast(Silu(v) * up);
     }
   }
 }
@@ -665,6 +768,7 @@ template<int MT, int RG, ASource SRC, Output OUT, int PW = 1, int JR = 2 * MT,
 __global__ __launch_bounds__(EngineThreads(MT, RG)) void EngineKernel(TileArgs a) {
   EngineBody<MT, RG, SRC, OUT, PW, JR, WK>(a);
 }
+
 
 }  // namespace vx::q8
 

@@ -33,7 +33,7 @@ namespace {
 constexpr int kChunk = 64;     // keys per workgroup of the split attention
 constexpr int kThreads = 256;  // four waves, 16 keys each when scoring
 constexpr int kWaves = kThreads / kWave;
-constexpr int kMaxGroup = 16;  // query heads per KV head
+constexpr int kMaxNormRows = 8;  // rows of the one-tile row-major path
 
 struct AttentionArgs {
   const float* q;        // [rows][heads][D], rotated, unscaled
@@ -51,6 +51,9 @@ struct AttentionArgs {
   int splits;
   float scale;
   int fragment;  // bf16 fragment order (rows <= 32) instead of row-major
+  // When non-null, `past` is read here instead (a captured graph replays
+  // with the value of each call; the grid then covers the cache).
+  const int* past_device;
 };
 
 __device__ inline std::size_t OutIndex(const AttentionArgs& a, int row, int column, int width) {
@@ -65,96 +68,136 @@ constexpr std::size_t SharedFloats(int group, int d) {
          2 * group + static_cast<std::size_t>(kWaves) * group * d;
 }
 
+/// Maximum over the wave: rows of 16 by DPP, then the rows by permlane
+/// swaps (every lane receives it).
+__device__ inline float WaveMax64(float x) {
+  x = RowMax16(x);
+  auto swapped = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false,
+                                                  false);
+  x = fmaxf(__uint_as_float(swapped[0]), __uint_as_float(swapped[1]));
+  swapped = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(swapped[0]), __uint_as_float(swapped[1]));
+}
+
+/// Sum over the wave in a fixed order (every lane receives the same bits).
+__device__ inline float WaveSum64(float x) { return AddXor32(AddXor16(RowSum16(x))); }
+
+/// Keys of a row: past + its position in the sequence (causal) or the
+/// whole sequence.
+__device__ inline int KeyCount(const AttentionArgs& a, int row) {
+  const int past = a.past_device != nullptr ? *a.past_device : a.past;
+  return past + (a.causal != 0 ? row % a.rows_per_sequence + 1 : a.rows_per_sequence);
+}
+
 /// One chunk of keys of one (row, KV head) for the KV head's `group` query
-/// heads (kernels/generator_kernels.hip:160-241 in the chunk): scores
-/// q . k scale with lanes over (key, quarter of the dimensions) and the
-/// quarters met by permlane swaps; the chunk's maximum and sum per head;
-/// the values weighted by exp(score - max) with lanes over dimensions and
-/// the four waves' sums added in wave order. One chunk writes the output
-/// itself; several leave (max, sum, values) for MergeKernel.
-template<int D>
+/// heads (kernels/generator_kernels.hip:160-241 in the chunk). Every load
+/// is issued at the start -- the chunk's keys (lanes over key and quarter
+/// of the dimensions), each wave's 16 value rows (lanes over dimensions)
+/// and the queries -- so that one memory round trip serves the chunk.
+/// Scores q . k scale meet over the quarters by permlane swaps; the
+/// chunk's maximum and sum per head; the values weighted by exp(score -
+/// max), the four waves' sums added in wave order. One chunk writes the
+/// output itself; several leave (max, sum, values) for MergeKernel.
+/// Chunks past a row's keys do nothing (the merge reads the row's chunks
+/// only).
+template<int D, int G>
 __global__ __launch_bounds__(kThreads) void SplitAttentionKernel(AttentionArgs a) {
   constexpr int kQuarter = D / 4;
   constexpr int kPerLane = D / kWave;
   extern __shared__ float lds[];
-  const int group = a.heads / a.kv_heads;
-  float* qs = lds;                                  // [group][D]
-  float* ps = qs + group * D;                       // [group][kChunk]
-  float* stats = ps + group * kChunk;               // [group][2]
-  float* parts = stats + 2 * group;                 // [waves][group][D]
+  float* qs = lds;                 // [G][D]
+  float* ps = qs + G * D;          // [G][kChunk]
+  float* stats = ps + G * kChunk;  // [G][2]
+  float* parts = stats + 2 * G;    // [waves][G][D]
   const int split = static_cast<int>(blockIdx.x);
   const int row = static_cast<int>(blockIdx.y);
   const int g = static_cast<int>(blockIdx.z);
   const int lane = static_cast<int>(threadIdx.x) % kWave;
   const int wave = static_cast<int>(threadIdx.x) / kWave;
-  const int sequence = row / a.rows_per_sequence;
-  const int local = row % a.rows_per_sequence;
-  const int count = a.past + (a.causal != 0 ? local + 1 : a.rows_per_sequence);
-  const int first = sequence * a.keys_per_sequence;
+  const int first = (row / a.rows_per_sequence) * a.keys_per_sequence;
   const int key0 = split * kChunk;
-  const int key1 = min(count, key0 + kChunk);
-  const std::size_t stride = static_cast<std::size_t>(D) + 2;
-  const std::size_t partial0 =
-      (static_cast<std::size_t>(row) * a.heads + g * group) * a.splits + split;
+  // Keys and values are loaded before past is known (a chunk's first key
+  // lies in the cache for every past the grid covers); keys past the cache
+  // re-read the chunk's first.
+  const int limit = a.capacity - first;
+  const std::size_t base = static_cast<std::size_t>(g) * a.capacity + first;
 
-  if (key0 >= key1) {  // past this row's keys: an empty chunk
-    for (int e = static_cast<int>(threadIdx.x); e < group * static_cast<int>(stride);
-         e += kThreads) {
-      const int hh = e / static_cast<int>(stride);
-      const int i = e % static_cast<int>(stride);
-      a.partials[(partial0 + static_cast<std::size_t>(hh) * a.splits) * stride + i] =
-          i == 0 ? -INFINITY : 0.0F;
-    }
-    return;
+  // Keys: lane (key 16 wave + lane % 16, quarter lane / 16).
+  const int key_local = 16 * wave + lane % 16;
+  const int quarter = lane / 16;
+  float4 kv[kQuarter / 4];
+  {
+    const int key = key0 + key_local;
+    const float4* krow = reinterpret_cast<const float4*>(
+        a.k + (base + (key < limit ? key : key0)) * D + quarter * kQuarter);
+#pragma unroll
+    for (int i = 0; i < kQuarter / 4; ++i)
+      kv[i] = krow[i];
   }
-
-  for (int e = static_cast<int>(threadIdx.x); e < group * D; e += kThreads) {
-    const int hh = e / D;
-    qs[e] = a.q[(static_cast<std::size_t>(row) * a.heads + g * group + hh) * D + e % D] *
-            a.scale;
+  // Values: wave w's keys 16 w .. 16 w + 15, lanes over dimensions.
+  float vv[16][kPerLane];
+#pragma unroll
+  for (int kk = 0; kk < 16; ++kk) {
+    const int key = key0 + 16 * wave + kk;
+    const float* vrow = a.v + (base + (key < limit ? key : key0)) * D + lane * kPerLane;
+#pragma unroll
+    for (int j = 0; j < kPerLane; ++j)
+      vv[kk][j] = vrow[j];
+  }
+  // The group's queries, four floats per thread per step.
+  constexpr int kQueryLoads = (G * D / 4 + kThreads - 1) / kThreads;
+  float4 qv4[kQueryLoads];
+  const float4* qsrc = reinterpret_cast<const float4*>(
+      a.q + (static_cast<std::size_t>(row) * a.heads + g * G) * D);
+#pragma unroll
+  for (int i = 0; i < kQueryLoads; ++i) {
+    const int e4 = static_cast<int>(threadIdx.x) + i * kThreads;
+    if (e4 < G * D / 4)
+      qv4[i] = qsrc[e4];
+  }
+  const int count = KeyCount(a, row);
+  const int key1 = min(count, key0 + kChunk);
+  if (key0 >= key1)
+    return;  // past this row's keys: the merge reads the row's chunks only
+  const bool valid = key0 + key_local < key1;
+  // Rows past the row's keys may hold anything (the cache beyond what was
+  // written): their values are dropped, not weighted by 0.
+#pragma unroll
+  for (int kk = 0; kk < 16; ++kk)
+#pragma unroll
+    for (int j = 0; j < kPerLane; ++j)
+      vv[kk][j] = key0 + 16 * wave + kk < key1 ? vv[kk][j] : 0.0F;
+#pragma unroll
+  for (int i = 0; i < kQueryLoads; ++i) {
+    const int e4 = static_cast<int>(threadIdx.x) + i * kThreads;
+    if (e4 < G * D / 4) {
+      const float4 v = qv4[i];
+      reinterpret_cast<float4*>(qs)[e4] =
+          make_float4(v.x * a.scale, v.y * a.scale, v.z * a.scale, v.w * a.scale);
+    }
   }
   __syncthreads();
 
-  // Scores: lane (key 16 wave + lane % 16, quarter lane / 16).
-  {
-    const int key_local = 16 * wave + lane % 16;
-    const int quarter = lane / 16;
-    const int key = key0 + key_local;
-    const bool valid = key < key1;
-    const float4* krow = reinterpret_cast<const float4*>(
-        a.k + (static_cast<std::size_t>(g) * a.capacity + first + (valid ? key : key0)) * D +
-        quarter * kQuarter);
-    float kv[kQuarter];
+  for (int hh = 0; hh < G; ++hh) {
+    const float4* qrow = reinterpret_cast<const float4*>(qs + hh * D + quarter * kQuarter);
+    float s = 0.0F;
 #pragma unroll
     for (int i = 0; i < kQuarter / 4; ++i) {
-      const float4 f = krow[i];
-      kv[4 * i] = f.x;
-      kv[4 * i + 1] = f.y;
-      kv[4 * i + 2] = f.z;
-      kv[4 * i + 3] = f.w;
+      const float4 q = qrow[i];
+      s += q.x * kv[i].x + q.y * kv[i].y + q.z * kv[i].z + q.w * kv[i].w;
     }
-    for (int hh = 0; hh < group; ++hh) {
-      const float4* qrow = reinterpret_cast<const float4*>(qs + hh * D + quarter * kQuarter);
-      float s = 0.0F;
-#pragma unroll
-      for (int i = 0; i < kQuarter / 4; ++i) {
-        const float4 qv = qrow[i];
-        s += qv.x * kv[4 * i] + qv.y * kv[4 * i + 1] + qv.z * kv[4 * i + 2] +
-             qv.w * kv[4 * i + 3];
-      }
-      s = AddXor32(AddXor16(s));
-      if (quarter == 0)
-        ps[hh * kChunk + key_local] = valid ? s : -INFINITY;
-    }
+    s = AddXor32(AddXor16(s));
+    if (quarter == 0)
+      ps[hh * kChunk + key_local] = valid ? s : -INFINITY;
   }
   __syncthreads();
 
   // The chunk's softmax statistics per head (wave w: heads w, w + 4, ...).
-  for (int hh = wave; hh < group; hh += kWaves) {
+  for (int hh = wave; hh < G; hh += kWaves) {
     const float s = ps[hh * kChunk + lane];
-    const float m = WaveMax(s);
+    const float m = WaveMax64(s);
     const float p = s == -INFINITY ? 0.0F : expf(s - m);
-    const float l = WaveSum(p);
+    const float l = WaveSum64(p);
     ps[hh * kChunk + lane] = p;
     if (lane == 0) {
       stats[2 * hh] = m;
@@ -163,57 +206,44 @@ __global__ __launch_bounds__(kThreads) void SplitAttentionKernel(AttentionArgs a
   }
   __syncthreads();
 
-  // Values: wave w adds keys 16 w .. 16 w + 15 of the chunk, lanes over
-  // dimensions.
-  float o[kMaxGroup][kPerLane];
+  // Each head's weighted values over the wave's 16 keys into LDS.
+  for (int hh = 0; hh < G; ++hh) {
+    const float4* prow = reinterpret_cast<const float4*>(ps + hh * kChunk + 16 * wave);
+    float p[16];
 #pragma unroll
-  for (int hh = 0; hh < kMaxGroup; ++hh)
-#pragma unroll
-    for (int j = 0; j < kPerLane; ++j)
-      o[hh][j] = 0.0F;
-  for (int kk = 0; kk < 16; ++kk) {
-    const int key_local = 16 * wave + kk;
-    const int key = key0 + key_local;
-    if (key >= key1)
-      break;
-    const float* vrow =
-        a.v + (static_cast<std::size_t>(g) * a.capacity + first + key) * D + lane * kPerLane;
-    float vv[kPerLane];
-#pragma unroll
-    for (int j = 0; j < kPerLane; ++j)
-      vv[j] = vrow[j];
-#pragma unroll
-    for (int hh = 0; hh < kMaxGroup; ++hh) {
-      if (hh >= group)
-        break;
-      const float p = ps[hh * kChunk + key_local];
-#pragma unroll
-      for (int j = 0; j < kPerLane; ++j)
-        o[hh][j] += p * vv[j];
+    for (int i = 0; i < 4; ++i) {
+      const float4 f = prow[i];
+      p[4 * i] = f.x;
+      p[4 * i + 1] = f.y;
+      p[4 * i + 2] = f.z;
+      p[4 * i + 3] = f.w;
     }
-  }
 #pragma unroll
-  for (int hh = 0; hh < kMaxGroup; ++hh) {
-    if (hh >= group)
-      break;
+    for (int j = 0; j < kPerLane; ++j) {
+      float o = 0.0F;
 #pragma unroll
-    for (int j = 0; j < kPerLane; ++j)
-      parts[(wave * group + hh) * D + lane * kPerLane + j] = o[hh][j];
+      for (int kk = 0; kk < 16; ++kk)
+        o += p[kk] * vv[kk][j];
+      parts[(wave * G + hh) * D + lane * kPerLane + j] = o;
+    }
   }
   __syncthreads();
   const int width = a.heads * D;
-  for (int e = static_cast<int>(threadIdx.x); e < group * D; e += kThreads) {
+  const std::size_t stride = static_cast<std::size_t>(D) + 2;
+  for (int e = static_cast<int>(threadIdx.x); e < G * D; e += kThreads) {
     float total = parts[e];
 #pragma unroll
     for (int w = 1; w < kWaves; ++w)
-      total += parts[w * group * D + e];
+      total += parts[w * G * D + e];
     const int hh = e / D;
     const int d = e % D;
     if (a.splits == 1) {
-      a.out[OutIndex(a, row, (g * group + hh) * D + d, width)] =
+      a.out[OutIndex(a, row, (g * G + hh) * D + d, width)] =
           Bf16Bits(total * (1.0F / stats[2 * hh + 1]));
     } else {
-      float* target = a.partials + (partial0 + static_cast<std::size_t>(hh) * a.splits) * stride;
+      float* target =
+          a.partials +
+          ((static_cast<std::size_t>(row) * a.heads + g * G + hh) * a.splits + split) * stride;
       target[2 + d] = total;
       if (d == 0) {
         target[0] = stats[2 * hh];
@@ -224,34 +254,61 @@ __global__ __launch_bounds__(kThreads) void SplitAttentionKernel(AttentionArgs a
 }
 
 /// The chunks of one (row, head) met in chunk order: M = max m_c,
-/// L = sum l_c exp(m_c - M), out = bf16(sum o_c exp(m_c - M) / L).
+/// L = sum l_c exp(m_c - M), out = bf16(sum o_c exp(m_c - M) / L), over the
+/// row's chunks only. Lane c takes chunk c's statistics (chunks 64 apart in
+/// turn); the values are loaded eight chunks at a time.
 template<int D>
 __global__ __launch_bounds__(kWave) void MergeKernel(AttentionArgs a) {
   constexpr int kPerLane = D / kWave;
+  constexpr int kBatch = 8;
   const int row = static_cast<int>(blockIdx.x);
   const int head = static_cast<int>(blockIdx.y);
   const int lane = static_cast<int>(threadIdx.x);
+  const int chunks = (KeyCount(a, row) + kChunk - 1) / kChunk;
   const std::size_t stride = static_cast<std::size_t>(D) + 2;
   const float* base =
       a.partials + (static_cast<std::size_t>(row) * a.heads + head) * a.splits * stride;
   float m = -INFINITY;
-  for (int c = 0; c < a.splits; ++c)
+  for (int c = lane; c < chunks; c += kWave)
     m = fmaxf(m, base[c * stride]);
-  float l = 0.0F;
+  m = WaveMax64(m);
   float o[kPerLane];
 #pragma unroll
   for (int j = 0; j < kPerLane; ++j)
     o[j] = 0.0F;
-  for (int c = 0; c < a.splits; ++c) {
-    const float* part = base + c * stride;
-    if (part[1] == 0.0F)
-      continue;  // an empty chunk
-    const float factor = expf(part[0] - m);
-    l += part[1] * factor;
+  float l = 0.0F;
+  for (int c0 = 0; c0 < chunks; c0 += kWave) {
+    const int c = c0 + lane;
+    float factor = 0.0F;
+    if (c < chunks) {
+      const float* part = base + c * stride;
+      factor = expf(part[0] - m);
+      l += part[1] * factor;
+    }
+    const int count = min(kWave, chunks - c0);
+    for (int i0 = 0; i0 < count; i0 += kBatch) {
+      float values[kBatch][kPerLane];
 #pragma unroll
-    for (int j = 0; j < kPerLane; ++j)
-      o[j] += part[2 + lane * kPerLane + j] * factor;
+      for (int b = 0; b < kBatch; ++b) {
+        const float* part =
+            base + (c0 + min(i0 + b, count - 1)) * stride + 2 + lane * kPerLane;
+#pragma unroll
+        for (int j = 0; j < kPerLane; ++j)
+          values[b][j] = part[j];
+      }
+#pragma unroll
+      for (int b = 0; b < kBatch; ++b) {
+        const float f = __shfl(factor, i0 + b, kWave);
+        if (i0 + b < count) {
+#pragma unroll
+          for (int j = 0; j < kPerLane; ++j)
+            o[j] += values[b][j] * f;
+        }
+      }
+    }
   }
+  // Lane c's chunks' sums, then the lanes by a fixed tree.
+  l = WaveSum64(l);
   const float inverse = 1.0F / l;
   const int width = a.heads * D;
 #pragma unroll
@@ -259,13 +316,23 @@ __global__ __launch_bounds__(kWave) void MergeKernel(AttentionArgs a) {
     a.out[OutIndex(a, row, head * D + lane * kPerLane + j, width)] = Bf16Bits(o[j] * inverse);
 }
 
+template<int D, int G>
+void LaunchSplit(const AttentionArgs& a, int rows, hipStream_t stream) {
+  const std::size_t shared = SharedFloats(G, D) * sizeof(float);
+  SplitAttentionKernel<D, G><<<dim3(static_cast<unsigned>(a.splits), static_cast<unsigned>(rows),
+                                    static_cast<unsigned>(a.kv_heads)),
+                               kThreads, shared, stream>>>(a);
+}
+
 template<int D>
 void LaunchAttention(const AttentionArgs& a, int rows, hipStream_t stream) {
-  const int group = a.heads / a.kv_heads;
-  const std::size_t shared = SharedFloats(group, D) * sizeof(float);
-  SplitAttentionKernel<D><<<dim3(static_cast<unsigned>(a.splits), static_cast<unsigned>(rows),
-                                 static_cast<unsigned>(a.kv_heads)),
-                            kThreads, shared, stream>>>(a);
+  switch (a.heads / a.kv_heads) {
+    case 1: LaunchSplit<D, 1>(a, rows, stream); break;
+    case 2: LaunchSplit<D, 2>(a, rows, stream); break;
+    case 4: LaunchSplit<D, 4>(a, rows, stream); break;
+    case 8: LaunchSplit<D, 8>(a, rows, stream); break;
+    default: LaunchSplit<D, 16>(a, rows, stream); break;
+  }
   if (a.splits > 1)
     MergeKernel<D><<<dim3(static_cast<unsigned>(rows), static_cast<unsigned>(a.heads)), kWave, 0,
                      stream>>>(a);
@@ -279,6 +346,13 @@ int AttentionSplits(std::size_t past, std::size_t rows_per_sequence) {
   return static_cast<int>((past + rows_per_sequence + kChunk - 1) / kChunk);
 }
 
+/// Writes `past` for the attention launches of a replayed graph.
+__global__ void SetPastKernel(int* past_device, int past) { *past_device = past; }
+
+void SetPast(int* past_device, std::size_t past, hipStream_t stream) {
+  SetPastKernel<<<1, 1, 0, stream>>>(past_device, static_cast<int>(past));
+}
+
 /// Floats of the chunks' partial results of `rows` rows.
 std::size_t AttentionPartialFloats(std::size_t rows, std::size_t heads, std::size_t head_dim,
                                    int splits) {
@@ -286,10 +360,13 @@ std::size_t AttentionPartialFloats(std::size_t rows, std::size_t heads, std::siz
 }
 
 /// Checks the shape the split attention takes: head_dim 64 or 128 (VoxCPM2's
-/// stacks take 128), at most 16 query heads per KV head, its LDS within
+/// stacks take 128), 1, 2, 4, 8 or 16 query heads per KV head, its LDS within
 /// 64 KB.
 bool AttentionSupported(std::size_t heads, std::size_t kv_heads, std::size_t head_dim) {
-  if (kv_heads == 0 || heads % kv_heads != 0 || heads / kv_heads > kMaxGroup)
+  if (kv_heads == 0 || heads % kv_heads != 0)
+    return false;
+  const std::size_t group = heads / kv_heads;
+  if (group != 1 && group != 2 && group != 4 && group != 8 && group != 16)
     return false;
   if (head_dim != 64 && head_dim != 128)
     return false;
@@ -299,12 +376,13 @@ bool AttentionSupported(std::size_t heads, std::size_t kv_heads, std::size_t hea
 }
 
 /// The split attention over one layer's cache (the caller has checked the
-/// shape, the bounds and the partials' size).
+/// shape, the bounds and the partials' size). `splits` chunks per (row, KV
+/// head); with `past_device` non-null the kernels read past there.
 void Attention(const float* q, const float* k_cache, const float* v_cache, Bf16* out,
                bool fragment, float* partials, std::size_t rows,
                std::size_t rows_per_sequence, std::size_t keys_per_sequence, std::size_t past,
                bool causal, std::size_t heads, std::size_t kv_heads, std::size_t head_dim,
-               std::size_t capacity, hipStream_t stream) {
+               std::size_t capacity, int splits, const int* past_device, hipStream_t stream) {
   AttentionArgs a{};
   a.q = q;
   a.k = k_cache;
@@ -318,9 +396,10 @@ void Attention(const float* q, const float* k_cache, const float* v_cache, Bf16*
   a.heads = static_cast<int>(heads);
   a.kv_heads = static_cast<int>(kv_heads);
   a.capacity = static_cast<int>(capacity);
-  a.splits = AttentionSplits(past, rows_per_sequence);
+  a.splits = splits;
   a.scale = 1.0F / std::sqrt(static_cast<float>(head_dim));
   a.fragment = fragment ? 1 : 0;
+  a.past_device = past_device;
   const int r = static_cast<int>(rows);
   if (head_dim == 64)
     LaunchAttention<64>(a, r, stream);
@@ -347,6 +426,74 @@ __global__ void FromFragmentsKernel(const float* h, float* rows_out, int rows, i
 }
 
 }  // namespace
+
+namespace {
+
+template<q8::ASource SRC, q8::Output OUT, int RG, int PW>
+void LaunchRowEngine(const q8::TileArgs& args, int tiles, q8::Weights kind, hipStream_t stream) {
+  constexpr int kEngineThreads = q8::EngineThreads(1, RG);
+  const std::size_t shared = q8::NormRowsShared(1, RG, args.m, args.k);
+  if (kind == q8::Weights::kQ8)
+    q8::EngineKernel<1, RG, SRC, OUT, PW, 2, q8::Weights::kQ8>
+        <<<tiles, kEngineThreads, shared, stream>>>(args);
+  else
+    q8::EngineKernel<1, RG, SRC, OUT, PW, 2, q8::Weights::kBf16>
+        <<<tiles, kEngineThreads, shared, stream>>>(args);
+}
+
+q8::TileArgs RowArgs(const void* weight, int m, int k, int n) {
+  q8::TileArgs args{};
+  args.w = static_cast<const std::uint8_t*>(weight);
+  args.m = m;
+  args.k = k;
+  args.n = n;
+  args.pairs = static_cast<int>(q8::Pairs(static_cast<std::size_t>(k)));
+  args.groups = (n + 15) / 16;
+  args.group_stride = 1;
+  args.row_blocks = 1;
+  args.rows_per_block = m;
+  args.tile_blocks = 1;
+  return args;
+}
+
+}  // namespace
+
+bool RowsSupported(std::size_t hidden, std::size_t ffn) {
+  return hidden % 64 == 0 && hidden <= 2 * 64 * 16 && ffn % 16 == 0 &&
+         q8::NormRowsShared(1, 2, kMaxNormRows, static_cast<int>(hidden)) <= 65536;
+}
+
+void NormQkvRows(const float* h, const Bf16* gamma, float eps, const void* weight, float* qkv,
+                 int rows, int hidden, int n, q8::Weights kind, hipStream_t stream) {
+  q8::TileArgs args = RowArgs(weight, rows, hidden, n);
+  args.h = h;
+  args.gamma = gamma;
+  args.eps = eps;
+  args.y = qkv;
+  if (args.pairs <= 16)
+    LaunchRowEngine<q8::ASource::kNormRows, q8::Output::kStore, 1, 1>(args, args.groups, kind,
+                                                                       stream);
+  else
+    LaunchRowEngine<q8::ASource::kNormRows, q8::Output::kStore, 1, 2>(args, args.groups, kind,
+                                                                       stream);
+}
+
+void NormGateUpRows(const float* h, const Bf16* gamma, float eps, const void* weight, Bf16* act,
+                    int rows, int hidden, int ffn, q8::Weights kind, hipStream_t stream) {
+  q8::TileArgs args = RowArgs(weight, rows, hidden, 2 * ffn);
+  args.h = h;
+  args.gamma = gamma;
+  args.eps = eps;
+  args.y_bf16 = act;
+  args.group_stride = ffn / 16;
+  const int tiles = ffn / 16;
+  if (args.pairs <= 16)
+    LaunchRowEngine<q8::ASource::kNormRows, q8::Output::kSwiGluRows, 2, 1>(args, tiles, kind,
+                                                                           stream);
+  else
+    LaunchRowEngine<q8::ASource::kNormRows, q8::Output::kSwiGluRows, 2, 2>(args, tiles, kind,
+                                                                           stream);
+}
 
 void ToFragments(const float* rows_in, float* h, int rows, int width, hipStream_t stream) {
   const int count = rows * width;
@@ -382,6 +529,32 @@ int Grow(T** pointer, std::size_t* have, std::size_t need, const char* what) {
 
 }  // namespace
 
+/// What a captured forward depends on besides `past`.
+struct ForwardKey {
+  float* hidden = nullptr;
+  float* output = nullptr;
+  std::size_t rows = 0;
+  const std::int32_t* positions = nullptr;
+  const std::int32_t* cache_rows = nullptr;
+  std::size_t rows_per_sequence = 0;
+  std::size_t keys_per_sequence = 0;
+  bool causal = false;
+  float* k_cache = nullptr;
+  float* v_cache = nullptr;
+  std::size_t capacity = 0;
+  int path = 0;
+  hipStream_t stream = nullptr;
+
+  bool operator==(const ForwardKey& o) const {
+    return hidden == o.hidden && output == o.output && rows == o.rows &&
+           positions == o.positions && cache_rows == o.cache_rows &&
+           rows_per_sequence == o.rows_per_sequence &&
+           keys_per_sequence == o.keys_per_sequence && causal == o.causal &&
+           k_cache == o.k_cache && v_cache == o.v_cache && capacity == o.capacity &&
+           path == o.path && stream == o.stream;
+  }
+};
+
 struct vx_stack {
   vx_stack_shape shape{};
   vx_stack_weights weights{};
@@ -389,7 +562,8 @@ struct vx_stack {
   std::size_t q_width = 0;
   std::size_t kv_width = 0;
   std::size_t qkv_width = 0;
-  bool fused = false;
+  bool fused = false;       // the fragment-order kernels take the shape
+  bool rows_fused = false;  // the one-tile row-major kernels take it
   vx::fused::Shape fs{};
   int path = VX_STACK_PATH_AUTO;
 
@@ -412,7 +586,16 @@ struct vx_stack {
   Bf16* attention_frag = nullptr;
   Bf16* swiglu_frag = nullptr;
 
+  // The replayed forward of up to 32 rows and the past it reads.
+  int* past_device = nullptr;
+  ForwardKey graph_key;
+  hipGraphExec_t graph = nullptr;
+
   ~vx_stack() {
+    if (graph != nullptr)
+      (void)hipGraphExecDestroy(graph);
+    if (past_device != nullptr)
+      (void)hipFree(past_device);
     for (void* pointer :
          {static_cast<void*>(qkv), static_cast<void*>(q), static_cast<void*>(bf16),
           static_cast<void*>(gate_up), static_cast<void*>(attention_partials),
@@ -443,75 +626,165 @@ struct vx_stack {
   }
 
   int Resolved(std::size_t rows) const {
-    if (path == VX_STACK_PATH_UNFUSED || !fused || rows > vx::q8::kFragRows)
-      return VX_STACK_PATH_UNFUSED;
-    return VX_STACK_PATH_FUSED;
+    const bool rows_ok = rows_fused && rows <= vx::stack::kMaxNormRows;
+    const bool fragments_ok = fused && rows <= vx::q8::kFragRows;
+    switch (path) {
+      case VX_STACK_PATH_ROWS: return rows_ok ? VX_STACK_PATH_ROWS : VX_STACK_PATH_UNFUSED;
+      case VX_STACK_PATH_FUSED: return fragments_ok ? VX_STACK_PATH_FUSED : VX_STACK_PATH_UNFUSED;
+      case VX_STACK_PATH_UNFUSED: return VX_STACK_PATH_UNFUSED;
+      default:
+        return rows_ok ? VX_STACK_PATH_ROWS
+                       : fragments_ok ? VX_STACK_PATH_FUSED : VX_STACK_PATH_UNFUSED;
+    }
   }
 
-  int Forward(float* hidden, float* output, std::size_t rows, const std::int32_t* positions,
-              const std::int32_t* cache_rows, std::size_t rows_per_sequence,
-              std::size_t keys_per_sequence, std::size_t past, bool causal, float* k_cache,
-              float* v_cache, std::size_t capacity, hipStream_t stream) {
+  /// The launches of one forward; `splits` chunks per (row, KV head) of the
+  /// attention, past read from `past_device` when it is non-null.
+  int Launch(const ForwardKey& f, std::size_t past, int splits, const int* past_device,
+             hipStream_t stream) {
+    const std::size_t rows = f.rows;
     const std::size_t width = shape.hidden;
     const std::size_t ffn = shape.ffn;
-    const std::size_t layer_stride = shape.kv_heads * capacity * shape.head_dim;
-    const int splits = vx::stack::AttentionSplits(past, rows_per_sequence);
-    VX_TRY(Grow(&attention_partials, &attention_partial_floats,
-                vx::stack::AttentionPartialFloats(rows, shape.heads, shape.head_dim, splits),
-                "vx_stack_forward: hipMalloc"));
-    VX_TRY(Grow(&q, &q_floats, rows * q_width, "vx_stack_forward: hipMalloc"));
-    VX_TRY(Grow(&qkv, &qkv_floats, rows * qkv_width, "vx_stack_forward: hipMalloc"));
+    const std::size_t layer_stride = shape.kv_heads * f.capacity * shape.head_dim;
     const float* rope = shape.rope != 0 ? weights.rope : nullptr;
-
-    if (Resolved(rows) == VX_STACK_PATH_FUSED) {
-      vx::fused::Shape s = fs;
-      s.rows = static_cast<int>(rows);
-      vx::stack::ToFragments(hidden, h_frag, s.rows, s.hidden, stream);
+    if (f.path == VX_STACK_PATH_ROWS) {
+      const int m = static_cast<int>(rows);
       for (std::size_t l = 0; l < layers.size(); ++l) {
         const vx_dit_layer& layer = layers[l];
-        float* keys = k_cache + l * layer_stride;
-        float* values = v_cache + l * layer_stride;
+        float* keys = f.k_cache + l * layer_stride;
+        float* values = f.v_cache + l * layer_stride;
+        vx::stack::NormQkvRows(f.hidden, layer.input_norm, shape.eps, layer.qkv, qkv, m,
+                               static_cast<int>(width), static_cast<int>(qkv_width), Kind(),
+                               stream);
+        vx::kernels::QkvRope(qkv, rope, f.positions, f.cache_rows, q, keys, values, rows,
+                             shape.heads, shape.kv_heads, shape.head_dim, f.capacity, stream);
+        vx::stack::Attention(q, keys, values, bf16, false, attention_partials, rows,
+                             f.rows_per_sequence, f.keys_per_sequence, past, f.causal,
+                             shape.heads, shape.kv_heads, shape.head_dim, f.capacity, splits,
+                             past_device, stream);
+        VX_TRY(Linear(bf16, layer.o, f.hidden, rows, q_width, width, true, stream));
+        vx::stack::NormGateUpRows(f.hidden, layer.post_norm, shape.eps, layer.gate_up, bf16, m,
+                                  static_cast<int>(width), static_cast<int>(ffn), Kind(),
+                                  stream);
+        VX_TRY(Linear(bf16, layer.down, f.hidden, rows, ffn, width, true, stream));
+      }
+      vx::kernels::RmsNorm(f.hidden, weights.norm, bf16, f.output, rows, width, shape.eps,
+                           stream);
+      return vx::LaunchStatus("vx_stack_forward");
+    }
+    if (f.path == VX_STACK_PATH_FUSED) {
+      vx::fused::Shape s = fs;
+      s.rows = static_cast<int>(rows);
+      vx::stack::ToFragments(f.hidden, h_frag, s.rows, s.hidden, stream);
+      for (std::size_t l = 0; l < layers.size(); ++l) {
+        const vx_dit_layer& layer = layers[l];
+        float* keys = f.k_cache + l * layer_stride;
+        float* values = f.v_cache + l * layer_stride;
         vx::fused::Qkv(h_frag, layer.input_norm, layer.qkv, qkv, s, stream);
-        vx::kernels::QkvRope(qkv, rope, positions, cache_rows, q, keys, values, rows,
-                             shape.heads, shape.kv_heads, shape.head_dim, capacity, stream);
+        vx::kernels::QkvRope(qkv, rope, f.positions, f.cache_rows, q, keys, values, rows,
+                             shape.heads, shape.kv_heads, shape.head_dim, f.capacity, stream);
         vx::stack::Attention(q, keys, values, attention_frag, true, attention_partials, rows,
-                             rows_per_sequence, keys_per_sequence, past, causal, shape.heads,
-                             shape.kv_heads, shape.head_dim, capacity, stream);
+                             f.rows_per_sequence, f.keys_per_sequence, past, f.causal,
+                             shape.heads, shape.kv_heads, shape.head_dim, f.capacity, splits,
+                             past_device, stream);
         vx::fused::Residual(attention_frag, layer.o, static_cast<int>(q_width), s.hidden,
                             h_frag, s, stream);
         vx::fused::GateUp(h_frag, layer.post_norm, layer.gate_up, swiglu_frag, s, stream);
         vx::fused::Residual(swiglu_frag, layer.down, s.ffn, s.hidden, h_frag, s, stream);
       }
-      vx::stack::FromFragments(h_frag, hidden, s.rows, s.hidden, stream);
-      VX_TRY(Grow(&bf16, &bf16_count, rows * width, "vx_stack_forward: hipMalloc"));
-      vx::kernels::RmsNorm(hidden, weights.norm, bf16, output, rows, width, shape.eps, stream);
+      vx::stack::FromFragments(h_frag, f.hidden, s.rows, s.hidden, stream);
+      vx::kernels::RmsNorm(f.hidden, weights.norm, bf16, f.output, rows, width, shape.eps,
+                           stream);
       return vx::LaunchStatus("vx_stack_forward");
     }
-
-    const std::size_t wide = std::max({width, qkv_width, ffn});
-    VX_TRY(Grow(&bf16, &bf16_count, rows * wide, "vx_stack_forward: hipMalloc"));
-    VX_TRY(Grow(&gate_up, &gate_up_floats, rows * 2 * ffn, "vx_stack_forward: hipMalloc"));
     for (std::size_t l = 0; l < layers.size(); ++l) {
       const vx_dit_layer& layer = layers[l];
-      float* keys = k_cache + l * layer_stride;
-      float* values = v_cache + l * layer_stride;
-      vx::kernels::RmsNorm(hidden, layer.input_norm, bf16, nullptr, rows, width, shape.eps,
+      float* keys = f.k_cache + l * layer_stride;
+      float* values = f.v_cache + l * layer_stride;
+      vx::kernels::RmsNorm(f.hidden, layer.input_norm, bf16, nullptr, rows, width, shape.eps,
                            stream);
       VX_TRY(Linear(bf16, layer.qkv, qkv, rows, width, qkv_width, false, stream));
-      vx::kernels::QkvRope(qkv, rope, positions, cache_rows, q, keys, values, rows,
-                           shape.heads, shape.kv_heads, shape.head_dim, capacity, stream);
+      vx::kernels::QkvRope(qkv, rope, f.positions, f.cache_rows, q, keys, values, rows,
+                           shape.heads, shape.kv_heads, shape.head_dim, f.capacity, stream);
       vx::stack::Attention(q, keys, values, bf16, false, attention_partials, rows,
-                           rows_per_sequence, keys_per_sequence, past, causal, shape.heads,
-                           shape.kv_heads, shape.head_dim, capacity, stream);
-      VX_TRY(Linear(bf16, layer.o, hidden, rows, q_width, width, true, stream));
-      vx::kernels::RmsNorm(hidden, layer.post_norm, bf16, nullptr, rows, width, shape.eps,
+                           f.rows_per_sequence, f.keys_per_sequence, past, f.causal,
+                           shape.heads, shape.kv_heads, shape.head_dim, f.capacity, splits,
+                           past_device, stream);
+      VX_TRY(Linear(bf16, layer.o, f.hidden, rows, q_width, width, true, stream));
+      vx::kernels::RmsNorm(f.hidden, layer.post_norm, bf16, nullptr, rows, width, shape.eps,
                            stream);
       VX_TRY(Linear(bf16, layer.gate_up, gate_up, rows, width, 2 * ffn, false, stream));
       vx::kernels::SwiGlu(gate_up, bf16, rows, ffn, stream);
-      VX_TRY(Linear(bf16, layer.down, hidden, rows, ffn, width, true, stream));
+      VX_TRY(Linear(bf16, layer.down, f.hidden, rows, ffn, width, true, stream));
     }
-    vx::kernels::RmsNorm(hidden, weights.norm, bf16, output, rows, width, shape.eps, stream);
+    vx::kernels::RmsNorm(f.hidden, weights.norm, bf16, f.output, rows, width, shape.eps,
+                         stream);
     return vx::LaunchStatus("vx_stack_forward");
+  }
+
+  int Forward(const ForwardKey& f, std::size_t past) {
+    const std::size_t rows = f.rows;
+    const std::size_t sequences = rows / f.rows_per_sequence;
+    // Up to 32 rows (decode steps, encoder patches: the same buffers call
+    // after call) the launches replay as one graph captured on first use;
+    // its attention grid covers every chunk the cache can hold and reads
+    // past from the device.
+    hipStreamCaptureStatus capturing = hipStreamCaptureStatusNone;
+    if (f.stream != nullptr)
+      VX_HIP(hipStreamIsCapturing(f.stream, &capturing), "vx_stack_forward: capture status");
+    const bool graphed = f.stream != nullptr && capturing == hipStreamCaptureStatusNone &&
+                         rows <= vx::q8::kFragRows;
+    const int splits =
+        graphed ? vx::stack::AttentionSplits(
+                      f.capacity - (sequences - 1) * f.keys_per_sequence - f.rows_per_sequence,
+                      f.rows_per_sequence)
+                : vx::stack::AttentionSplits(past, f.rows_per_sequence);
+    const std::size_t partials =
+        vx::stack::AttentionPartialFloats(rows, shape.heads, shape.head_dim, splits);
+    const std::size_t wide = std::max({shape.hidden, qkv_width, shape.ffn});
+    const char* what = "vx_stack_forward: hipMalloc";
+    // Growing a buffer moves it: a graph that holds the old one is dropped.
+    // (Products beyond 128 rows grow their own partials; those rows are
+    // never replayed.)
+    const void* before[] = {attention_partials, q, qkv, bf16, gate_up};
+    VX_TRY(Grow(&attention_partials, &attention_partial_floats, partials, what));
+    VX_TRY(Grow(&q, &q_floats, rows * q_width, what));
+    VX_TRY(Grow(&qkv, &qkv_floats, rows * qkv_width, what));
+    VX_TRY(Grow(&bf16, &bf16_count, rows * wide, what));
+    VX_TRY(Grow(&gate_up, &gate_up_floats, rows * 2 * shape.ffn, what));
+    const void* after[] = {attention_partials, q, qkv, bf16, gate_up};
+    const bool moved = !std::equal(std::begin(before), std::end(before), std::begin(after));
+    if (!graphed)
+      return Launch(f, past, splits, nullptr, f.stream);
+
+    vx::stack::SetPast(past_device, past, f.stream);
+    if (graph == nullptr || moved || !(graph_key == f)) {
+      if (graph != nullptr) {
+        (void)hipGraphExecDestroy(graph);
+        graph = nullptr;
+      }
+      VX_HIP(hipStreamBeginCapture(f.stream, hipStreamCaptureModeThreadLocal),
+             "vx_stack_forward: begin capture");
+      const int status = Launch(f, past, splits, past_device, f.stream);
+      hipGraph_t captured = nullptr;
+      const hipError_t ended = hipStreamEndCapture(f.stream, &captured);
+      if (status != VX_OK) {
+        if (captured != nullptr)
+          (void)hipGraphDestroy(captured);
+        return status;
+      }
+      if (ended != hipSuccess)
+        return vx::FailHip(ended, "vx_stack_forward: end capture");
+      const hipError_t instantiated = hipGraphInstantiate(&graph, captured, nullptr, nullptr, 0);
+      (void)hipGraphDestroy(captured);
+      if (instantiated != hipSuccess) {
+        graph = nullptr;
+        return vx::FailHip(instantiated, "vx_stack_forward: instantiate");
+      }
+      graph_key = f;
+    }
+    VX_HIP(hipGraphLaunch(graph, f.stream), "vx_stack_forward: graph launch");
+    return vx::Succeed();
   }
 };
 
@@ -529,8 +802,8 @@ int CheckStack(const vx_stack_shape& s, const vx_stack_weights& w) {
     return vx::Fail(VX_BAD_ARG, "vx_stack_create: head_dim must be even");
   if (!vx::stack::AttentionSupported(s.heads, s.kv_heads, s.head_dim))
     return vx::Fail(VX_UNSUPPORTED,
-                    "vx_stack_create: attention takes head_dim 64 or 128 and at most 16 "
-                    "query heads per KV head");
+                    "vx_stack_create: attention takes head_dim 64 or 128 and 1, 2, 4, 8 "
+                    "or 16 query heads per KV head");
   if (w.layers == nullptr || w.norm == nullptr)
     return vx::Fail(VX_BAD_ARG, "vx_stack_create: null weights");
   if (s.rope != 0 && w.rope == nullptr)
@@ -583,8 +856,9 @@ int vx_stack_create(vx_stack** stack, const vx_stack_shape* shape,
   fs.eps = shape->eps;
   fs.weights = created->Kind();
   created->fused = vx::fused::StackSupported(fs);
-  int status = VX_OK;
-  if (created->fused) {
+  created->rows_fused = vx::stack::RowsSupported(shape->hidden, shape->ffn);
+  int status = Allocate(&created->past_device, 1);
+  if (status == VX_OK && created->fused) {
     status = Allocate(&created->h_frag, vx::q8::FragElements(shape->hidden));
     if (status == VX_OK)
       status = Allocate(&created->attention_frag, vx::q8::FragElements(created->q_width));
@@ -619,9 +893,21 @@ int vx_stack_forward(vx_stack* stack, float* hidden, float* output, size_t rows,
     return vx::Fail(VX_BAD_ARG, "vx_stack_forward: the attended keys exceed the cache");
   if (capacity > (1U << 24) || rows > (1U << 16))
     return vx::Fail(VX_BAD_ARG, "vx_stack_forward: capacity or rows too large");
-  return stack->Forward(hidden, output, rows, positions, cache_rows, rows_per_sequence,
-                        keys_per_sequence, past, causal != 0, k_cache, v_cache, capacity,
-                        vx::Stream(stream));
+  ForwardKey f;
+  f.hidden = hidden;
+  f.output = output;
+  f.rows = rows;
+  f.positions = positions;
+  f.cache_rows = cache_rows;
+  f.rows_per_sequence = rows_per_sequence;
+  f.keys_per_sequence = keys_per_sequence;
+  f.causal = causal != 0;
+  f.k_cache = k_cache;
+  f.v_cache = v_cache;
+  f.capacity = capacity;
+  f.path = stack->Resolved(rows);
+  f.stream = vx::Stream(stream);
+  return stack->Forward(f, past);
 }
 
 void vx_stack_destroy(vx_stack* stack) { delete stack; }
@@ -629,11 +915,12 @@ void vx_stack_destroy(vx_stack* stack) { delete stack; }
 int vx_stack_set_path(vx_stack* stack, int path) {
   if (stack == nullptr)
     return vx::Fail(VX_BAD_ARG, "vx_stack_set_path: null handle");
-  if (path == VX_STACK_PATH_FUSED && !stack->fused)
-    return vx::Fail(VX_UNSUPPORTED, "vx_stack_set_path: no fused kernels for this shape");
   if (path != VX_STACK_PATH_AUTO && path != VX_STACK_PATH_FUSED &&
-      path != VX_STACK_PATH_UNFUSED)
+      path != VX_STACK_PATH_UNFUSED && path != VX_STACK_PATH_ROWS)
     return vx::Fail(VX_BAD_ARG, "vx_stack_set_path: unknown path");
+  if ((path == VX_STACK_PATH_FUSED && !stack->fused) ||
+      (path == VX_STACK_PATH_ROWS && !stack->rows_fused))
+    return vx::Fail(VX_UNSUPPORTED, "vx_stack_set_path: no such kernels for this shape");
   stack->path = path;
   return VX_OK;
 }
@@ -662,7 +949,7 @@ int vx_split_attention(const float* q, const float* k_cache, const float* v_cach
     return vx::Fail(VX_BAD_ARG, "vx_split_attention: partials too small");
   vx::stack::Attention(q, k_cache, v_cache, output, false, partials, rows, rows_per_sequence,
                        keys_per_sequence, past, causal != 0, heads, kv_heads, head_dim,
-                       capacity, vx::Stream(stream));
+                       capacity, splits, nullptr, vx::Stream(stream));
   return vx::LaunchStatus("vx_split_attention");
 }
 

@@ -361,7 +361,8 @@ def split_attention(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tenso
 
 class Stack:
     """vx_stack (ForwardStack with a key/value cache) over device copies of
-    synthetic stack weights."""
+    synthetic stack weights (synth.StackWeightsHost, or the same fields
+    holding device tensors: uint8 Q8_0 blocks, int16 bf16 bits)."""
 
     def __init__(self, weights: synth.StackWeightsHost, rope: np.ndarray | None,
                  device=None, stream=None, bf16_weights: bool = False):
@@ -369,17 +370,20 @@ class Stack:
         device = _device(device)
         self._keep = []
 
-        def upload_q8(blocks: np.ndarray) -> torch.Tensor:
+        def upload_q8(blocks) -> torch.Tensor:
+            # GGML Q8_0 blocks [n][k / 32][34]: host numpy or device uint8.
             n, kb, _ = blocks.shape
-            raw = torch.from_numpy(np.ascontiguousarray(blocks)).to(device)
+            raw = blocks.to(device) if isinstance(blocks, torch.Tensor) else \
+                torch.from_numpy(np.ascontiguousarray(blocks)).to(device)
             packed = q8_pack(raw, n, kb * 32, stream)
             if bf16_weights:
                 packed = bf16_pack(q8_unpack_bf16(packed, n, kb * 32, stream), stream)
             self._keep.append(packed)
             return packed
 
-        def upload_bf16(bits: np.ndarray) -> torch.Tensor:
-            tensor = torch.from_numpy(bits.view(np.int16).copy()).to(device)
+        def upload_bf16(bits) -> torch.Tensor:
+            tensor = bits.to(device) if isinstance(bits, torch.Tensor) else \
+                torch.from_numpy(bits.view(np.int16).copy()).to(device)
             self._keep.append(tensor)
             return tensor
 
