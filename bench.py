@@ -599,6 +599,8 @@ def main() -> int:
                         help="skip the prefill-sized products")
     parser.add_argument("--pmc-workload", action="store_true",
                         help="only run the eager launches that counter runs read")
+    parser.add_argument("--lm-step-workload", action="store_true",
+                        help="only run the stacks' decode steps (for kernel traces)")
     args = parser.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
@@ -619,6 +621,9 @@ def main() -> int:
     log(f"device {torch.cuda.get_device_properties(0).gcnArchName}")
     if args.pmc_workload:
         pmc_workload(torch, ops, synth, device, stream)
+        return 0
+    if args.lm_step_workload:
+        gpu_lm_step(args, torch, ops, synth, device, stream)
         return 0
 
     probe = read_probe(torch, device, stream)

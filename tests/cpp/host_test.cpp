@@ -1,5 +1,6 @@
-// The C++ host surface (Bf16Gemm::Linear, Generator::Velocity and
-// Generator::Step over the voxcpm_amd C ABI) against the CPU oracle, in the
+// The C++ host surface (Bf16Gemm::Linear, Generator::Velocity,
+// Generator::Step and ForwardStack over the voxcpm_amd C ABI) against the
+// CPU oracle, in the
 // style of the reference's tests/products_test.cpp and
 // tests/generator_test.cpp: random GGML Q8_0 weights, products compared with
 // a double-precision sum relative to sum |x w| (limit 1e-5; 1e-4 for the
@@ -420,6 +421,142 @@ void TestGenerator(Random& rng) {
   Report(on_device == latent, "latent() holds the returned latent");
 }
 
+/// ForwardStack (transformer.cpp:55-100) on a small GQA stack with a key/
+/// value cache: a causal 6-row prefill, then one-row decode steps (the
+/// LM's layout, generator.cpp:482-510) against the oracle's stack, on Q8_0
+/// panels (one vx_stack_forward call) and on bf16 rows of the same weights
+/// (the reference's launch sequence).
+void TestForwardStack(Random& rng, hipStream_t stream) {
+  vc::TransformerConfig config;
+  config.hidden = 256;
+  config.intermediate = 512;
+  config.layers = 2;
+  config.heads = 4;
+  config.kv_heads = 2;
+  config.head_dim = 64;
+  config.rms_eps = 1e-5F;
+  const std::size_t h = config.hidden;
+  const std::size_t qkv = (config.heads + 2 * config.kv_heads) * config.head_dim;
+  const std::size_t q_width = config.heads * config.head_dim;
+  const std::size_t capacity = 16;
+  std::vector<std::vector<std::uint8_t>> blocks;
+  std::vector<std::vector<std::uint16_t>> vectors;
+  std::vector<vc::DeviceBuffer<std::uint8_t>> panels;
+  std::vector<vc::DeviceBuffer<std::uint16_t>> rows_bf16;
+  std::vector<vc::DeviceBuffer<std::uint16_t>> device_vectors;
+  blocks.reserve(16);
+  vectors.reserve(16);
+  panels.reserve(16);
+  rows_bf16.reserve(16);
+  device_vectors.reserve(16);
+  vc::StackWeights q8_stack, bf16_stack;
+  q8_stack.config = bf16_stack.config = config;
+  std::vector<vo_layer> q8_layers, bf16_layers;
+  std::vector<std::vector<std::uint16_t>> dequantized;
+  dequantized.reserve(16);
+  const auto vector = [&](std::size_t count) {
+    std::vector<std::uint16_t> v(count);
+    for (auto& x : v)
+      x = vo_bf16_bits(static_cast<float>(1.0 + 0.02 * rng.Normal()));
+    vectors.push_back(v);
+    device_vectors.push_back(Upload(v));
+    return static_cast<const vc::Bf16*>(device_vectors.back().get());
+  };
+  // One matrix: Q8_0 panels for the first stack, bf16 rows of bf16(scale q)
+  // for the second; the oracle's copies of both.
+  const auto matrix = [&](std::size_t out, std::size_t in, vc::Projection& q8,
+                          vc::Projection& bf16, const std::uint8_t** q8_host,
+                          const std::uint8_t** bf16_host) {
+    blocks.push_back(ModelWeights(out, in, rng));
+    panels.push_back(Pack(blocks.back(), out, in));
+    std::vector<std::uint16_t> w(out * in);
+    vo_q8_dequant_bf16(blocks.back().data(), out, in, w.data());
+    dequantized.push_back(w);
+    rows_bf16.push_back(Upload(w));
+    q8 = {vc::Matrix{vc::WeightFormat::kQ8Panels, panels.back().get()}, nullptr, in, out};
+    bf16 = {vc::Matrix{vc::WeightFormat::kBf16, rows_bf16.back().get()}, nullptr, in, out};
+    *q8_host = blocks.back().data();
+    *bf16_host = reinterpret_cast<const std::uint8_t*>(dequantized.back().data());
+  };
+  for (std::size_t l = 0; l < config.layers; ++l) {
+    vc::LayerWeights a, b;
+    vo_layer oa{}, ob{};
+    a.input_norm = b.input_norm = vector(h);
+    oa.input_norm = ob.input_norm = vectors.back().data();
+    matrix(qkv, h, a.qkv, b.qkv, &oa.qkv, &ob.qkv);
+    matrix(h, q_width, a.o, b.o, &oa.o, &ob.o);
+    a.post_norm = b.post_norm = vector(h);
+    oa.post_norm = ob.post_norm = vectors.back().data();
+    matrix(2 * config.intermediate, h, a.gate_up, b.gate_up, &oa.gate_up, &ob.gate_up);
+    matrix(h, config.intermediate, a.down, b.down, &oa.down, &ob.down);
+    q8_stack.layers.push_back(a);
+    bf16_stack.layers.push_back(b);
+    q8_layers.push_back(oa);
+    bf16_layers.push_back(ob);
+  }
+  q8_stack.norm = bf16_stack.norm = vector(h);
+  vc::RopeConfig rope_config;
+  rope_config.dim = config.head_dim;
+  const std::vector<float> rope = vc::RopeTable(rope_config, 64);
+  const auto rope_device = Upload(rope);
+
+  for (const bool native : {true, false}) {
+    const vc::StackWeights& stack = native ? q8_stack : bf16_stack;
+    vo_stack oracle{};
+    oracle.hidden = h;
+    oracle.heads = config.heads;
+    oracle.kv_heads = config.kv_heads;
+    oracle.head_dim = config.head_dim;
+    oracle.ffn = config.intermediate;
+    oracle.layers = config.layers;
+    oracle.eps = config.rms_eps;
+    oracle.rope = rope.data();
+    oracle.layer = native ? q8_layers.data() : bf16_layers.data();
+    oracle.norm = vectors.back().data();
+    oracle.threads = 4;
+    oracle.bf16_weights = native ? 0 : 1;
+    vc::KvCache cache(config, capacity);
+    vc::StackScratch scratch;
+    vc::Bf16Gemm gemm(nullptr, stream);
+    const std::size_t cache_floats = config.layers * config.kv_heads * capacity * config.head_dim;
+    std::vector<float> k_host(cache_floats, 0.0F), v_host(cache_floats, 0.0F);
+    vc::Check(hipMemset(cache.keys(0), 0, cache_floats * sizeof(float)), "clear");
+    vc::Check(hipMemset(cache.values(0), 0, cache_floats * sizeof(float)), "clear");
+    double worst = 0.0;
+    for (const std::size_t position : {0, 6, 7}) {
+      const std::size_t rows = position == 0 ? 6 : 1;
+      std::vector<std::int32_t> at(rows);
+      for (std::size_t r = 0; r < rows; ++r)
+        at[r] = static_cast<std::int32_t>(position + r);
+      const auto at_device = Upload(at);
+      vc::AttentionLayout layout;
+      layout.positions = at_device.get();
+      layout.cache_rows = at_device.get();
+      layout.rows_per_sequence = rows;
+      layout.keys_per_sequence = rows;
+      layout.past = position;
+      layout.causal = true;
+      std::vector<float> hidden(rows * h);
+      for (auto& v : hidden)
+        v = static_cast<float>(rng.Normal());
+      auto hidden_device = Upload(hidden);
+      vc::DeviceBuffer<float> output(rows * h);
+      vc::ForwardStack(stack, rope_device.get(), layout, cache, hidden_device.get(),
+                       output.get(), rows, scratch, gemm, stream);
+      vc::Check(hipStreamSynchronize(stream), "sync");
+      std::vector<float> expected(rows * h);
+      vo_stack_forward(&oracle, hidden.data(), expected.data(), rows, at.data(), at.data(),
+                       rows, rows, position, 1, k_host.data(), v_host.data(), capacity);
+      worst = std::max(worst, RelativeMax(Download(output.get(), rows * h), expected));
+      worst = std::max(worst, RelativeMax(Download(hidden_device.get(), rows * h), hidden));
+    }
+    worst = std::max(worst, RelativeMax(Download(cache.keys(0), cache_floats), k_host));
+    Report(worst <= 1e-2, std::string("ForwardStack on ") +
+                              (native ? "Q8_0 panels (vx_stack)" : "bf16 rows (per kernel)") +
+                              " against the oracle: " + Scientific(worst));
+  }
+}
+
 }  // namespace
 
 int main() {
@@ -436,6 +573,7 @@ int main() {
     TestLinear(4096, 1024, rng, stream);
     TestLinearBf16(1024, 2560, rng, stream);
     TestGenerator(rng);
+    TestForwardStack(rng, stream);
     vc::Check(hipStreamDestroy(stream), "stream");
   } catch (const std::exception& failure) {
     std::cout << "FAIL " << failure.what() << "\n";

@@ -30,10 +30,56 @@ void Project(const Projection& projection, const Bf16* x, float* y,
             "Project bias");
 }
 
+NativeStacks::~NativeStacks() {
+  for (const Entry& entry : entries_)
+    vx_stack_destroy(entry.handle);
+}
+
+vx_stack* NativeStacks::Get(const StackWeights& stack, const float* rope) {
+  if (stack.layers.empty())
+    return nullptr;
+  const void* key = stack.layers.front().qkv.weight.data;
+  for (const Entry& entry : entries_)
+    if (entry.key == key && entry.rope == rope)
+      return entry.handle;
+  const WeightFormat format = stack.layers.front().qkv.weight.format;
+  if (format != WeightFormat::kQ8Panels && format != WeightFormat::kBf16Panels)
+    return nullptr;
+  std::vector<vx_dit_layer> layers;
+  for (const LayerWeights& layer : stack.layers) {
+    for (const Projection* p : {&layer.qkv, &layer.o, &layer.gate_up, &layer.down})
+      if (p->weight.format != format || p->bias != nullptr)
+        return nullptr;
+    layers.push_back({layer.input_norm, layer.qkv.weight.data, layer.o.weight.data,
+                      layer.post_norm, layer.gate_up.weight.data, layer.down.weight.data});
+  }
+  const TransformerConfig& c = stack.config;
+  const bool rotary = c.rope && rope != nullptr;
+  const vx_stack_shape shape{c.hidden, c.heads, c.kv_heads, c.head_dim, c.intermediate,
+                             stack.layers.size(), c.rms_eps, rotary ? 1 : 0};
+  const vx_stack_weights weights{
+      layers.data(), stack.norm, rotary ? rope : nullptr,
+      format == WeightFormat::kQ8Panels ? static_cast<std::uint32_t>(VX_WEIGHTS_Q8_0)
+                                        : static_cast<std::uint32_t>(VX_WEIGHTS_BF16)};
+  vx_stack* handle = nullptr;
+  if (vx_stack_create(&handle, &shape, &weights) != VX_OK)
+    return nullptr;  // a shape the native stack does not take
+  entries_.push_back({key, rope, handle});
+  return handle;
+}
+
 void ForwardStack(const StackWeights& stack, const float* rope,
                   const AttentionLayout& layout, KvCache& cache, float* hidden,
                   float* output, std::size_t rows, StackScratch& scratch,
                   Bf16Gemm& gemm, hipStream_t stream) {
+  if (vx_stack* native = scratch.native.Get(stack, rope)) {
+    CheckVx(vx_stack_forward(native, hidden, output, rows, layout.positions,
+                             layout.cache_rows, layout.rows_per_sequence,
+                             layout.keys_per_sequence, layout.past, layout.causal ? 1 : 0,
+                             cache.keys(0), cache.values(0), cache.capacity(), stream),
+            "ForwardStack");
+    return;
+  }
   // transformer.cpp:55-100: 12x [RMSNorm, qkv, RoPE + cache, attention,
   // o (+residual), RMSNorm, gate_up, SwiGLU, down (+residual)], final norm.
   const TransformerConfig& config = stack.config;

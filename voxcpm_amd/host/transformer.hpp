@@ -95,6 +95,29 @@ struct AttentionLayout {
   bool causal = true;
 };
 
+/// The vx_stack handles ForwardStack runs, one per stack (by its first
+/// layer's qkv weights) and rotary table; destroyed with the scratch.
+class NativeStacks {
+public:
+  NativeStacks() = default;
+  NativeStacks(const NativeStacks&) = delete;
+  NativeStacks& operator=(const NativeStacks&) = delete;
+  ~NativeStacks();
+
+  /// The handle of `stack` with `rope` (created on first use), or null when
+  /// its weights are in a format vx_stack does not take (rows, tiles,
+  /// biases): ForwardStack then runs its kernels one by one.
+  vx_stack* Get(const StackWeights& stack, const float* rope);
+
+private:
+  struct Entry {
+    const void* key = nullptr;
+    const float* rope = nullptr;
+    vx_stack* handle = nullptr;
+  };
+  std::vector<Entry> entries_;
+};
+
 /// Scratch shared by the stacks (transformer.hpp:51-58).
 struct StackScratch {
   DeviceBuffer<Bf16> normed;
@@ -103,6 +126,7 @@ struct StackScratch {
   DeviceBuffer<Bf16> attention;
   DeviceBuffer<float> gate_up;
   DeviceBuffer<Bf16> activation;
+  NativeStacks native;
 };
 
 /// The rotary table [position][cos (dim / 2) | sin (dim / 2)] in float32
@@ -112,7 +136,9 @@ struct StackScratch {
 
 /// One stack over `rows` rows of the float32 residual `hidden` (updated in
 /// place); the final norm's float32 output goes to `output`
-/// (transformer.hpp:69-72).
+/// (transformer.hpp:69-72). Stacks of Q8_0 or bf16 panels without biases
+/// run as one vx_stack_forward call (fused launches, one HIP graph up to 32
+/// rows); others run the reference's launch sequence.
 void ForwardStack(const StackWeights& stack, const float* rope,
                   const AttentionLayout& layout, KvCache& cache, float* hidden,
                   float* output, std::size_t rows, StackScratch& scratch,
