@@ -355,6 +355,48 @@ int vx_stack_forward(vx_stack* stack, float* hidden, float* output,
                      float* k_cache, float* v_cache, size_t capacity,
                      void* stream);
 
+/* ---- GGUF ingest -----------------------------------------------------------
+ *
+ * The audio.cpp VoxCPM2 GGUF the reference opens in ModelFiles::Open
+ * (model_files.cpp:111-184, model_files.hpp:34-45): a read-only map of the
+ * file, the generator's tensors (VX_GGUF_MODEL, names without "weights/")
+ * and AudioVAE's (VX_GGUF_VAE, without "audiovae_weights/"), abbreviated
+ * names resolved through audiocpp.tensor_names, shapes outermost first
+ * (PyTorch's order), config.json and tokenizer.json from the embedded
+ * files. A Q8_0 matrix goes to the panel layout in one call, as the
+ * reference's Uploader writes kQ8Tiles (weights.cpp:160-186). */
+
+#define VX_GGUF_MODEL 0
+#define VX_GGUF_VAE 1
+
+typedef struct vx_gguf vx_gguf;
+
+/* voxcpm2_layout = 1: the audio.cpp VoxCPM2 layout (VX_BAD_ARG when the
+ * file is not one); 0: any GGUF of version 2 or 3, every tensor under
+ * VX_GGUF_MODEL with the file's own names. VX_BAD_ARG for a malformed file
+ * (vx_gguf_last_error says why). */
+int vx_gguf_open(const char* path, int voxcpm2_layout, vx_gguf** gguf);
+void vx_gguf_close(vx_gguf* gguf);
+/* The message of the last failed vx_gguf_* call of this thread. */
+const char* vx_gguf_last_error(void);
+size_t vx_gguf_tensor_count(const vx_gguf* gguf, int component);
+/* Tensor `index` of a component: name, GGML type (0 F32, 1 F16, 8 Q8_0,
+ * 26 I32, 30 BF16), shape [rank] outermost first (rank <= 8), the mapped
+ * bytes and their count. Any output may be NULL. */
+int vx_gguf_tensor(const vx_gguf* gguf, int component, size_t index,
+                   const char** name, uint32_t* type, size_t* shape,
+                   size_t* rank, const void** data, uint64_t* bytes);
+int vx_gguf_find(const vx_gguf* gguf, int component, const char* name,
+                 size_t* index);
+/* "config.json" or "tokenizer.json" of the VoxCPM2 layout (NULL otherwise);
+ * the text lives as long as the handle. */
+const char* vx_gguf_embedded(const vx_gguf* gguf, const char* file,
+                             size_t* bytes);
+/* A Q8_0 matrix [out][in] into Q8_0 panels (`packed`: device, at least
+ * vx_q8_packed_bytes(out, in) bytes) on `stream`; returns when done. */
+int vx_gguf_upload_q8(const vx_gguf* gguf, int component, size_t index,
+                      void* packed, size_t packed_bytes, void* stream);
+
 /* The rotary table of MiniCPM's LongRoPE on the host, float32 as the
  * reference computes it (transformer.cpp:20-45): [positions][dim], cos in
  * the first half, sin in the second. factors: dim/2 values or NULL. */

@@ -63,6 +63,10 @@ class DitWeights(ctypes.Structure):
 VX_WEIGHTS_Q8_0 = 0
 VX_WEIGHTS_BF16 = 1
 
+# GGUF components (voxcpm_amd.h).
+GGUF_MODEL = 0
+GGUF_VAE = 1
+
 # Stack paths (voxcpm_amd_internal.h).
 STACK_PATH_AUTO = 0
 STACK_PATH_FUSED = 2
@@ -147,6 +151,17 @@ _SIGNATURES = {
     "vx_split_attention": ([c_void_p] * 4 + [c_size] * 4 + [c_int] + [c_size] * 4
                            + [c_void_p, c_size, c_void_p], c_int),
     "vx_split_attention_floats": ([c_size] * 5, c_size),
+    "vx_gguf_open": ([ctypes.c_char_p, c_int, ctypes.POINTER(c_void_p)], c_int),
+    "vx_gguf_close": ([c_void_p], None),
+    "vx_gguf_last_error": ([], ctypes.c_char_p),
+    "vx_gguf_tensor_count": ([c_void_p, c_int], c_size),
+    "vx_gguf_tensor": ([c_void_p, c_int, c_size, ctypes.POINTER(ctypes.c_char_p),
+                        ctypes.POINTER(ctypes.c_uint32), ctypes.POINTER(c_size),
+                        ctypes.POINTER(c_size), ctypes.POINTER(c_void_p),
+                        ctypes.POINTER(ctypes.c_uint64)], c_int),
+    "vx_gguf_find": ([c_void_p, c_int, ctypes.c_char_p, ctypes.POINTER(c_size)], c_int),
+    "vx_gguf_embedded": ([c_void_p, ctypes.c_char_p, ctypes.POINTER(c_size)], c_void_p),
+    "vx_gguf_upload_q8": ([c_void_p, c_int, c_size, c_void_p, c_size, c_void_p], c_int),
     "vx_euler_schedule": ([c_size, c_float, c_int, c_void_p, c_void_p,
                            c_void_p], c_int),
     "vx_rope_table": ([ctypes.c_double, c_size, c_void_p, c_float, c_size,

@@ -19,7 +19,7 @@ __all__ = [
     "Scratch", "Dit", "q8_pack", "q8_unpack_blocks", "q8_unpack_bf16",
     "q8_linear", "q8_linear_bf16", "q8_plan", "bf16_pack", "bf16_unpack", "bf16_linear",
     "bf16_linear_rows", "stream_read", "euler_schedule", "rope_table", "Stack",
-    "split_attention",
+    "split_attention", "Gguf",
 ]
 
 
@@ -448,3 +448,71 @@ class Stack:
                                      _ptr(positions), _ptr(cache_rows), rows_per_sequence,
                                      keys_per_sequence, past, int(causal), _ptr(k_cache),
                                      _ptr(v_cache), k_cache.shape[2], _stream(stream)))
+
+
+class Gguf:
+    """vx_gguf: a GGUF file mapped read-only -- the audio.cpp VoxCPM2 layout
+    (`voxcpm2=True`, ModelFiles::Open's GGUF branch) or any GGUF with its
+    own tensor names."""
+
+    def __init__(self, path: str, voxcpm2: bool = True):
+        from ._lib import VxError
+        handle = ctypes.c_void_p()
+        status = lib().vx_gguf_open(str(path).encode(), int(voxcpm2), ctypes.byref(handle))
+        if status != 0:
+            raise VxError(status, lib().vx_gguf_last_error().decode())
+        self.handle = handle
+
+    def close(self) -> None:
+        if getattr(self, "handle", None):
+            lib().vx_gguf_close(self.handle)
+            self.handle = ctypes.c_void_p()
+
+    def __del__(self):
+        self.close()
+
+    def tensors(self, component: int = 0) -> list[dict]:
+        """Name, GGML type, shape (outermost first) and bytes (a numpy copy)
+        of every tensor of a component (voxcpm_amd._lib.GGUF_MODEL / _VAE)."""
+        out = []
+        for index in range(lib().vx_gguf_tensor_count(self.handle, component)):
+            name = ctypes.c_char_p()
+            kind = ctypes.c_uint32()
+            shape = (ctypes.c_size_t * 8)()
+            rank = ctypes.c_size_t()
+            data = ctypes.c_void_p()
+            size = ctypes.c_uint64()
+            check(lib().vx_gguf_tensor(self.handle, component, index, ctypes.byref(name),
+                                       ctypes.byref(kind), shape, ctypes.byref(rank),
+                                       ctypes.byref(data), ctypes.byref(size)))
+            raw = np.ctypeslib.as_array(ctypes.cast(data, ctypes.POINTER(ctypes.c_uint8)),
+                                        shape=(size.value,)).copy()
+            out.append({"name": name.value.decode(), "type": kind.value,
+                        "shape": tuple(shape[d] for d in range(rank.value)), "bytes": raw})
+        return out
+
+    def embedded(self, file: str) -> str | None:
+        size = ctypes.c_size_t()
+        text = lib().vx_gguf_embedded(self.handle, file.encode(), ctypes.byref(size))
+        return None if text is None else ctypes.string_at(text, size.value).decode()
+
+    def upload_q8(self, name: str, component: int = 0, device=None,
+                  stream=None) -> torch.Tensor:
+        """A Q8_0 matrix [out][in] of the file as Q8_0 panels on the device."""
+        from ._lib import VxError
+        index = ctypes.c_size_t()
+        status = lib().vx_gguf_find(self.handle, component, name.encode(), ctypes.byref(index))
+        if status != 0:
+            raise VxError(status, lib().vx_gguf_last_error().decode())
+        shape = (ctypes.c_size_t * 8)()
+        rank = ctypes.c_size_t()
+        check(lib().vx_gguf_tensor(self.handle, component, index.value, None, None, shape,
+                                   ctypes.byref(rank), None, None))
+        out, inner = (shape[0], shape[1]) if rank.value == 2 else (1, 32)
+        packed = torch.empty(lib().vx_q8_packed_bytes(out, inner), dtype=torch.uint8,
+                             device=_device(device))
+        status = lib().vx_gguf_upload_q8(self.handle, component, index.value, _ptr(packed),
+                                         packed.numel(), _stream(stream))
+        if status != 0:
+            raise VxError(status, lib().vx_gguf_last_error().decode())
+        return packed
