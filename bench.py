@@ -335,6 +335,81 @@ def gpu_lm_step(args, torch, ops, synth, device, stream):
     return out
 
 
+def device_vae_weights(torch, synth, config, device, seed: int):
+    """AudioVAE decoder weights of `config` made on the device with the
+    scales of synth.vae_weights (1/sqrt(fan-in) products, Snake alphas
+    near 1)."""
+    gen = torch.Generator(device=device)
+    gen.manual_seed(seed)
+
+    def normal(shape, std):
+        return torch.randn(shape, device=device, generator=gen) * std
+
+    def alpha(c):
+        return (1.0 + normal((c,), 0.1)).abs() + 0.05
+
+    t = {"in_depthwise": normal((config.latent, 7), 7 ** -0.5),
+         "in_depthwise_bias": normal((config.latent,), 0.02),
+         "in_pointwise": normal((config.decoder_dim, config.latent), config.latent ** -0.5),
+         "in_pointwise_bias": normal((config.decoder_dim,), 0.02), "blocks": []}
+    for b, s in enumerate(config.rates):
+        c_in, c_out = config.channels(b)
+        units = [{"alpha_in": alpha(c_out), "depthwise": normal((c_out, 7), 7 ** -0.5),
+                  "depthwise_bias": normal((c_out,), 0.02), "alpha_out": alpha(c_out),
+                  "pointwise": normal((c_out, c_out), 0.5 * c_out ** -0.5),
+                  "pointwise_bias": normal((c_out,), 0.02)} for _ in range(3)]
+        t["blocks"].append({"stride": s, "scale": 1.0 + normal((c_in,), 0.05),
+                            "bias": normal((c_in,), 0.05), "alpha": alpha(c_in),
+                            "up": normal((c_in, c_out, 2 * s), (2 * c_in) ** -0.5),
+                            "up_bias": normal((c_out,), 0.02), "units": units})
+    c_last = config.channels(len(config.rates) - 1)[1]
+    t["out_alpha"] = alpha(c_last)
+    t["out_conv"] = normal((c_last, 7), (7 * c_last) ** -0.5)
+    t["out_bias"] = 0.01
+    return synth.VaeWeightsHost(config, t)
+
+
+def vae_weight_bytes(config) -> int:
+    """float32 weight bytes one chunk reads: every matrix once (the
+    transposed convolutions as their repacked [s out][2 in] products)."""
+    total = config.latent * 7 + config.decoder_dim * config.latent
+    for b, s in enumerate(config.rates):
+        c_in, c_out = config.channels(b)
+        total += s * c_out * 2 * c_in + 3 * (c_out * c_out + c_out * 7)
+    return 4 * total
+
+
+def gpu_vae(args, torch, ops, synth, device, stream):
+    """AudioVAE V2's decoder on each patch's 4 latent frames (VoxCPM2's
+    shape: 2048 channels, rates 8 6 5 2 2 2: 7680 samples at 48 kHz per
+    patch), the same chunk buffers replayed as one graph."""
+    config = synth.VOXCPM2_VAE
+    weights = device_vae_weights(torch, synth, config, device, 11)
+    vae = ops.Vae(weights, device, stream)
+    chunk = torch.randn((4, config.latent), dtype=torch.float32, device=device)
+    samples = torch.empty(4 * config.hop, dtype=torch.float32, device=device)
+    for _ in range(3):
+        vae.decode(chunk, samples, stream)
+    torch.cuda.synchronize()
+    patches = max(10, args.steps)
+    start = torch.cuda.Event(enable_timing=True)
+    stop = torch.cuda.Event(enable_timing=True)
+    start.record(stream)
+    for _ in range(patches):
+        vae.decode(chunk, samples, stream)
+    stop.record(stream)
+    stop.synchronize()
+    us = start.elapsed_time(stop) * 1e3 / patches
+    nbytes = vae_weight_bytes(config)
+    log(f"AudioVAE decode of one patch (4 frames, {4 * config.hop} samples): {us:.1f} us, "
+        f"{nbytes / 1e6:.1f} MB of float32 weights, {nbytes / us / 1e3:.0f} GB/s")
+    vae.close()
+    return {"us_per_patch": round(us, 1), "frames": 4, "samples": 4 * config.hop,
+            "weight_bytes": nbytes, "gbs": round(nbytes / us / 1e3, 1),
+            "hbm_frac": round(nbytes / us / 1e3 / HBM_PEAK_GBS, 4),
+            "realtime_factor": round(4 * config.hop / 48000 / (us * 1e-6), 1)}
+
+
 def gpu_bf16(args, torch, ops, synth, device, stream):
     """The sweep shapes at M=22 on bf16 weights (2 N K bytes): panels
     (vx_bf16_linear) and rows as they come (vx_bf16_linear_rows), rotated
@@ -594,13 +669,14 @@ def main() -> int:
     parser.add_argument("--no-bf16", action="store_true",
                         help="skip the bf16-weight products")
     parser.add_argument("--no-lm", action="store_true",
-                        help="skip the LM decode shapes")
+                        help="skip the LM decode shapes and steps and the AudioVAE")
     parser.add_argument("--no-prefill", action="store_true",
                         help="skip the prefill-sized products")
     parser.add_argument("--pmc-workload", action="store_true",
                         help="only run the eager launches that counter runs read")
     parser.add_argument("--lm-step-workload", action="store_true",
-                        help="only run the stacks' decode steps (for kernel traces)")
+                        help="only run the stacks' decode steps and the AudioVAE "
+                             "(for kernel traces)")
     args = parser.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
@@ -624,6 +700,7 @@ def main() -> int:
         return 0
     if args.lm_step_workload:
         gpu_lm_step(args, torch, ops, synth, device, stream)
+        gpu_vae(args, torch, ops, synth, device, stream)
         return 0
 
     probe = read_probe(torch, device, stream)
@@ -632,6 +709,7 @@ def main() -> int:
     lm = None if args.no_lm else gpu_lm(args, torch, ops, synth, device, stream)
     if lm is not None:
         lm["steps"] = gpu_lm_step(args, torch, ops, synth, device, stream)
+    vae = None if args.no_lm else gpu_vae(args, torch, ops, synth, device, stream)
     bf16 = None if args.no_bf16 else gpu_bf16(args, torch, ops, synth, device, stream)
     prefill = None if args.no_prefill else gpu_prefill(args, torch, ops, synth, device, stream)
     patch = None if args.no_patch else gpu_patch(args, torch, ops, synth, device, stream)
@@ -688,6 +766,7 @@ def main() -> int:
         "read_probe_gbs": round(probe, 1),
         "sweep": products["sweep"],
         "lm_decode": lm,
+        "vae_decode": vae,
         "bf16_weights": bf16,
         "prefill": prefill,
         "patch": patch,

@@ -397,6 +397,70 @@ const char* vx_gguf_embedded(const vx_gguf* gguf, const char* file,
 int vx_gguf_upload_q8(const vx_gguf* gguf, int component, size_t index,
                       void* packed, size_t packed_bytes, void* stream);
 
+/* ---- AudioVAE V2's decoder ---------------------------------------------------
+ *
+ * AudioVae's decoding (vae.hpp:25-80, vae.cpp:370-481): float32, time-major
+ * [t][c], chunk by chunk with each causal convolution's history kept in the
+ * handle (decoding in chunks equals decoding at once). Weights are the
+ * checkpoint's tensors with weight normalization folded, in PyTorch's
+ * layouts, device float32; the rate conditioning is the bucket of the
+ * output rate (AudioVaeConfig::rate_bucket, config.cpp:269-275). */
+
+typedef struct vx_vae_unit {    /* a residual unit of c channels */
+  const float* alpha_in;        /* [c] Snake */
+  const float* depthwise;       /* [c][7] */
+  const float* depthwise_bias;  /* [c] */
+  const float* alpha_out;       /* [c] Snake */
+  const float* pointwise;       /* [c][c] (out, in) */
+  const float* pointwise_bias;  /* [c] */
+} vx_vae_unit;
+
+typedef struct vx_vae_block {   /* in -> in / 2 channels, rate x frames */
+  const float* scale;           /* [in] the rate bucket's scale_embed row */
+  const float* bias;            /* [in] the rate bucket's bias_embed row */
+  const float* alpha;           /* [in] Snake */
+  const float* up;              /* ConvTranspose1d [in][in / 2][2 rate] */
+  const float* up_bias;         /* [in / 2] */
+  vx_vae_unit units[3];         /* dilations 1, 3, 9 */
+} vx_vae_block;
+
+typedef struct vx_vae_shape {
+  size_t latent_dim;            /* AudioVaeConfig (config.hpp:55-72) */
+  size_t decoder_dim;
+  size_t rate_count;            /* decoder blocks, at most 8 */
+  size_t rates[8];
+} vx_vae_shape;
+
+typedef struct vx_vae_weights {
+  const float* in_depthwise;       /* [latent][7] */
+  const float* in_depthwise_bias;  /* [latent] */
+  const float* in_pointwise;       /* [decoder_dim][latent] */
+  const float* in_pointwise_bias;  /* [decoder_dim] */
+  const vx_vae_block* blocks;      /* host array of rate_count entries */
+  const float* out_alpha;          /* [c] of the last block */
+  const float* out_conv;           /* [c][7] (Conv1d to one channel) */
+  float out_bias;
+} vx_vae_weights;
+
+typedef struct vx_vae vx_vae;
+
+/* Creates a decoder over caller-owned device weights (the handle keeps the
+ * pointers; the transposed convolutions are repacked into its own
+ * buffers), its history cleared. */
+int vx_vae_create(vx_vae** vae, const vx_vae_shape* shape,
+                  const vx_vae_weights* weights);
+void vx_vae_destroy(vx_vae* vae);
+/* AudioVae::Reset: a new stream (zero history). */
+int vx_vae_reset(vx_vae* vae, void* stream);
+/* Output samples per latent frame (AudioVaeConfig::decode_hop). */
+size_t vx_vae_hop(const vx_vae* vae);
+/* AudioVae::Decode / Enqueue on device data: latents [frames][latent]
+ * -> samples [frames * hop] at the output rate, continuing the stream.
+ * Chunks of up to 16 frames replay as one HIP graph from their second call
+ * with the same buffers. */
+int vx_vae_decode(vx_vae* vae, const float* latents, size_t frames,
+                  float* samples, void* stream);
+
 /* The rotary table of MiniCPM's LongRoPE on the host, float32 as the
  * reference computes it (transformer.cpp:20-45): [positions][dim], cos in
  * the first half, sin in the second. factors: dim/2 values or NULL. */

@@ -756,3 +756,128 @@ void vo_stack_forward(const vo_stack* stack, float* hidden, float* output,
   free(q);
   free(gate_up);
 }
+
+/* ---- AudioVAE V2's causal decoder --------------------------------------- */
+
+/* x + (1 / (alpha + 1e-9)) sin^2(alpha x) (kernels/vae_kernels.hip:19-34),
+ * after the optional rate conditioning x scale + bias. */
+static void vae_snake(float* data, size_t t, size_t c, const float* alpha,
+                      const float* scale, const float* bias) {
+  for (size_t i = 0; i < t * c; ++i) {
+    const size_t ch = i % c;
+    float y = data[i];
+    if (scale != NULL)
+      y = y * scale[ch] + bias[ch];
+    const float a = alpha[ch];
+    const float s = sinf(a * y);
+    data[i] = y + (1.0f / (a + 1e-9f)) * (s * s);
+  }
+}
+
+/* Causal depthwise convolution, kernel 7, dilation d, zero history
+ * (vae_kernels.hip:36-53). */
+static void vae_depthwise(const float* in, const float* w, const float* b,
+                          float* out, size_t t, size_t c, size_t d) {
+  for (size_t f = 0; f < t; ++f)
+    for (size_t ch = 0; ch < c; ++ch) {
+      float sum = b[ch];
+      for (size_t j = 0; j < 7; ++j) {
+        const long src = (long)f + (long)(j * d) - (long)(6 * d);
+        if (src >= 0)
+          sum += w[ch * 7 + j] * in[(size_t)src * c + ch];
+      }
+      out[f * c + ch] = sum;
+    }
+}
+
+/* y[t][o] (+)= sum_i w[o][i] x[t][i] + b[o]. */
+static void vae_pointwise(const float* x, const float* w, const float* b,
+                          float* y, size_t t, size_t in, size_t out,
+                          int accumulate) {
+  for (size_t f = 0; f < t; ++f)
+    for (size_t o = 0; o < out; ++o) {
+      float sum = 0.0f;
+      for (size_t i = 0; i < in; ++i)
+        sum += w[o * in + i] * x[f * in + i];
+      sum += b[o];
+      y[f * out + o] = accumulate ? y[f * out + o] + sum : sum;
+    }
+}
+
+void vo_vae_decode(const vo_vae* vae, const float* latents, size_t frames,
+                   float* samples) {
+  /* vae.cpp:415-481 */
+  size_t widest = frames * (vae->latent > vae->decoder_dim ? vae->latent
+                                                           : vae->decoder_dim);
+  size_t length = frames, channels = vae->decoder_dim;
+  for (size_t b = 0; b < vae->block_count; ++b) {
+    length *= vae->blocks[b].stride;
+    channels /= 2;
+    if (length * channels > widest)
+      widest = length * channels;
+  }
+  float* hidden = (float*)malloc(widest * sizeof(float));
+  float* next = (float*)malloc(widest * sizeof(float));
+  float* work = (float*)malloc(widest * sizeof(float));
+  float* scratch = (float*)malloc(widest * sizeof(float));
+
+  /* Input: depthwise (latent channels), then pointwise to decoder_dim. */
+  vae_depthwise(latents, vae->in_depthwise, vae->in_depthwise_bias, scratch,
+                frames, vae->latent, 1);
+  vae_pointwise(scratch, vae->in_pointwise, vae->in_pointwise_bias, hidden,
+                frames, vae->latent, vae->decoder_dim, 0);
+  size_t t = frames, c = vae->decoder_dim;
+  static const size_t dilations[3] = {1, 3, 9};
+  for (size_t b = 0; b < vae->block_count; ++b) {
+    const vo_vae_block* block = &vae->blocks[b];
+    const size_t in = c, out = c / 2, s = block->stride;
+    memcpy(work, hidden, t * in * sizeof(float));
+    vae_snake(work, t, in, block->alpha, block->scale, block->bias);
+    /* ConvTranspose1d, kernel 2s, stride s, the first t s outputs:
+     * out[f s + r][o] = b[o] + sum_i W[i][o][r] x[f][i]
+     *                        + sum_i W[i][o][r + s] x[f - 1][i]. */
+    for (size_t f = 0; f < t; ++f)
+      for (size_t r = 0; r < s; ++r)
+        for (size_t o = 0; o < out; ++o) {
+          float sum = 0.0f;
+          for (size_t i = 0; i < in; ++i)
+            sum += block->up[(i * out + o) * 2 * s + r] * work[f * in + i];
+          if (f > 0)
+            for (size_t i = 0; i < in; ++i)
+              sum += block->up[(i * out + o) * 2 * s + r + s] *
+                     work[(f - 1) * in + i];
+          next[(f * s + r) * out + o] = sum + block->up_bias[o];
+        }
+    t *= s;
+    c = out;
+    memcpy(hidden, next, t * c * sizeof(float));
+    for (size_t u = 0; u < 3; ++u) {
+      const vo_vae_unit* unit = &block->units[u];
+      memcpy(work, hidden, t * c * sizeof(float));
+      vae_snake(work, t, c, unit->alpha_in, NULL, NULL);
+      vae_depthwise(work, unit->depthwise, unit->depthwise_bias, scratch, t, c,
+                    dilations[u]);
+      vae_snake(scratch, t, c, unit->alpha_out, NULL, NULL);
+      vae_pointwise(scratch, unit->pointwise, unit->pointwise_bias, hidden, t,
+                    c, c, 1);
+    }
+  }
+  /* Output: Snake, causal conv c -> 1 (kernel 7), tanh
+   * (vae_kernels.hip:70-93). */
+  memcpy(work, hidden, t * c * sizeof(float));
+  vae_snake(work, t, c, vae->out_alpha, NULL, NULL);
+  for (size_t f = 0; f < t; ++f) {
+    float sum = 0.0f;
+    for (size_t ch = 0; ch < c; ++ch)
+      for (size_t j = 0; j < 7; ++j) {
+        const long src = (long)f + (long)j - 6;
+        if (src >= 0)
+          sum += vae->out_conv[ch * 7 + j] * work[(size_t)src * c + ch];
+      }
+    samples[f] = tanhf(sum + vae->out_bias);
+  }
+  free(hidden);
+  free(next);
+  free(work);
+  free(scratch);
+}

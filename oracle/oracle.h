@@ -205,6 +205,45 @@ void vo_stack_forward(const vo_stack* stack, float* hidden, float* output,
                       size_t keys_per_sequence, size_t past, int causal,
                       float* k_cache, float* v_cache, size_t capacity);
 
+/* ---- AudioVAE V2's causal decoder (float32, time-major [t][c]) ---------- */
+
+typedef struct vo_vae_unit {   /* a residual unit of `c` channels */
+  const float* alpha_in;       /* [c] */
+  const float* depthwise;      /* [c][7] */
+  const float* depthwise_bias; /* [c] */
+  const float* alpha_out;      /* [c] */
+  const float* pointwise;      /* [c][c] (out, in) */
+  const float* pointwise_bias; /* [c] */
+} vo_vae_unit;
+
+typedef struct vo_vae_block {  /* in -> out = in / 2 channels, x stride */
+  size_t stride;
+  const float* scale;          /* [in]: the rate bucket's conditioning */
+  const float* bias;           /* [in] */
+  const float* alpha;          /* [in] */
+  const float* up;             /* ConvTranspose1d [in][out][2 stride] */
+  const float* up_bias;        /* [out] */
+  vo_vae_unit units[3];        /* dilations 1, 3, 9 */
+} vo_vae_block;
+
+typedef struct vo_vae {
+  size_t latent, decoder_dim, block_count;
+  const float* in_depthwise;      /* [latent][7] */
+  const float* in_depthwise_bias; /* [latent] */
+  const float* in_pointwise;      /* [decoder_dim][latent] */
+  const float* in_pointwise_bias; /* [decoder_dim] */
+  const vo_vae_block* blocks;
+  const float* out_alpha;         /* [c] of the last block */
+  const float* out_conv;          /* [c][7] */
+  float out_bias;
+} vo_vae;
+
+/* The decoder over whole sequences from zero history (vae.cpp:415-481 for
+ * one chunk; weight normalization already folded): latents
+ * [frames][latent] -> samples [frames * prod(strides)]. */
+void vo_vae_decode(const vo_vae* vae, const float* latents, size_t frames,
+                   float* samples);
+
 #ifdef __cplusplus
 }
 #endif

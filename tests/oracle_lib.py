@@ -86,6 +86,7 @@ _SIGNATURES = {
                      None),
     # (vo_stack*, hidden, output, rows, positions, cache_rows,
     #  rows_per_sequence, keys_per_sequence, past, causal, k, v, capacity)
+    "vo_vae_decode": ([c_void_p, c_void_p, c_size, c_void_p], None),
     "vo_stack_forward": ([c_void_p, c_void_p, c_void_p, c_size, c_void_p, c_void_p,
                           c_size, c_size, c_size, c_int, c_void_p, c_void_p, c_size],
                          None),
@@ -191,6 +192,24 @@ class Stack(ctypes.Structure):
         "hidden", "heads", "kv_heads", "head_dim", "ffn", "layers")] + [
         ("eps", ctypes.c_float), ("rope", c_void_p), ("layer", ctypes.POINTER(Layer)),
         ("norm", c_void_p), ("threads", ctypes.c_int), ("bf16_weights", ctypes.c_int)]
+
+
+class VaeUnit(ctypes.Structure):
+    _fields_ = [(n, c_void_p) for n in ("alpha_in", "depthwise", "depthwise_bias",
+                                         "alpha_out", "pointwise", "pointwise_bias")]
+
+
+class VaeBlock(ctypes.Structure):
+    _fields_ = [("stride", c_size)] + [(n, c_void_p) for n in (
+        "scale", "bias", "alpha", "up", "up_bias")] + [("units", VaeUnit * 3)]
+
+
+class Vae(ctypes.Structure):
+    _fields_ = [(n, c_size) for n in ("latent", "decoder_dim", "block_count")] + [
+        (n, c_void_p) for n in ("in_depthwise", "in_depthwise_bias", "in_pointwise",
+                                "in_pointwise_bias")] + [
+        ("blocks", ctypes.POINTER(VaeBlock)), ("out_alpha", c_void_p),
+        ("out_conv", c_void_p), ("out_bias", c_float)]
 
 
 class OracleDit:
@@ -320,3 +339,40 @@ class OracleStack:
                                keys_per_sequence, past, int(causal), ptr(k_cache),
                                ptr(v_cache), capacity)
         return hidden, output
+
+
+class OracleVae:
+    """A vo_vae over host copies of synthetic decoder weights."""
+
+    def __init__(self, weights):
+        t = weights.tensors
+        self.config = weights.config
+        self._keep = []
+
+        def keep(array):
+            array = np.ascontiguousarray(array, dtype=np.float32)
+            self._keep.append(array)
+            return array.ctypes.data
+
+        blocks = (VaeBlock * len(t["blocks"]))()
+        for i, b in enumerate(t["blocks"]):
+            units = (VaeUnit * 3)()
+            for u, unit in enumerate(b["units"]):
+                units[u] = VaeUnit(*(keep(unit[n]) for n in (
+                    "alpha_in", "depthwise", "depthwise_bias", "alpha_out", "pointwise",
+                    "pointwise_bias")))
+            blocks[i] = VaeBlock(b["stride"], keep(b["scale"]), keep(b["bias"]),
+                                 keep(b["alpha"]), keep(b["up"]), keep(b["up_bias"]), units)
+        self._blocks = blocks
+        c = self.config
+        self.struct = Vae(c.latent, c.decoder_dim, len(t["blocks"]), keep(t["in_depthwise"]),
+                          keep(t["in_depthwise_bias"]), keep(t["in_pointwise"]),
+                          keep(t["in_pointwise_bias"]), blocks, keep(t["out_alpha"]),
+                          keep(t["out_conv"]), t["out_bias"])
+
+    def decode(self, latents: np.ndarray) -> np.ndarray:
+        latents = np.ascontiguousarray(latents, dtype=np.float32)
+        frames = latents.shape[0]
+        out = np.zeros(frames * self.config.hop, dtype=np.float32)
+        lib().vo_vae_decode(ctypes.addressof(self.struct), ptr(latents), frames, ptr(out))
+        return out

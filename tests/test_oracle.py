@@ -626,3 +626,71 @@ def test_stack_bidirectional_sequences(oracle):
     assert relative(out, ref_out) < 5e-4
     assert relative(h, ref_h) < 5e-4
     assert relative(out[::-1], ref_out) > 5e-2
+
+
+# ---- AudioVAE's decoder against a float64 torch formulation ----------------
+
+def torch_vae_decode(weights, latents):
+    """AudioVAE V2's causal decoder in float64 torch from the module
+    description: causal convolutions as left-padded conv1d, the causal
+    transposed convolution as conv_transpose1d's first T s outputs, Snake
+    x + sin^2(a x) / (a + 1e-9), the output conv's tanh."""
+    t = weights.tensors
+    F = torch.nn.functional
+
+    def T(a):
+        return torch.from_numpy(np.asarray(a, dtype=np.float64))
+
+    def snake(x, a):
+        a = T(a)[None, :, None]
+        return x + torch.sin(a * x) ** 2 / (a + 1e-9)
+
+    def depthwise(x, w, b, d):
+        c = x.shape[1]
+        return F.conv1d(F.pad(x, (6 * d, 0)), T(w).reshape(c, 1, 7), T(b), dilation=d, groups=c)
+
+    x = T(latents).T[None]  # [1][latent][frames]
+    x = depthwise(x, t["in_depthwise"], t["in_depthwise_bias"], 1)
+    x = F.conv1d(x, T(t["in_pointwise"])[:, :, None], T(t["in_pointwise_bias"]))
+    for block in t["blocks"]:
+        s = block["stride"]
+        frames = x.shape[2]
+        x = x * T(block["scale"])[None, :, None] + T(block["bias"])[None, :, None]
+        x = snake(x, block["alpha"])
+        x = F.conv_transpose1d(x, T(block["up"]), T(block["up_bias"]), stride=s)[..., :frames * s]
+        for unit, d in zip(block["units"], (1, 3, 9)):
+            y = snake(x, unit["alpha_in"])
+            y = depthwise(y, unit["depthwise"], unit["depthwise_bias"], d)
+            y = snake(y, unit["alpha_out"])
+            x = x + F.conv1d(y, T(unit["pointwise"])[:, :, None], T(unit["pointwise_bias"]))
+    x = snake(x, t["out_alpha"])
+    c = x.shape[1]
+    x = F.conv1d(F.pad(x, (6, 0)), T(t["out_conv"]).reshape(1, c, 7), T([t["out_bias"]]))
+    return torch.tanh(x)[0, 0].numpy()
+
+
+def test_vae_decoder_against_float64_torch(oracle):
+    config = synth.VaeConfig(latent=16, decoder_dim=64, rates=(3, 2, 2))
+    weights = synth.vae_weights(config, 81)
+    vae = oracle.OracleVae(weights)
+    rng = synth.Rng(82, 1)
+    latents = rng.normal(9 * config.latent).astype(np.float32).reshape(9, config.latent)
+    got = vae.decode(latents)
+    ref = torch_vae_decode(weights, latents)
+    assert got.shape == ref.shape == (9 * config.hop,)
+    error = float(np.max(np.abs(got - ref)))
+    assert error < 2e-5, error  # float32 against float64
+    assert np.std(ref) > 0.05  # a signal, not a saturated or silent output
+    # Causality: the first five frames' samples do not depend on the rest.
+    head = vae.decode(latents[:5])
+    assert np.array_equal(head, got[:5 * config.hop])
+    # A planted slip (the transposed convolution's previous-frame taps taken
+    # from the current frame) is caught.
+    slip = synth.VaeWeightsHost(config, dict(weights.tensors))
+    blocks = [dict(b) for b in weights.tensors["blocks"]]
+    s = blocks[0]["stride"]
+    up = blocks[0]["up"].copy()
+    up[:, :, s:] = up[:, :, :s]
+    blocks[0]["up"] = up
+    slip.tensors["blocks"] = blocks
+    assert np.max(np.abs(oracle.OracleVae(slip).decode(latents) - ref)) > 1e-2

@@ -63,6 +63,28 @@ class DitWeights(ctypes.Structure):
 VX_WEIGHTS_Q8_0 = 0
 VX_WEIGHTS_BF16 = 1
 
+
+class VaeUnit(ctypes.Structure):
+    _fields_ = [(n, c_void_p) for n in ("alpha_in", "depthwise", "depthwise_bias",
+                                         "alpha_out", "pointwise", "pointwise_bias")]
+
+
+class VaeBlock(ctypes.Structure):
+    _fields_ = [(n, c_void_p) for n in ("scale", "bias", "alpha", "up", "up_bias")] + [
+        ("units", VaeUnit * 3)]
+
+
+class VaeShape(ctypes.Structure):
+    _fields_ = [("latent_dim", c_size), ("decoder_dim", c_size), ("rate_count", c_size),
+                ("rates", c_size * 8)]
+
+
+class VaeWeights(ctypes.Structure):
+    _fields_ = [(n, c_void_p) for n in ("in_depthwise", "in_depthwise_bias", "in_pointwise",
+                                         "in_pointwise_bias")] + [
+        ("blocks", ctypes.POINTER(VaeBlock)), ("out_alpha", c_void_p), ("out_conv", c_void_p),
+        ("out_bias", c_float)]
+
 # GGUF components (voxcpm_amd.h).
 GGUF_MODEL = 0
 GGUF_VAE = 1
@@ -162,6 +184,12 @@ _SIGNATURES = {
     "vx_gguf_find": ([c_void_p, c_int, ctypes.c_char_p, ctypes.POINTER(c_size)], c_int),
     "vx_gguf_embedded": ([c_void_p, ctypes.c_char_p, ctypes.POINTER(c_size)], c_void_p),
     "vx_gguf_upload_q8": ([c_void_p, c_int, c_size, c_void_p, c_size, c_void_p], c_int),
+    "vx_vae_create": ([ctypes.POINTER(c_void_p), ctypes.POINTER(VaeShape),
+                       ctypes.POINTER(VaeWeights)], c_int),
+    "vx_vae_destroy": ([c_void_p], None),
+    "vx_vae_reset": ([c_void_p, c_void_p], c_int),
+    "vx_vae_hop": ([c_void_p], c_size),
+    "vx_vae_decode": ([c_void_p, c_void_p, c_size, c_void_p, c_void_p], c_int),
     "vx_euler_schedule": ([c_size, c_float, c_int, c_void_p, c_void_p,
                            c_void_p], c_int),
     "vx_rope_table": ([ctypes.c_double, c_size, c_void_p, c_float, c_size,

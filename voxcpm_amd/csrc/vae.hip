@@ -1,0 +1,598 @@
+// AudioVAE V2's causal decoder on one stream, float32, time-major [t][c]:
+// the consumer of each patch's latents (vae.cpp:415-481). Chunk by chunk
+// with every causal convolution's history carried in a state buffer, which
+// equals decoding at once.
+//
+// Per chunk: the latents' depthwise and pointwise input convolutions, then
+// per decoder block the rate-conditioned Snake, the causal transposed
+// convolution as ONE product over [x(t) | x(t-1)] (the two taps' weights
+// side by side, K = 2 in), and three residual units (Snake, dilated
+// depthwise conv fused with the second Snake, pointwise product added into
+// the stream), then Snake and the 7-tap convolution to mono with tanh.
+// Each bias is applied by the next elementwise kernel as it reads the
+// stream; each state is filled by the kernel that first reads it and
+// refreshed by a later kernel that does not, so no copies remain. The
+// products are plain float32 GEMMs (rocBLAS, as the reference calls
+// hipblasSgemm) except those of up to 32 rows (the first blocks, whose
+// weights are most of the bytes), which take a float32 MFMA kernel reading
+// the weights once; up to 16 latent frames per chunk the launches replay
+// as one HIP graph.
+#include <hip/hip_runtime.h>
+#include <rocblas/rocblas.h>
+
+#include <algorithm>
+#include <cmath>
+#include <cstdint>
+#include <vector>
+
+#include "common.hpp"
+#include "q8_tile.hpp"
+#include "voxcpm_amd.h"
+
+namespace {
+
+using vx::kWave;
+
+constexpr int kThreads = 256;
+constexpr int kTaps = 7;
+constexpr int kDilations[3] = {1, 3, 9};
+constexpr std::size_t kMaxGraphFrames = 16;
+
+dim3 Blocks(std::size_t count) {
+  return dim3(static_cast<unsigned>((count + kThreads - 1) / kThreads));
+}
+
+__device__ inline float Snake(float y, float a) {
+  const float s = sinf(a * y);
+  return y + (1.0F / (a + 1e-9F)) * (s * s);
+}
+
+/// work = [state (kTaps - 1 rows) | latents (t rows)] of `c` channels.
+__global__ void StageKernel(const float* state, const float* latents, float* work,
+                            std::size_t t, std::size_t c) {
+  const std::size_t i = static_cast<std::size_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  const std::size_t head = (kTaps - 1) * c;
+  if (i < head)
+    work[i] = state[i];
+  else if (i < head + t * c)
+    work[i] = latents[i - head];
+}
+
+/// out[f][c] = b[c] + sum_j w[c][j] work[f + j d][c] (work holds 6 d rows
+/// of history first), optionally through Snake(alpha); afterwards
+/// state = work's last 6 d rows (this kernel never reads the state).
+__global__ void DepthwiseKernel(const float* work, const float* w, const float* b,
+                                const float* alpha, float* out, float* state, std::size_t t,
+                                std::size_t c, int d) {
+  const std::size_t i = static_cast<std::size_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  const std::size_t rows = static_cast<std::size_t>(kTaps - 1) * d;
+  if (i < rows * c)
+    state[i] = work[t * c + i];
+  if (i >= t * c)
+    return;
+  const std::size_t f = i / c;
+  const std::size_t ch = i % c;
+  float sum = b[ch];
+#pragma unroll
+  for (int j = 0; j < kTaps; ++j)
+    sum += w[ch * kTaps + j] * work[(f + static_cast<std::size_t>(j) * d) * c + ch];
+  out[i] = alpha != nullptr ? Snake(sum, alpha[ch]) : sum;
+}
+
+/// The block's input: v = hidden + pending bias, y = Snake(v scale + bias);
+/// x2[f] = [y(f) | y(f - 1)] with y(-1) the state (the last frame of the
+/// previous chunk). The thread of (frame 0, channel c) also recomputes
+/// y(t - 1, c) into the state after reading it.
+__global__ void BlockInputKernel(const float* hidden, const float* pending, const float* scale,
+                                 const float* bias, const float* alpha, float* x2,
+                                 float* state, std::size_t t, std::size_t c) {
+  const std::size_t i = static_cast<std::size_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i >= t * c)
+    return;
+  const std::size_t f = i / c;
+  const std::size_t ch = i % c;
+  const auto snake_at = [&](std::size_t frame) {
+    const float v = hidden[frame * c + ch] + pending[ch];
+    return Snake(v * scale[ch] + bias[ch], alpha[ch]);
+  };
+  const float y = snake_at(f);
+  x2[f * 2 * c + ch] = y;
+  if (f + 1 < t)
+    x2[(f + 1) * 2 * c + c + ch] = y;
+  if (f == 0) {
+    x2[c + ch] = state[ch];
+    state[ch] = t == 1 ? y : snake_at(t - 1);
+  }
+}
+
+/// A residual unit's input: hidden += pending bias (in place), work =
+/// [state (6 d rows) | Snake(hidden, alpha)].
+__global__ void UnitInputKernel(float* hidden, const float* pending, const float* alpha,
+                                const float* state, float* work, std::size_t t, std::size_t c,
+                                int d) {
+  const std::size_t i = static_cast<std::size_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  const std::size_t head = static_cast<std::size_t>(kTaps - 1) * d * c;
+  if (i < head)
+    work[i] = state[i];
+  if (i >= t * c)
+    return;
+  const std::size_t ch = i % c;
+  const float v = hidden[i] + (pending != nullptr ? pending[ch] : 0.0F);
+  hidden[i] = v;
+  work[head + i] = Snake(v, alpha[ch]);
+}
+
+/// The output: work = [state (6 rows) | Snake(hidden + pending, alpha)].
+__global__ void OutputInputKernel(const float* hidden, const float* pending, const float* alpha,
+                                  const float* state, float* work, std::size_t t, std::size_t c) {
+  const std::size_t i = static_cast<std::size_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  const std::size_t head = (kTaps - 1) * c;
+  if (i < head)
+    work[i] = state[i];
+  if (i >= t * c)
+    return;
+  const std::size_t ch = i % c;
+  work[head + i] = Snake(hidden[i] + pending[ch], alpha[ch]);
+}
+
+/// samples[f] = tanh(b + sum_c sum_j w[c][j] work[f + j][c]), one
+/// workgroup per 4 frames, lanes over channels; afterwards state = work's
+/// last 6 rows (this kernel never reads the state).
+__global__ void ToMonoKernel(const float* work, const float* w, float b, float* samples,
+                             float* state, std::size_t t, std::size_t c) {
+  __shared__ float partial[kThreads / kWave];
+  const std::size_t first = static_cast<std::size_t>(blockIdx.x) * 4;
+  const int lane = static_cast<int>(threadIdx.x) % kWave;
+  const int wave = static_cast<int>(threadIdx.x) / kWave;  // frame first + wave
+  if (blockIdx.x == 0)
+    for (std::size_t i = threadIdx.x; i < (kTaps - 1) * c; i += blockDim.x)
+      state[i] = work[t * c + i];
+  const std::size_t f = first + wave;
+  float sum = 0.0F;
+  if (f < t)
+    for (std::size_t ch = lane; ch < c; ch += kWave)
+#pragma unroll
+      for (int j = 0; j < kTaps; ++j)
+        sum += w[ch * kTaps + j] * work[(f + j) * c + ch];
+  sum = vx::WaveSum(sum);
+  if (lane == 0)
+    partial[wave] = sum;
+  __syncthreads();
+  if (threadIdx.x < 4 && first + threadIdx.x < t)
+    samples[first + threadIdx.x] = tanhf(partial[threadIdx.x] + b);
+}
+
+// ---- float32 products of few rows ------------------------------------------
+//
+// y[t][n] (+)= x[t][k] W[n][k]^T for t <= 32 (the first blocks: 4 and 32
+// frames per patch) on v_mfma_f32_16x16x4_f32, float32 throughout. A
+// workgroup owns 16 columns of W; its 16 waves split k in groups of 16.
+// Within a group lane L (r = L % 16, g = L / 16) loads W[n0 + r][k0 + 4 g
+// .. + 3] and x[16 m + r][k0 + 4 g .. + 3] as float4 and step s of four
+// multiplies the k-slots {k0 + 4 g + s}: the weights are read in place, 64
+// contiguous bytes per row per load. The waves' sums meet in LDS in wave
+// order.
+
+constexpr int kF32Waves = 16;
+typedef float F32x4 __attribute__((ext_vector_type(4)));
+
+template<int MT>
+__global__ __launch_bounds__(kF32Waves * kWave) void F32SkinnyKernel(
+    const float* x, const float* w, float* y, int t, int k, int n, int accumulate) {
+  __shared__ float reduce[kF32Waves][MT][4][kWave];
+  const int lane = static_cast<int>(threadIdx.x) % kWave;
+  const int wave = static_cast<int>(threadIdx.x) / kWave;
+  const int r = lane % 16;
+  const int g = lane / 16;
+  const int n0 = 16 * static_cast<int>(blockIdx.x);
+  const bool column_ok = n0 + r < n;
+  // Buffer loads: masked lanes read zero without a branch, so a wave's
+  // loads stay in flight together.
+  const __amdgpu_buffer_rsrc_t w_buffer =
+      vx::q8::BufferOf(w, 4U * static_cast<std::uint32_t>(n) * static_cast<std::uint32_t>(k));
+  const __amdgpu_buffer_rsrc_t x_buffer =
+      vx::q8::BufferOf(x, 4U * static_cast<std::uint32_t>(t) * static_cast<std::uint32_t>(k));
+  const std::uint32_t w_at = 4U * static_cast<std::uint32_t>((n0 + r) * k + 4 * g);
+  std::uint32_t x_at[MT];
+  bool row_ok[MT];
+#pragma unroll
+  for (int m = 0; m < MT; ++m) {
+    row_ok[m] = 16 * m + r < t;
+    x_at[m] = 4U * static_cast<std::uint32_t>((16 * m + r) * k + 4 * g);
+  }
+  F32x4 acc[MT];
+#pragma unroll
+  for (int m = 0; m < MT; ++m)
+    acc[m] = F32x4{0.0F, 0.0F, 0.0F, 0.0F};
+  const int groups = k / 16;
+  constexpr int kAhead = 4;
+  for (int base = wave; base < groups; base += kF32Waves * kAhead) {
+    float4 wv[kAhead];
+    float4 xv[kAhead][MT];
+#pragma unroll
+    for (int a = 0; a < kAhead; ++a) {
+      const int group = base + a * kF32Waves;
+      const bool ok = group < groups;
+      wv[a] = __builtin_bit_cast(
+          float4, vx::q8::BufferLoad16(w_buffer, w_at + 64U * static_cast<std::uint32_t>(group),
+                                       ok && column_ok));
+#pragma unroll
+      for (int m = 0; m < MT; ++m)
+        xv[a][m] = __builtin_bit_cast(
+            float4, vx::q8::BufferLoad16(x_buffer,
+                                         x_at[m] + 64U * static_cast<std::uint32_t>(group),
+                                         ok && row_ok[m]));
+    }
+#pragma unroll
+    for (int a = 0; a < kAhead; ++a)
+#pragma unroll
+      for (int m = 0; m < MT; ++m) {
+        acc[m] = __builtin_amdgcn_mfma_f32_16x16x4f32(xv[a][m].x, wv[a].x, acc[m], 0, 0, 0);
+        acc[m] = __builtin_amdgcn_mfma_f32_16x16x4f32(xv[a][m].y, wv[a].y, acc[m], 0, 0, 0);
+        acc[m] = __builtin_amdgcn_mfma_f32_16x16x4f32(xv[a][m].z, wv[a].z, acc[m], 0, 0, 0);
+        acc[m] = __builtin_amdgcn_mfma_f32_16x16x4f32(xv[a][m].w, wv[a].w, acc[m], 0, 0, 0);
+      }
+  }
+#pragma unroll
+  for (int m = 0; m < MT; ++m)
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      reduce[wave][m][i][lane] = acc[m][i];
+  __syncthreads();
+  // Output element e = (m, i, lane): row 16 m + 4 (lane / 16) + i, column
+  // n0 + lane % 16.
+  for (int e = static_cast<int>(threadIdx.x); e < MT * 4 * kWave; e += kF32Waves * kWave) {
+    const int m = e / (4 * kWave);
+    const int i = (e / kWave) % 4;
+    const int l = e % kWave;
+    const int row = 16 * m + 4 * (l / 16) + i;
+    const int column = n0 + l % 16;
+    if (row >= t || column >= n)
+      continue;
+    float total = reduce[0][m][i][l];
+#pragma unroll
+    for (int v = 1; v < kF32Waves; ++v)
+      total += reduce[v][m][i][l];
+    float* target = y + static_cast<std::size_t>(row) * n + column;
+    *target = accumulate != 0 ? *target + total : total;
+  }
+}
+
+/// W2[(r out + o)][k]: k < in the tap r of input channel k, k >= in the tap
+/// r + s of channel k - in, from ConvTranspose1d's [in][out][2 s].
+__global__ void RepackUpKernel(const float* up, float* w2, std::size_t in, std::size_t out,
+                               std::size_t s) {
+  const std::size_t i = static_cast<std::size_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i >= s * out * 2 * in)
+    return;
+  const std::size_t row = i / (2 * in);
+  const std::size_t k = i % (2 * in);
+  const std::size_t r = row / out;
+  const std::size_t o = row % out;
+  const std::size_t channel = k < in ? k : k - in;
+  const std::size_t tap = k < in ? r : r + s;
+  w2[i] = up[(channel * out + o) * 2 * s + tap];
+}
+
+template<typename T>
+int Allocate(T** pointer, std::size_t count, const char* what) {
+  if (hipMalloc(reinterpret_cast<void**>(pointer), std::max<std::size_t>(count, 1) * sizeof(T)) !=
+      hipSuccess)
+    return vx::Fail(VX_HIP_ERROR, what);
+  return VX_OK;
+}
+
+struct Block {
+  std::size_t in = 0;
+  std::size_t out = 0;
+  std::size_t stride = 0;
+  vx_vae_block w{};
+  float* up2 = nullptr;       // [s out][2 in]
+  float* state = nullptr;     // [in]: the last frame's Snake output
+  float* unit_state[3] = {};  // [6 d][out]
+};
+
+struct GraphKey {
+  const float* latents = nullptr;
+  float* samples = nullptr;
+  std::size_t frames = 0;
+  hipStream_t stream = nullptr;
+  bool operator==(const GraphKey& o) const {
+    return latents == o.latents && samples == o.samples && frames == o.frames &&
+           stream == o.stream;
+  }
+};
+
+}  // namespace
+
+struct vx_vae {
+  vx_vae_shape shape{};
+  vx_vae_weights weights{};
+  std::vector<Block> blocks;
+  std::size_t out_channels = 0;
+  std::size_t hop = 1;
+  rocblas_handle blas = nullptr;
+  float* in_state = nullptr;   // [6][latent]
+  float* out_state = nullptr;  // [6][out_channels]
+  float* hidden = nullptr;
+  float* next = nullptr;
+  float* work = nullptr;
+  float* scratch = nullptr;
+  std::size_t capacity_frames = 0;
+  GraphKey graph_key;
+  hipGraphExec_t graph = nullptr;
+  bool seen = false;  // the key has run once eagerly (the library's lazy setup)
+
+  ~vx_vae() {
+    if (graph != nullptr)
+      (void)hipGraphExecDestroy(graph);
+    if (blas != nullptr)
+      (void)rocblas_destroy_handle(blas);
+    for (Block& b : blocks) {
+      (void)hipFree(b.up2);
+      (void)hipFree(b.state);
+      for (float* s : b.unit_state)
+        (void)hipFree(s);
+    }
+    for (void* p : {static_cast<void*>(in_state), static_cast<void*>(out_state),
+                    static_cast<void*>(hidden), static_cast<void*>(next),
+                    static_cast<void*>(work), static_cast<void*>(scratch)})
+      (void)hipFree(p);
+  }
+
+  /// y[t][n] (+)= x[t][k] W[n][k]^T.
+  int Gemm(const float* x, const float* w, float* y, std::size_t t, std::size_t k, std::size_t n,
+           bool accumulate, hipStream_t stream) {
+    if (t <= 32 && k % 16 == 0) {
+      const dim3 grid(static_cast<unsigned>((n + 15) / 16));
+      if (t <= 16)
+        F32SkinnyKernel<1><<<grid, kF32Waves * kWave, 0, stream>>>(
+            x, w, y, static_cast<int>(t), static_cast<int>(k), static_cast<int>(n),
+            accumulate ? 1 : 0);
+      else
+        F32SkinnyKernel<2><<<grid, kF32Waves * kWave, 0, stream>>>(
+            x, w, y, static_cast<int>(t), static_cast<int>(k), static_cast<int>(n),
+            accumulate ? 1 : 0);
+      return VX_OK;
+    }
+    const float alpha = 1.0F;
+    const float beta = accumulate ? 1.0F : 0.0F;
+    if (rocblas_sgemm(blas, rocblas_operation_transpose, rocblas_operation_none,
+                      static_cast<rocblas_int>(n), static_cast<rocblas_int>(t),
+                      static_cast<rocblas_int>(k), &alpha, w, static_cast<rocblas_int>(k), x,
+                      static_cast<rocblas_int>(k), &beta, y,
+                      static_cast<rocblas_int>(n)) != rocblas_status_success)
+      return vx::Fail(VX_HIP_ERROR, "vx_vae_decode: rocblas_sgemm");
+    return VX_OK;
+  }
+
+  /// Buffers for chunks of `frames` latent frames.
+  int Reserve(std::size_t frames) {
+    if (frames <= capacity_frames)
+      return VX_OK;
+    std::size_t widest = frames * std::max(shape.latent_dim, shape.decoder_dim);
+    std::size_t t = frames;
+    for (const Block& b : blocks) {
+      widest = std::max(widest, t * 2 * b.in);
+      t *= b.stride;
+      widest = std::max(widest, t * b.out + 54 * b.out);
+    }
+    widest = std::max(widest, (t + kTaps) * out_channels);
+    for (float** p : {&hidden, &next, &work, &scratch}) {
+      if (*p != nullptr)
+        (void)hipFree(*p);
+      *p = nullptr;
+      VX_TRY(Allocate(p, widest + (kTaps - 1) * shape.latent_dim, "vx_vae: hipMalloc"));
+    }
+    capacity_frames = frames;
+    if (graph != nullptr) {
+      (void)hipGraphExecDestroy(graph);
+      graph = nullptr;
+      seen = false;
+    }
+    return VX_OK;
+  }
+
+  int Launch(const float* latents, std::size_t frames, float* samples, hipStream_t stream) {
+    VX_TRY(rocblas_set_stream(blas, stream) == rocblas_status_success
+               ? VX_OK
+               : vx::Fail(VX_HIP_ERROR, "vx_vae_decode: rocblas_set_stream"));
+    const std::size_t latent = shape.latent_dim;
+    // The residual stream and the transposed convolutions' outputs trade
+    // buffers block by block (locals: every call starts from the same two).
+    float* stream_rows = hidden;
+    float* next_rows = next;
+    std::size_t t = frames;
+    StageKernel<<<Blocks((kTaps - 1 + t) * latent), kThreads, 0, stream>>>(in_state, latents,
+                                                                          work, t, latent);
+    DepthwiseKernel<<<Blocks(std::max(t, std::size_t{kTaps - 1}) * latent), kThreads, 0,
+                      stream>>>(work, weights.in_depthwise, weights.in_depthwise_bias, nullptr,
+                                scratch, in_state, t, latent, 1);
+    VX_TRY(Gemm(scratch, weights.in_pointwise, stream_rows, t, latent, shape.decoder_dim, false,
+                stream));
+    const float* pending = weights.in_pointwise_bias;
+    for (Block& b : blocks) {
+      BlockInputKernel<<<Blocks(t * b.in), kThreads, 0, stream>>>(
+          stream_rows, pending, b.w.scale, b.w.bias, b.w.alpha, work, b.state, t, b.in);
+      VX_TRY(Gemm(work, b.up2, next_rows, t, 2 * b.in, b.stride * b.out, false, stream));
+      std::swap(stream_rows, next_rows);
+      pending = b.w.up_bias;
+      t *= b.stride;
+      const std::size_t c = b.out;
+      for (int u = 0; u < 3; ++u) {
+        const vx_vae_unit& unit = b.w.units[u];
+        const int d = kDilations[u];
+        const std::size_t rows = static_cast<std::size_t>(kTaps - 1) * d;
+        UnitInputKernel<<<Blocks(std::max(t, rows) * c), kThreads, 0, stream>>>(
+            stream_rows, pending, unit.alpha_in, b.unit_state[u], work, t, c, d);
+        DepthwiseKernel<<<Blocks(std::max(t, rows) * c), kThreads, 0, stream>>>(
+            work, unit.depthwise, unit.depthwise_bias, unit.alpha_out, scratch,
+            b.unit_state[u], t, c, d);
+        VX_TRY(Gemm(scratch, unit.pointwise, stream_rows, t, c, c, true, stream));
+        pending = unit.pointwise_bias;
+      }
+    }
+    const std::size_t c = out_channels;
+    OutputInputKernel<<<Blocks(std::max(t, std::size_t{kTaps - 1}) * c), kThreads, 0, stream>>>(
+        stream_rows, pending, weights.out_alpha, out_state, work, t, c);
+    ToMonoKernel<<<static_cast<unsigned>((t + 3) / 4), kThreads, 0, stream>>>(
+        work, weights.out_conv, weights.out_bias, samples, out_state, t, c);
+    return vx::LaunchStatus("vx_vae_decode");
+  }
+};
+
+namespace {
+
+int CheckUnit(const vx_vae_unit& u) {
+  return u.alpha_in && u.depthwise && u.depthwise_bias && u.alpha_out && u.pointwise &&
+                 u.pointwise_bias
+             ? VX_OK
+             : vx::Fail(VX_BAD_ARG, "vx_vae_create: null unit weights");
+}
+
+}  // namespace
+
+extern "C" {
+
+int vx_vae_create(vx_vae** vae, const vx_vae_shape* shape, const vx_vae_weights* weights) {
+  if (vae == nullptr || shape == nullptr || weights == nullptr)
+    return vx::Fail(VX_BAD_ARG, "vx_vae_create: null argument");
+  *vae = nullptr;
+  if (shape->latent_dim == 0 || shape->decoder_dim == 0 || shape->rate_count == 0 ||
+      shape->rate_count > 8 || (shape->decoder_dim >> shape->rate_count) == 0 ||
+      shape->decoder_dim % (std::size_t{1} << shape->rate_count) != 0)
+    return vx::Fail(VX_BAD_ARG, "vx_vae_create: bad shape");
+  if (weights->blocks == nullptr || weights->in_depthwise == nullptr ||
+      weights->in_depthwise_bias == nullptr || weights->in_pointwise == nullptr ||
+      weights->in_pointwise_bias == nullptr || weights->out_alpha == nullptr ||
+      weights->out_conv == nullptr)
+    return vx::Fail(VX_BAD_ARG, "vx_vae_create: null weights");
+  for (std::size_t b = 0; b < shape->rate_count; ++b) {
+    const vx_vae_block& block = weights->blocks[b];
+    if (shape->rates[b] == 0 || !block.scale || !block.bias || !block.alpha || !block.up ||
+        !block.up_bias)
+      return vx::Fail(VX_BAD_ARG, "vx_vae_create: null block weights or zero rate");
+    for (const vx_vae_unit& u : block.units)
+      VX_TRY(CheckUnit(u));
+  }
+  auto* created = new vx_vae();
+  created->shape = *shape;
+  created->weights = *weights;
+  created->weights.blocks = nullptr;
+  int status = VX_OK;
+  std::size_t c = shape->decoder_dim;
+  for (std::size_t b = 0; b < shape->rate_count && status == VX_OK; ++b) {
+    Block block;
+    block.in = c;
+    block.out = c / 2;
+    block.stride = shape->rates[b];
+    block.w = weights->blocks[b];
+    created->hop *= block.stride;
+    status = Allocate(&block.up2, block.stride * block.out * 2 * block.in, "vx_vae: hipMalloc");
+    if (status == VX_OK)
+      status = Allocate(&block.state, block.in, "vx_vae: hipMalloc");
+    for (int u = 0; u < 3 && status == VX_OK; ++u)
+      status = Allocate(&block.unit_state[u],
+                        static_cast<std::size_t>(kTaps - 1) * kDilations[u] * block.out,
+                        "vx_vae: hipMalloc");
+    if (status == VX_OK) {
+      const std::size_t count = block.stride * block.out * 2 * block.in;
+      RepackUpKernel<<<Blocks(count), kThreads>>>(block.w.up, block.up2, block.in, block.out,
+                                                  block.stride);
+      status = vx::LaunchStatus("vx_vae_create");
+    }
+    created->blocks.push_back(block);
+    c /= 2;
+  }
+  created->out_channels = c;
+  if (status == VX_OK)
+    status = Allocate(&created->in_state, (kTaps - 1) * shape->latent_dim, "vx_vae: hipMalloc");
+  if (status == VX_OK)
+    status = Allocate(&created->out_state, (kTaps - 1) * c, "vx_vae: hipMalloc");
+  if (status == VX_OK && rocblas_create_handle(&created->blas) != rocblas_status_success)
+    status = vx::Fail(VX_HIP_ERROR, "vx_vae_create: rocblas_create_handle");
+  if (status == VX_OK && hipDeviceSynchronize() != hipSuccess)
+    status = vx::Fail(VX_HIP_ERROR, "vx_vae_create: repack");
+  if (status != VX_OK) {
+    delete created;
+    return status;
+  }
+  *vae = created;
+  return vx_vae_reset(created, nullptr);
+}
+
+void vx_vae_destroy(vx_vae* vae) { delete vae; }
+
+int vx_vae_reset(vx_vae* vae, void* stream) {
+  if (vae == nullptr)
+    return vx::Fail(VX_BAD_ARG, "vx_vae_reset: null handle");
+  hipStream_t s = vx::Stream(stream);
+  const auto clear = [&](float* p, std::size_t count) {
+    return hipMemsetAsync(p, 0, count * sizeof(float), s) == hipSuccess;
+  };
+  bool ok = clear(vae->in_state, (kTaps - 1) * vae->shape.latent_dim) &&
+            clear(vae->out_state, (kTaps - 1) * vae->out_channels);
+  for (Block& b : vae->blocks) {
+    ok = ok && clear(b.state, b.in);
+    for (int u = 0; u < 3; ++u)
+      ok = ok && clear(b.unit_state[u], static_cast<std::size_t>(kTaps - 1) * kDilations[u] * b.out);
+  }
+  if (!ok)
+    return vx::Fail(VX_HIP_ERROR, "vx_vae_reset: hipMemsetAsync");
+  return vx::Succeed();
+}
+
+size_t vx_vae_hop(const vx_vae* vae) { return vae == nullptr ? 0 : vae->hop; }
+
+int vx_vae_decode(vx_vae* vae, const float* latents, size_t frames, float* samples,
+                  void* stream) {
+  if (vae == nullptr || latents == nullptr || samples == nullptr)
+    return vx::Fail(VX_BAD_ARG, "vx_vae_decode: null argument");
+  if (frames == 0)
+    return VX_OK;
+  if (frames > (1U << 16))
+    return vx::Fail(VX_BAD_ARG, "vx_vae_decode: too many frames in one chunk");
+  hipStream_t s = vx::Stream(stream);
+  VX_TRY(vae->Reserve(frames));
+  GraphKey key{latents, samples, frames, s};
+  hipStreamCaptureStatus capturing = hipStreamCaptureStatusNone;
+  if (s != nullptr)
+    VX_HIP(hipStreamIsCapturing(s, &capturing), "vx_vae_decode: capture status");
+  if (s == nullptr || capturing != hipStreamCaptureStatusNone || frames > kMaxGraphFrames)
+    return vae->Launch(latents, frames, samples, s);
+  if (!(vae->graph_key == key)) {
+    if (vae->graph != nullptr)
+      (void)hipGraphExecDestroy(vae->graph);
+    vae->graph = nullptr;
+    vae->graph_key = key;
+    vae->seen = false;
+  }
+  if (vae->graph == nullptr) {
+    if (!vae->seen) {  // the first call of a key runs eagerly
+      vae->seen = true;
+      return vae->Launch(latents, frames, samples, s);
+    }
+    VX_HIP(hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal),
+           "vx_vae_decode: begin capture");
+    const int status = vae->Launch(latents, frames, samples, s);
+    hipGraph_t captured = nullptr;
+    const hipError_t ended = hipStreamEndCapture(s, &captured);
+    if (status != VX_OK) {
+      if (captured != nullptr)
+        (void)hipGraphDestroy(captured);
+      return status;
+    }
+    if (ended != hipSuccess)
+      return vx::FailHip(ended, "vx_vae_decode: end capture");
+    const hipError_t made = hipGraphInstantiate(&vae->graph, captured, nullptr, nullptr, 0);
+    (void)hipGraphDestroy(captured);
+    if (made != hipSuccess) {
+      vae->graph = nullptr;
+      return vx::FailHip(made, "vx_vae_decode: instantiate");
+    }
+  }
+  VX_HIP(hipGraphLaunch(vae->graph, s), "vx_vae_decode: graph launch");
+  return vx::Succeed();
+}
+
+}  // extern "C"

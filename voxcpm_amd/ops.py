@@ -13,13 +13,14 @@ import torch
 
 from . import synth
 from ._lib import (VX_WEIGHTS_BF16, VX_WEIGHTS_Q8_0, DitLayer, DitProjection, DitShape,
-                   DitWeights, StackShape, StackWeights, check, lib)
+                   DitWeights, StackShape, StackWeights, VaeBlock, VaeShape, VaeUnit,
+                   VaeWeights, check, lib)
 
 __all__ = [
     "Scratch", "Dit", "q8_pack", "q8_unpack_blocks", "q8_unpack_bf16",
     "q8_linear", "q8_linear_bf16", "q8_plan", "bf16_pack", "bf16_unpack", "bf16_linear",
     "bf16_linear_rows", "stream_read", "euler_schedule", "rope_table", "Stack",
-    "split_attention", "Gguf",
+    "split_attention", "Gguf", "Vae",
 ]
 
 
@@ -516,3 +517,66 @@ class Gguf:
         if status != 0:
             raise VxError(status, lib().vx_gguf_last_error().decode())
         return packed
+
+
+class Vae:
+    """vx_vae (AudioVAE V2's streaming decoder) over device copies of
+    float32 decoder weights (synth.VaeWeightsHost; numpy arrays or device
+    tensors)."""
+
+    def __init__(self, weights, device=None, stream=None):
+        self.config = config = weights.config
+        t = weights.tensors
+        device = _device(device)
+        self._keep = []
+
+        def up(array) -> int:
+            tensor = array.to(device) if isinstance(array, torch.Tensor) else \
+                torch.from_numpy(np.ascontiguousarray(array, dtype=np.float32)).to(device)
+            self._keep.append(tensor)
+            return tensor.data_ptr()
+
+        blocks = (VaeBlock * len(t["blocks"]))()
+        for i, b in enumerate(t["blocks"]):
+            units = (VaeUnit * 3)()
+            for u, unit in enumerate(b["units"]):
+                units[u] = VaeUnit(*(up(unit[n]) for n in (
+                    "alpha_in", "depthwise", "depthwise_bias", "alpha_out", "pointwise",
+                    "pointwise_bias")))
+            blocks[i] = VaeBlock(up(b["scale"]), up(b["bias"]), up(b["alpha"]), up(b["up"]),
+                                 up(b["up_bias"]), units)
+        self._blocks = blocks
+        rates = (ctypes.c_size_t * 8)(*config.rates)
+        self._shape = VaeShape(config.latent, config.decoder_dim, len(config.rates), rates)
+        self._weights = VaeWeights(up(t["in_depthwise"]), up(t["in_depthwise_bias"]),
+                                   up(t["in_pointwise"]), up(t["in_pointwise_bias"]), blocks,
+                                   up(t["out_alpha"]), up(t["out_conv"]), t["out_bias"])
+        torch.cuda.synchronize(device)
+        handle = ctypes.c_void_p()
+        check(lib().vx_vae_create(ctypes.byref(handle), ctypes.byref(self._shape),
+                                  ctypes.byref(self._weights)))
+        self.handle = handle
+        self.device = device
+        self.hop = lib().vx_vae_hop(handle)
+
+    def close(self) -> None:
+        if getattr(self, "handle", None):
+            lib().vx_vae_destroy(self.handle)
+            self.handle = ctypes.c_void_p()
+
+    def __del__(self):
+        self.close()
+
+    def reset(self, stream=None) -> None:
+        check(lib().vx_vae_reset(self.handle, _stream(stream)))
+
+    def decode(self, latents: torch.Tensor, samples: torch.Tensor | None = None,
+               stream=None) -> torch.Tensor:
+        """latents float32 [frames][latent] on the device -> samples
+        [frames * hop], continuing the stream."""
+        frames = latents.shape[0]
+        if samples is None:
+            samples = torch.empty(frames * self.hop, dtype=torch.float32, device=latents.device)
+        check(lib().vx_vae_decode(self.handle, _ptr(latents), frames, _ptr(samples),
+                                  _stream(stream)))
+        return samples

@@ -301,3 +301,73 @@ def stack_weights(config: StackConfig, seed: int) -> StackWeightsHost:
             "down": q8_blocks(rng, h, config.ffn),
         })
     return StackWeightsHost(config, layers, bf16_vector(rng, h, 1.0, 0.02))
+
+
+@dataclasses.dataclass(frozen=True)
+class VaeConfig:
+    """AudioVAE V2's decoder shape (AudioVaeConfig, config.hpp:55-72)."""
+    latent: int = 64
+    decoder_dim: int = 2048
+    rates: tuple = (8, 6, 5, 2, 2, 2)
+
+    @property
+    def hop(self) -> int:
+        return int(np.prod(self.rates))
+
+    def channels(self, block: int) -> tuple[int, int]:
+        """(in, out) channels of decoder block `block`."""
+        c = self.decoder_dim >> block
+        return c, c // 2
+
+
+# VoxCPM2's AudioVAE (tests/config_samples.hpp of the reference): latent 64,
+# decoder 2048 channels, rates 8 6 5 2 2 2 (1920 samples per latent frame at
+# 48 kHz).
+VOXCPM2_VAE = VaeConfig()
+
+
+@dataclasses.dataclass
+class VaeWeightsHost:
+    """float32 decoder weights in PyTorch's layouts, weight norm folded;
+    blocks: dicts scale, bias, alpha, up [in][out][2s], up_bias, units
+    (dicts alpha_in, depthwise [c][7], depthwise_bias, alpha_out,
+    pointwise [c][c], pointwise_bias)."""
+    config: VaeConfig
+    tensors: dict
+
+
+def vae_weights(config: VaeConfig, seed: int) -> VaeWeightsHost:
+    """Random decoder weights scaled by 1/sqrt(fan-in) (activations stay
+    O(1) through the blocks); Snake alphas 1 + N(0, 0.1) kept positive."""
+    rng = Rng(seed, 5)
+
+    def normal(shape, std):
+        count = int(np.prod(shape))
+        return (rng.normal(count) * std).astype(np.float32).reshape(shape)
+
+    def alpha(c):
+        return np.abs(1.0 + normal((c,), 0.1)).astype(np.float32) + 0.05
+
+    t = {"in_depthwise": normal((config.latent, 7), 1 / np.sqrt(7)),
+         "in_depthwise_bias": normal((config.latent,), 0.02),
+         "in_pointwise": normal((config.decoder_dim, config.latent), 1 / np.sqrt(config.latent)),
+         "in_pointwise_bias": normal((config.decoder_dim,), 0.02), "blocks": []}
+    for b, s in enumerate(config.rates):
+        c_in, c_out = config.channels(b)
+        units = []
+        for _ in range(3):
+            units.append({"alpha_in": alpha(c_out),
+                          "depthwise": normal((c_out, 7), 1 / np.sqrt(7)),
+                          "depthwise_bias": normal((c_out,), 0.02),
+                          "alpha_out": alpha(c_out),
+                          "pointwise": normal((c_out, c_out), 0.5 / np.sqrt(c_out)),
+                          "pointwise_bias": normal((c_out,), 0.02)})
+        t["blocks"].append({"stride": s, "scale": 1.0 + normal((c_in,), 0.05),
+                            "bias": normal((c_in,), 0.05), "alpha": alpha(c_in),
+                            "up": normal((c_in, c_out, 2 * s), 1 / np.sqrt(2 * c_in)),
+                            "up_bias": normal((c_out,), 0.02), "units": units})
+    c_last = config.channels(len(config.rates) - 1)[1]
+    t["out_alpha"] = alpha(c_last)
+    t["out_conv"] = normal((c_last, 7), 1 / np.sqrt(7 * c_last))
+    t["out_bias"] = float(normal((1,), 0.02)[0])
+    return VaeWeightsHost(config, t)
