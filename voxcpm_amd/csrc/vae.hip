@@ -12,11 +12,11 @@
 // Each bias is applied by the next elementwise kernel as it reads the
 // stream; each state is filled by the kernel that first reads it and
 // refreshed by a later kernel that does not, so no copies remain. The
-// products are plain float32 GEMMs (rocBLAS, as the reference calls
-// hipblasSgemm) except those of up to 32 rows (the first blocks, whose
-// weights are most of the bytes), which take a float32 MFMA kernel reading
-// the weights once; up to 16 latent frames per chunk the launches replay
-// as one HIP graph.
+// products (the reference calls hipblasSgemm) take a float32 MFMA kernel
+// over 16-column, 32-row tiles that reads the weights in place; a product
+// whose tiles would re-read over 32 MiB of activations between them goes
+// to rocBLAS. Up to 16 latent frames per chunk the launches replay as one
+// HIP graph.
 #include <hip/hip_runtime.h>
 #include <rocblas/rocblas.h>
 
@@ -164,28 +164,32 @@ __global__ void ToMonoKernel(const float* work, const float* w, float b, float* 
 
 // ---- float32 products of few rows ------------------------------------------
 //
-// y[t][n] (+)= x[t][k] W[n][k]^T for t <= 32 (the first blocks: 4 and 32
-// frames per patch) on v_mfma_f32_16x16x4_f32, float32 throughout. A
-// workgroup owns 16 columns of W; its 16 waves split k in groups of 16.
-// Within a group lane L (r = L % 16, g = L / 16) loads W[n0 + r][k0 + 4 g
-// .. + 3] and x[16 m + r][k0 + 4 g .. + 3] as float4 and step s of four
-// multiplies the k-slots {k0 + 4 g + s}: the weights are read in place, 64
-// contiguous bytes per row per load. The waves' sums meet in LDS in wave
-// order.
+// y[t][n] (+)= x[t][k] W[n][k]^T on v_mfma_f32_16x16x4_f32, float32
+// throughout. A workgroup owns 16 columns of W and a block of 16 MT rows
+// (grid y: the row blocks); its W waves split k in groups of 16. Within a
+// group lane L (r = L % 16, g = L / 16) loads W[n0 + r][k0 + 4 g .. + 3]
+// and x[16 m + r][k0 + 4 g .. + 3] as float4 and step s of four multiplies
+// the k-slots {k0 + 4 g + s}: the weights are read in place, 64 contiguous
+// bytes per row per load. The waves' sums meet in LDS in wave order.
 
-constexpr int kF32Waves = 16;
+constexpr int kF32Waves = 16;  // most waves per workgroup
 typedef float F32x4 __attribute__((ext_vector_type(4)));
 
-template<int MT>
-__global__ __launch_bounds__(kF32Waves * kWave) void F32SkinnyKernel(
+template<int MT, int W>
+__global__ __launch_bounds__(W * kWave) void F32SkinnyKernel(
     const float* x, const float* w, float* y, int t, int k, int n, int accumulate) {
-  __shared__ float reduce[kF32Waves][MT][4][kWave];
+  __shared__ float reduce[W][MT][4][kWave];
   const int lane = static_cast<int>(threadIdx.x) % kWave;
   const int wave = static_cast<int>(threadIdx.x) / kWave;
   const int r = lane % 16;
   const int g = lane / 16;
   const int n0 = 16 * static_cast<int>(blockIdx.x);
   const bool column_ok = n0 + r < n;
+  // This workgroup's rows: x and y from row0 on, t rows of them.
+  const int row0 = 16 * MT * static_cast<int>(blockIdx.y);
+  x += static_cast<std::size_t>(row0) * k;
+  y += static_cast<std::size_t>(row0) * n;
+  t = min(t - row0, 16 * MT);
   // Buffer loads: masked lanes read zero without a branch, so a wave's
   // loads stay in flight together.
   const __amdgpu_buffer_rsrc_t w_buffer =
@@ -200,18 +204,40 @@ __global__ __launch_bounds__(kF32Waves * kWave) void F32SkinnyKernel(
     row_ok[m] = 16 * m + r < t;
     x_at[m] = 4U * static_cast<std::uint32_t>((16 * m + r) * k + 4 * g);
   }
+  // Output element e = (m, i, lane): row 16 m + 4 (lane / 16) + i, column
+  // n0 + lane % 16; thread j-th element e = threadIdx.x + j W 64. With
+  // accumulate, y's current values are loaded here beside the operands, not
+  // after the products.
+  constexpr int kOut = (MT * 4 + W - 1) / W;
+  const __amdgpu_buffer_rsrc_t y_buffer =
+      vx::q8::BufferOf(y, 4U * static_cast<std::uint32_t>(t) * static_cast<std::uint32_t>(n));
+  int out_row[kOut];
+  int out_column[kOut];
+  float prior[kOut];
+#pragma unroll
+  for (int j = 0; j < kOut; ++j) {
+    const int e = static_cast<int>(threadIdx.x) + j * W * kWave;
+    const int l = e % kWave;
+    out_row[j] = e < MT * 4 * kWave ? 16 * (e / (4 * kWave)) + 4 * (l / 16) + (e / kWave) % 4 : t;
+    out_column[j] = n0 + l % 16;
+    const bool keep = accumulate != 0 && out_row[j] < t && out_column[j] < n;
+    prior[j] = __builtin_bit_cast(
+        float, vx::q8::BufferLoad4(
+                   y_buffer, 4U * static_cast<std::uint32_t>(out_row[j] * n + out_column[j]),
+                   keep));
+  }
   F32x4 acc[MT];
 #pragma unroll
   for (int m = 0; m < MT; ++m)
     acc[m] = F32x4{0.0F, 0.0F, 0.0F, 0.0F};
   const int groups = k / 16;
   constexpr int kAhead = 4;
-  for (int base = wave; base < groups; base += kF32Waves * kAhead) {
+  for (int base = wave; base < groups; base += W * kAhead) {
     float4 wv[kAhead];
     float4 xv[kAhead][MT];
 #pragma unroll
     for (int a = 0; a < kAhead; ++a) {
-      const int group = base + a * kF32Waves;
+      const int group = base + a * W;
       const bool ok = group < groups;
       wv[a] = __builtin_bit_cast(
           float4, vx::q8::BufferLoad16(w_buffer, w_at + 64U * static_cast<std::uint32_t>(group),
@@ -239,22 +265,20 @@ __global__ __launch_bounds__(kF32Waves * kWave) void F32SkinnyKernel(
     for (int i = 0; i < 4; ++i)
       reduce[wave][m][i][lane] = acc[m][i];
   __syncthreads();
-  // Output element e = (m, i, lane): row 16 m + 4 (lane / 16) + i, column
-  // n0 + lane % 16.
-  for (int e = static_cast<int>(threadIdx.x); e < MT * 4 * kWave; e += kF32Waves * kWave) {
+#pragma unroll
+  for (int j = 0; j < kOut; ++j) {
+    if (out_row[j] >= t || out_column[j] >= n)
+      continue;
+    const int e = static_cast<int>(threadIdx.x) + j * W * kWave;
     const int m = e / (4 * kWave);
     const int i = (e / kWave) % 4;
     const int l = e % kWave;
-    const int row = 16 * m + 4 * (l / 16) + i;
-    const int column = n0 + l % 16;
-    if (row >= t || column >= n)
-      continue;
     float total = reduce[0][m][i][l];
 #pragma unroll
-    for (int v = 1; v < kF32Waves; ++v)
+    for (int v = 1; v < W; ++v)
       total += reduce[v][m][i][l];
-    float* target = y + static_cast<std::size_t>(row) * n + column;
-    *target = accumulate != 0 ? *target + total : total;
+    y[static_cast<std::size_t>(out_row[j]) * n + out_column[j]] =
+        accumulate != 0 ? prior[j] + total : total;
   }
 }
 
@@ -340,19 +364,40 @@ struct vx_vae {
       (void)hipFree(p);
   }
 
-  /// y[t][n] (+)= x[t][k] W[n][k]^T.
+  /// y[t][n] (+)= x[t][k] W[n][k]^T. F32SkinnyKernel where k is whole
+  /// groups of 16 and its workgroups re-read at most 32 MiB of x between
+  /// them (one x read per 16 columns): every product of VoxCPM2's decoder
+  /// but block 2's transposed convolution (192 rows x 2048 over 1280
+  /// columns), which rocBLAS tiles in both dimensions.
   int Gemm(const float* x, const float* w, float* y, std::size_t t, std::size_t k, std::size_t n,
            bool accumulate, hipStream_t stream) {
-    if (t <= 32 && k % 16 == 0) {
-      const dim3 grid(static_cast<unsigned>((n + 15) / 16));
-      if (t <= 16)
-        F32SkinnyKernel<1><<<grid, kF32Waves * kWave, 0, stream>>>(
-            x, w, y, static_cast<int>(t), static_cast<int>(k), static_cast<int>(n),
-            accumulate ? 1 : 0);
-      else
-        F32SkinnyKernel<2><<<grid, kF32Waves * kWave, 0, stream>>>(
-            x, w, y, static_cast<int>(t), static_cast<int>(k), static_cast<int>(n),
-            accumulate ? 1 : 0);
+    const std::size_t x_reads = t * k * sizeof(float) * ((n + 15) / 16);
+    if (k % 16 == 0 && n * k * sizeof(float) < (std::size_t{1} << 32) &&
+        (t <= 32 || x_reads <= (std::size_t{32} << 20))) {
+      const int mt = t <= 16 ? 1 : 2;
+      const std::size_t groups = k / 16;
+      int waves = kF32Waves;  // at least two groups of k per wave
+      while (waves > 1 && groups < 2 * static_cast<std::size_t>(waves))
+        waves /= 2;
+      const dim3 grid(static_cast<unsigned>((n + 15) / 16),
+                      static_cast<unsigned>((t + 16 * mt - 1) / (16 * mt)));
+      const auto launch = [&](auto kernel) {
+        kernel<<<grid, waves * kWave, 0, stream>>>(x, w, y, static_cast<int>(t),
+                                                   static_cast<int>(k), static_cast<int>(n),
+                                                   accumulate ? 1 : 0);
+      };
+      switch (mt * 100 + waves) {
+        case 101: launch(F32SkinnyKernel<1, 1>); break;
+        case 102: launch(F32SkinnyKernel<1, 2>); break;
+        case 104: launch(F32SkinnyKernel<1, 4>); break;
+        case 108: launch(F32SkinnyKernel<1, 8>); break;
+        case 116: launch(F32SkinnyKernel<1, 16>); break;
+        case 201: launch(F32SkinnyKernel<2, 1>); break;
+        case 202: launch(F32SkinnyKernel<2, 2>); break;
+        case 204: launch(F32SkinnyKernel<2, 4>); break;
+        case 208: launch(F32SkinnyKernel<2, 8>); break;
+        default: launch(F32SkinnyKernel<2, 16>); break;
+      }
       return VX_OK;
     }
     const float alpha = 1.0F;
