@@ -10,8 +10,10 @@
 // depthwise conv fused with the second Snake, pointwise product added into
 // the stream), then Snake and the 7-tap convolution to mono with tanh.
 // Each bias is applied by the next elementwise kernel as it reads the
-// stream; each state is filled by the kernel that first reads it and
-// refreshed by a later kernel that does not, so no copies remain. The
+// stream, or by the product itself where the product's epilogue also makes
+// the next residual unit's input window (bias, Snake, history); each state
+// is filled by the kernel that first reads it and refreshed by a later
+// kernel that does not, so no copies remain. The
 // products (the reference calls hipblasSgemm) take a float32 MFMA kernel
 // over 16-column, 32-row tiles that reads the weights in place; a product
 // whose tiles would re-read over 32 MiB of activations between them goes
@@ -175,9 +177,26 @@ __global__ void ToMonoKernel(const float* work, const float* w, float b, float* 
 constexpr int kF32Waves = 16;  // most waves per workgroup
 typedef float F32x4 __attribute__((ext_vector_type(4)));
 
+/// A residual unit's input made in a product's epilogue (what
+/// UnitInputKernel does after a product it cannot see into). y's linear
+/// element i is (frame i / channels, channel i % channels), also for a
+/// transposed convolution's [t][stride channels] output: v = y[i] +
+/// bias[channel], y[i] = v, window[head + i] = Snake(v, alpha[channel]), and
+/// window[0 .. head) = state (copied by the first row block's workgroups).
+/// Unused when window is null.
+struct UnitWindow {
+  const float* bias = nullptr;
+  const float* alpha = nullptr;
+  float* window = nullptr;
+  const float* state = nullptr;
+  int head = 0;  // floats of history: 6 d rows of `channels`
+  int channels = 1;
+};
+
 template<int MT, int W>
 __global__ __launch_bounds__(W * kWave) void F32SkinnyKernel(
-    const float* x, const float* w, float* y, int t, int k, int n, int accumulate) {
+    const float* x, const float* w, float* y, int t, int k, int n, int accumulate,
+    UnitWindow unit) {
   __shared__ float reduce[W][MT][4][kWave];
   const int lane = static_cast<int>(threadIdx.x) % kWave;
   const int wave = static_cast<int>(threadIdx.x) / kWave;
@@ -187,6 +206,13 @@ __global__ __launch_bounds__(W * kWave) void F32SkinnyKernel(
   const bool column_ok = n0 + r < n;
   // This workgroup's rows: x and y from row0 on, t rows of them.
   const int row0 = 16 * MT * static_cast<int>(blockIdx.y);
+  if (unit.window != nullptr && blockIdx.y == 0)
+    for (int e = static_cast<int>(blockIdx.x * blockDim.x + threadIdx.x); e < unit.head;
+         e += static_cast<int>(gridDim.x * blockDim.x))
+      unit.window[e] = unit.state[e];
+  float* window = unit.window != nullptr
+                      ? unit.window + unit.head + static_cast<std::size_t>(row0) * n
+                      : nullptr;
   x += static_cast<std::size_t>(row0) * k;
   y += static_cast<std::size_t>(row0) * n;
   t = min(t - row0, 16 * MT);
@@ -211,20 +237,32 @@ __global__ __launch_bounds__(W * kWave) void F32SkinnyKernel(
   constexpr int kOut = (MT * 4 + W - 1) / W;
   const __amdgpu_buffer_rsrc_t y_buffer =
       vx::q8::BufferOf(y, 4U * static_cast<std::uint32_t>(t) * static_cast<std::uint32_t>(n));
+  const bool windowed = unit.window != nullptr;
+  const std::uint32_t channel_bytes = 4U * static_cast<std::uint32_t>(unit.channels);
+  const __amdgpu_buffer_rsrc_t bias_buffer =
+      vx::q8::BufferOf(unit.bias, windowed && unit.bias != nullptr ? channel_bytes : 0U);
+  const __amdgpu_buffer_rsrc_t alpha_buffer =
+      vx::q8::BufferOf(unit.alpha, windowed ? channel_bytes : 0U);
   int out_row[kOut];
   int out_column[kOut];
   float prior[kOut];
+  float bias[kOut];
+  float alpha[kOut];
 #pragma unroll
   for (int j = 0; j < kOut; ++j) {
     const int e = static_cast<int>(threadIdx.x) + j * W * kWave;
     const int l = e % kWave;
     out_row[j] = e < MT * 4 * kWave ? 16 * (e / (4 * kWave)) + 4 * (l / 16) + (e / kWave) % 4 : t;
     out_column[j] = n0 + l % 16;
-    const bool keep = accumulate != 0 && out_row[j] < t && out_column[j] < n;
+    const bool live = out_row[j] < t && out_column[j] < n;
     prior[j] = __builtin_bit_cast(
         float, vx::q8::BufferLoad4(
                    y_buffer, 4U * static_cast<std::uint32_t>(out_row[j] * n + out_column[j]),
-                   keep));
+                   live && accumulate != 0));
+    const std::uint32_t at = 4U * static_cast<std::uint32_t>(out_column[j] % unit.channels);
+    bias[j] = __builtin_bit_cast(
+        float, vx::q8::BufferLoad4(bias_buffer, at, live && windowed && unit.bias != nullptr));
+    alpha[j] = __builtin_bit_cast(float, vx::q8::BufferLoad4(alpha_buffer, at, live && windowed));
   }
   F32x4 acc[MT];
 #pragma unroll
@@ -277,8 +315,14 @@ __global__ __launch_bounds__(W * kWave) void F32SkinnyKernel(
 #pragma unroll
     for (int v = 1; v < W; ++v)
       total += reduce[v][m][i][l];
-    y[static_cast<std::size_t>(out_row[j]) * n + out_column[j]] =
-        accumulate != 0 ? prior[j] + total : total;
+    float v = accumulate != 0 ? prior[j] + total : total;
+    const std::size_t at = static_cast<std::size_t>(out_row[j]) * n + out_column[j];
+    if (windowed) {
+      if (unit.bias != nullptr)
+        v += bias[j];
+      window[at] = Snake(v, alpha[j]);
+    }
+    y[at] = v;
   }
 }
 
@@ -369,11 +413,17 @@ struct vx_vae {
   /// them (one x read per 16 columns): every product of VoxCPM2's decoder
   /// but block 2's transposed convolution (192 rows x 2048 over 1280
   /// columns), which rocBLAS tiles in both dimensions.
-  int Gemm(const float* x, const float* w, float* y, std::size_t t, std::size_t k, std::size_t n,
-           bool accumulate, hipStream_t stream) {
+  static bool Skinny(std::size_t t, std::size_t k, std::size_t n) {
     const std::size_t x_reads = t * k * sizeof(float) * ((n + 15) / 16);
-    if (k % 16 == 0 && n * k * sizeof(float) < (std::size_t{1} << 32) &&
-        (t <= 32 || x_reads <= (std::size_t{32} << 20))) {
+    return k % 16 == 0 && n * k * sizeof(float) < (std::size_t{1} << 32) &&
+           (t <= 32 || x_reads <= (std::size_t{32} << 20));
+  }
+
+  /// With `unit.window` set (and Skinny), the product's epilogue also makes
+  /// the next residual unit's input window.
+  int Gemm(const float* x, const float* w, float* y, std::size_t t, std::size_t k, std::size_t n,
+           bool accumulate, hipStream_t stream, const UnitWindow& unit = UnitWindow{}) {
+    if (Skinny(t, k, n)) {
       const int mt = t <= 16 ? 1 : 2;
       const std::size_t groups = k / 16;
       int waves = kF32Waves;  // at least two groups of k per wave
@@ -384,7 +434,7 @@ struct vx_vae {
       const auto launch = [&](auto kernel) {
         kernel<<<grid, waves * kWave, 0, stream>>>(x, w, y, static_cast<int>(t),
                                                    static_cast<int>(k), static_cast<int>(n),
-                                                   accumulate ? 1 : 0);
+                                                   accumulate ? 1 : 0, unit);
       };
       switch (mt * 100 + waves) {
         case 101: launch(F32SkinnyKernel<1, 1>); break;
@@ -459,22 +509,40 @@ struct vx_vae {
     for (Block& b : blocks) {
       BlockInputKernel<<<Blocks(t * b.in), kThreads, 0, stream>>>(
           stream_rows, pending, b.w.scale, b.w.bias, b.w.alpha, work, b.state, t, b.in);
-      VX_TRY(Gemm(work, b.up2, next_rows, t, 2 * b.in, b.stride * b.out, false, stream));
-      std::swap(stream_rows, next_rows);
-      pending = b.w.up_bias;
-      t *= b.stride;
       const std::size_t c = b.out;
+      // Each product's epilogue makes the next unit's window in scratch
+      // (bias added, Snake, history first) where the product is ours;
+      // otherwise UnitInputKernel does, with the bias still pending.
+      const auto window_of = [&](int u, const float* bias) {
+        UnitWindow unit;
+        unit.bias = bias;
+        unit.alpha = b.w.units[u].alpha_in;
+        unit.window = scratch;
+        unit.state = b.unit_state[u];
+        unit.head = (kTaps - 1) * kDilations[u] * static_cast<int>(c);
+        unit.channels = static_cast<int>(c);
+        return unit;
+      };
+      bool windowed = Skinny(t, 2 * b.in, b.stride * c);
+      VX_TRY(Gemm(work, b.up2, next_rows, t, 2 * b.in, b.stride * c, false, stream,
+                  windowed ? window_of(0, b.w.up_bias) : UnitWindow{}));
+      std::swap(stream_rows, next_rows);
+      pending = windowed ? nullptr : b.w.up_bias;
+      t *= b.stride;
       for (int u = 0; u < 3; ++u) {
         const vx_vae_unit& unit = b.w.units[u];
         const int d = kDilations[u];
         const std::size_t rows = static_cast<std::size_t>(kTaps - 1) * d;
-        UnitInputKernel<<<Blocks(std::max(t, rows) * c), kThreads, 0, stream>>>(
-            stream_rows, pending, unit.alpha_in, b.unit_state[u], work, t, c, d);
+        if (!windowed)
+          UnitInputKernel<<<Blocks(std::max(t, rows) * c), kThreads, 0, stream>>>(
+              stream_rows, pending, unit.alpha_in, b.unit_state[u], scratch, t, c, d);
         DepthwiseKernel<<<Blocks(std::max(t, rows) * c), kThreads, 0, stream>>>(
-            work, unit.depthwise, unit.depthwise_bias, unit.alpha_out, scratch,
+            scratch, unit.depthwise, unit.depthwise_bias, unit.alpha_out, work,
             b.unit_state[u], t, c, d);
-        VX_TRY(Gemm(scratch, unit.pointwise, stream_rows, t, c, c, true, stream));
-        pending = unit.pointwise_bias;
+        windowed = u < 2 && Skinny(t, c, c);
+        VX_TRY(Gemm(work, unit.pointwise, stream_rows, t, c, c, true, stream,
+                    windowed ? window_of(u + 1, unit.pointwise_bias) : UnitWindow{}));
+        pending = windowed ? nullptr : unit.pointwise_bias;
       }
     }
     const std::size_t c = out_channels;
