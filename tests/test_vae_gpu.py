@@ -16,14 +16,19 @@ pytestmark = pytest.mark.gpu
 
 BOUND = 2e-3
 
+# "small" and "odd" take channel counts that are not multiples of 16 (8;
+# 24 and 12): their products go to the library GEMM, and the elementwise
+# kernels make the next inputs (unit windows, a block's input, the output
+# window) in place of the products' epilogues.
 CONFIGS = {
     "small": synth.VaeConfig(latent=16, decoder_dim=64, rates=(3, 2, 2)),
+    "odd": synth.VaeConfig(latent=16, decoder_dim=48, rates=(2, 2)),
     "voxcpm2": synth.VOXCPM2_VAE,
 }
 
 
 @pytest.mark.parametrize("name,chunks", [("small", (4, 4, 1)), ("small", (9,)),
-                                         ("voxcpm2", (4, 4))])
+                                         ("odd", (3, 2, 5)), ("voxcpm2", (4, 4))])
 def test_vae_streaming_decode_against_oracle(vx, oracle, cuda, stream, name, chunks):
     config = CONFIGS[name]
     weights = synth.vae_weights(config, 91)

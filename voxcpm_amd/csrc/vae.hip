@@ -65,11 +65,14 @@ __global__ void StageKernel(const float* state, const float* latents, float* wor
 /// state = work's last 6 d rows (this kernel never reads the state).
 __global__ void DepthwiseKernel(const float* work, const float* w, const float* b,
                                 const float* alpha, float* out, float* state, std::size_t t,
-                                std::size_t c, int d) {
+                                std::size_t c, int d, const float* copy_from = nullptr,
+                                float* copy_to = nullptr, std::size_t copy_count = 0) {
   const std::size_t i = static_cast<std::size_t>(blockIdx.x) * blockDim.x + threadIdx.x;
   const std::size_t rows = static_cast<std::size_t>(kTaps - 1) * d;
   if (i < rows * c)
     state[i] = work[t * c + i];
+  if (i < copy_count)  // a refresh for a kernel before this one (the block input's state)
+    copy_to[i] = copy_from[i];
   if (i >= t * c)
     return;
   const std::size_t f = i / c;
@@ -184,6 +187,13 @@ typedef float F32x4 __attribute__((ext_vector_type(4)));
 /// bias[channel], y[i] = v, window[head + i] = Snake(v, alpha[channel]), and
 /// window[0 .. head) = state (copied by the first row block's workgroups).
 /// Unused when window is null.
+///
+/// With `scale` set it makes a decoder block's input instead (what
+/// BlockInputKernel does): u = Snake(v scale + shift, alpha) per frame f
+/// and channel c of a [frames][channels] output, window = x2 [frames][2
+/// channels] with x2[f] = [u(f) | u(f - 1)] and u(-1) = state (copied into
+/// x2[0]'s second half by the first row block's workgroups; a later kernel
+/// refreshes the state from x2's last frame).
 struct UnitWindow {
   const float* bias = nullptr;
   const float* alpha = nullptr;
@@ -191,6 +201,9 @@ struct UnitWindow {
   const float* state = nullptr;
   int head = 0;  // floats of history: 6 d rows of `channels`
   int channels = 1;
+  const float* scale = nullptr;
+  const float* shift = nullptr;
+  int frames = 0;
 };
 
 template<int MT, int W>
@@ -206,11 +219,14 @@ __global__ __launch_bounds__(W * kWave) void F32SkinnyKernel(
   const bool column_ok = n0 + r < n;
   // This workgroup's rows: x and y from row0 on, t rows of them.
   const int row0 = 16 * MT * static_cast<int>(blockIdx.y);
-  if (unit.window != nullptr && blockIdx.y == 0)
+  const bool block_input = unit.scale != nullptr;
+  if (unit.window != nullptr && blockIdx.y == 0) {
+    float* head = unit.window + (block_input ? unit.channels : 0);
     for (int e = static_cast<int>(blockIdx.x * blockDim.x + threadIdx.x); e < unit.head;
          e += static_cast<int>(gridDim.x * blockDim.x))
-      unit.window[e] = unit.state[e];
-  float* window = unit.window != nullptr
+      head[e] = unit.state[e];
+  }
+  float* window = unit.window != nullptr && !block_input
                       ? unit.window + unit.head + static_cast<std::size_t>(row0) * n
                       : nullptr;
   x += static_cast<std::size_t>(row0) * k;
@@ -243,11 +259,17 @@ __global__ __launch_bounds__(W * kWave) void F32SkinnyKernel(
       vx::q8::BufferOf(unit.bias, windowed && unit.bias != nullptr ? channel_bytes : 0U);
   const __amdgpu_buffer_rsrc_t alpha_buffer =
       vx::q8::BufferOf(unit.alpha, windowed ? channel_bytes : 0U);
+  const __amdgpu_buffer_rsrc_t scale_buffer =
+      vx::q8::BufferOf(unit.scale, windowed && block_input ? channel_bytes : 0U);
+  const __amdgpu_buffer_rsrc_t shift_buffer =
+      vx::q8::BufferOf(unit.shift, windowed && block_input ? channel_bytes : 0U);
   int out_row[kOut];
   int out_column[kOut];
   float prior[kOut];
   float bias[kOut];
   float alpha[kOut];
+  float scale[kOut];
+  float shift[kOut];
 #pragma unroll
   for (int j = 0; j < kOut; ++j) {
     const int e = static_cast<int>(threadIdx.x) + j * W * kWave;
@@ -263,6 +285,9 @@ __global__ __launch_bounds__(W * kWave) void F32SkinnyKernel(
     bias[j] = __builtin_bit_cast(
         float, vx::q8::BufferLoad4(bias_buffer, at, live && windowed && unit.bias != nullptr));
     alpha[j] = __builtin_bit_cast(float, vx::q8::BufferLoad4(alpha_buffer, at, live && windowed));
+    const bool block_live = live && windowed && block_input;
+    scale[j] = __builtin_bit_cast(float, vx::q8::BufferLoad4(scale_buffer, at, block_live));
+    shift[j] = __builtin_bit_cast(float, vx::q8::BufferLoad4(shift_buffer, at, block_live));
   }
   F32x4 acc[MT];
 #pragma unroll
@@ -320,7 +345,17 @@ __global__ __launch_bounds__(W * kWave) void F32SkinnyKernel(
     if (windowed) {
       if (unit.bias != nullptr)
         v += bias[j];
-      window[at] = Snake(v, alpha[j]);
+      if (block_input) {
+        // The output is [frames][channels]: frame row0 + row, channel column.
+        const float u = Snake(v * scale[j] + shift[j], alpha[j]);
+        const int frame = row0 + out_row[j];
+        const std::size_t c = static_cast<std::size_t>(unit.channels);
+        unit.window[static_cast<std::size_t>(frame) * 2 * c + out_column[j]] = u;
+        if (frame + 1 < unit.frames)
+          unit.window[static_cast<std::size_t>(frame + 1) * 2 * c + c + out_column[j]] = u;
+      } else {
+        window[at] = Snake(v, alpha[j]);
+      }
     }
     y[at] = v;
   }
@@ -503,53 +538,96 @@ struct vx_vae {
     DepthwiseKernel<<<Blocks(std::max(t, std::size_t{kTaps - 1}) * latent), kThreads, 0,
                       stream>>>(work, weights.in_depthwise, weights.in_depthwise_bias, nullptr,
                                 scratch, in_state, t, latent, 1);
+    // Each product's epilogue makes its consumer's input where the product
+    // is ours: a block's input x2 (in work; unit 0's depthwise kernel then
+    // refreshes the block's state from x2's last frame), a unit's window
+    // (in scratch) or the output window (in scratch). Otherwise the
+    // elementwise kernel does, with the product's bias still pending. The
+    // depthwise outputs go to the stream buffer the block's transposed
+    // convolution left behind.
+    const auto block_input_of = [&](const Block& b, const float* bias) {
+      UnitWindow unit;
+      unit.bias = bias;
+      unit.alpha = b.w.alpha;
+      unit.window = work;
+      unit.state = b.state;
+      unit.head = static_cast<int>(b.in);
+      unit.channels = static_cast<int>(b.in);
+      unit.scale = b.w.scale;
+      unit.shift = b.w.bias;
+      unit.frames = static_cast<int>(t);
+      return unit;
+    };
+    const auto window_of = [&](const float* alpha, float* state, int head_rows, std::size_t c,
+                               const float* bias) {
+      UnitWindow unit;
+      unit.bias = bias;
+      unit.alpha = alpha;
+      unit.window = scratch;
+      unit.state = state;
+      unit.head = head_rows * static_cast<int>(c);
+      unit.channels = static_cast<int>(c);
+      return unit;
+    };
+    // The consumer's input made by the last product, if any.
+    bool made = !blocks.empty() && Skinny(t, latent, shape.decoder_dim);
     VX_TRY(Gemm(scratch, weights.in_pointwise, stream_rows, t, latent, shape.decoder_dim, false,
-                stream));
-    const float* pending = weights.in_pointwise_bias;
-    for (Block& b : blocks) {
-      BlockInputKernel<<<Blocks(t * b.in), kThreads, 0, stream>>>(
-          stream_rows, pending, b.w.scale, b.w.bias, b.w.alpha, work, b.state, t, b.in);
+                stream,
+                made ? block_input_of(blocks.front(), weights.in_pointwise_bias) : UnitWindow{}));
+    const float* pending = made ? nullptr : weights.in_pointwise_bias;
+    for (std::size_t bi = 0; bi < blocks.size(); ++bi) {
+      Block& b = blocks[bi];
+      const bool block_made = made;
+      if (!made)
+        BlockInputKernel<<<Blocks(t * b.in), kThreads, 0, stream>>>(
+            stream_rows, pending, b.w.scale, b.w.bias, b.w.alpha, work, b.state, t, b.in);
+      const std::size_t t_in = t;
       const std::size_t c = b.out;
-      // Each product's epilogue makes the next unit's window in scratch
-      // (bias added, Snake, history first) where the product is ours;
-      // otherwise UnitInputKernel does, with the bias still pending.
-      const auto window_of = [&](int u, const float* bias) {
-        UnitWindow unit;
-        unit.bias = bias;
-        unit.alpha = b.w.units[u].alpha_in;
-        unit.window = scratch;
-        unit.state = b.unit_state[u];
-        unit.head = (kTaps - 1) * kDilations[u] * static_cast<int>(c);
-        unit.channels = static_cast<int>(c);
-        return unit;
-      };
-      bool windowed = Skinny(t, 2 * b.in, b.stride * c);
+      made = Skinny(t, 2 * b.in, b.stride * c);
       VX_TRY(Gemm(work, b.up2, next_rows, t, 2 * b.in, b.stride * c, false, stream,
-                  windowed ? window_of(0, b.w.up_bias) : UnitWindow{}));
+                  made ? window_of(b.w.units[0].alpha_in, b.unit_state[0], kTaps - 1, c,
+                                   b.w.up_bias)
+                       : UnitWindow{}));
       std::swap(stream_rows, next_rows);
-      pending = windowed ? nullptr : b.w.up_bias;
+      pending = made ? nullptr : b.w.up_bias;
       t *= b.stride;
       for (int u = 0; u < 3; ++u) {
         const vx_vae_unit& unit = b.w.units[u];
         const int d = kDilations[u];
         const std::size_t rows = static_cast<std::size_t>(kTaps - 1) * d;
-        if (!windowed)
+        if (!made)
           UnitInputKernel<<<Blocks(std::max(t, rows) * c), kThreads, 0, stream>>>(
               stream_rows, pending, unit.alpha_in, b.unit_state[u], scratch, t, c, d);
+        const bool refresh = u == 0 && block_made;
         DepthwiseKernel<<<Blocks(std::max(t, rows) * c), kThreads, 0, stream>>>(
-            scratch, unit.depthwise, unit.depthwise_bias, unit.alpha_out, work,
-            b.unit_state[u], t, c, d);
-        windowed = u < 2 && Skinny(t, c, c);
-        VX_TRY(Gemm(work, unit.pointwise, stream_rows, t, c, c, true, stream,
-                    windowed ? window_of(u + 1, unit.pointwise_bias) : UnitWindow{}));
-        pending = windowed ? nullptr : unit.pointwise_bias;
+            scratch, unit.depthwise, unit.depthwise_bias, unit.alpha_out, next_rows,
+            b.unit_state[u], t, c, d, refresh ? work + (t_in - 1) * 2 * b.in : nullptr,
+            refresh ? b.state : nullptr, refresh ? b.in : 0);
+        // The next consumer: unit u + 1, the next block's input or the output.
+        UnitWindow next;
+        made = Skinny(t, c, c);
+        if (made && u < 2) {
+          const int dn = kDilations[u + 1];
+          next = window_of(b.w.units[u + 1].alpha_in, b.unit_state[u + 1], (kTaps - 1) * dn, c,
+                           unit.pointwise_bias);
+        } else if (made && bi + 1 < blocks.size()) {
+          next = block_input_of(blocks[bi + 1], unit.pointwise_bias);
+        } else if (made) {
+          next = window_of(weights.out_alpha, out_state, kTaps - 1, c, unit.pointwise_bias);
+        }
+        VX_TRY(Gemm(next_rows, unit.pointwise, stream_rows, t, c, c, true, stream, next));
+        pending = made ? nullptr : unit.pointwise_bias;
       }
     }
     const std::size_t c = out_channels;
-    OutputInputKernel<<<Blocks(std::max(t, std::size_t{kTaps - 1}) * c), kThreads, 0, stream>>>(
-        stream_rows, pending, weights.out_alpha, out_state, work, t, c);
+    float* out_window = scratch;
+    if (!made) {
+      OutputInputKernel<<<Blocks(std::max(t, std::size_t{kTaps - 1}) * c), kThreads, 0,
+                          stream>>>(stream_rows, pending, weights.out_alpha, out_state,
+                                    out_window, t, c);
+    }
     ToMonoKernel<<<static_cast<unsigned>((t + 3) / 4), kThreads, 0, stream>>>(
-        work, weights.out_conv, weights.out_bias, samples, out_state, t, c);
+        out_window, weights.out_conv, weights.out_bias, samples, out_state, t, c);
     return vx::LaunchStatus("vx_vae_decode");
   }
 };
