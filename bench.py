@@ -622,9 +622,9 @@ def cpu_baseline(synth):
             repeats[f"{k}x{n}"] = count
         return total_bytes / total_seconds / 1e9, repeats, total_seconds
 
-    value, repeats, seconds = rate(threads, 2.5, 50)
+    value, repeats, seconds = rate(threads, 3.0, 400)
     log(f"CPU oracle: {value:.2f} GB/s on {threads} threads")
-    single, single_repeats, single_seconds = rate(1, 1.0, 20)
+    single, single_repeats, single_seconds = rate(1, 2.0, 40)
     log(f"CPU oracle: {single:.3f} GB/s on 1 thread")
     return {"value": round(value, 3), "unit": "GB/s", "cores": threads,
             "kind": "port",
