@@ -450,16 +450,21 @@ typedef struct vx_vae vx_vae;
 int vx_vae_create(vx_vae** vae, const vx_vae_shape* shape,
                   const vx_vae_weights* weights);
 void vx_vae_destroy(vx_vae* vae);
-/* AudioVae::Reset: a new stream (zero history). */
+/* AudioVae::Reset: a new stream (zero history), cleared by a kernel (no
+ * memset node when the caller captures it). */
 int vx_vae_reset(vx_vae* vae, void* stream);
 /* Output samples per latent frame (AudioVaeConfig::decode_hop). */
 size_t vx_vae_hop(const vx_vae* vae);
 /* AudioVae::Decode / Enqueue on device data: latents [frames][latent]
  * -> samples [frames * hop] at the output rate, continuing the stream.
  * Chunks of up to 16 frames replay as one HIP graph from their second call
- * with the same buffers. */
+ * with the same buffers. A chunk holds at most vx_vae_max_frames(vae)
+ * frames (VX_BAD_ARG beyond: decode longer audio in several chunks). */
 int vx_vae_decode(vx_vae* vae, const float* latents, size_t frames,
                   float* samples, void* stream);
+/* Most latent frames per vx_vae_decode call (65535 x 32 output samples /
+ * hop: 1092 frames, 43.7 s at 48 kHz, for VoxCPM2's hop of 1920). */
+size_t vx_vae_max_frames(const vx_vae* vae);
 
 /* The rotary table of MiniCPM's LongRoPE on the host, float32 as the
  * reference computes it (transformer.cpp:20-45): [positions][dim], cos in

@@ -10,7 +10,7 @@ import numpy as np
 import pytest
 import torch
 
-from voxcpm_amd import synth
+from voxcpm_amd import _lib, synth
 
 pytestmark = pytest.mark.gpu
 
@@ -70,3 +70,15 @@ def test_vae_graph_replays(vx, oracle, cuda, stream):
         got = samples.cpu().numpy()
         want = ref[4 * i * config.hop:4 * (i + 1) * config.hop]
         assert float(np.max(np.abs(got - want))) <= BOUND, i
+
+
+def test_vae_chunk_limit(vx, cuda):
+    """A chunk of more frames than vx_vae_max_frames is refused before any
+    launch (a product's 32-row blocks are grid rows, at most 65535)."""
+    config = CONFIGS["small"]
+    vae = vx.Vae(synth.vae_weights(config, 95))
+    assert vae.max_frames == 65535 * 32 // config.hop
+    latents = torch.zeros((vae.max_frames + 1, config.latent), dtype=torch.float32, device=cuda)
+    with pytest.raises(_lib.VxError) as info:
+        vae.decode(latents)
+    assert info.value.status == _lib.VX_BAD_ARG

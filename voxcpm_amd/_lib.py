@@ -189,6 +189,7 @@ _SIGNATURES = {
     "vx_vae_destroy": ([c_void_p], None),
     "vx_vae_reset": ([c_void_p, c_void_p], c_int),
     "vx_vae_hop": ([c_void_p], c_size),
+    "vx_vae_max_frames": ([c_void_p], c_size),
     "vx_vae_decode": ([c_void_p, c_void_p, c_size, c_void_p, c_void_p], c_int),
     "vx_euler_schedule": ([c_size, c_float, c_int, c_void_p, c_void_p,
                            c_void_p], c_int),

@@ -39,6 +39,9 @@ constexpr int kThreads = 256;
 constexpr int kTaps = 7;
 constexpr int kDilations[3] = {1, 3, 9};
 constexpr std::size_t kMaxGraphFrames = 16;
+// Output samples per decode call: a product's row blocks of 32 rows are
+// grid rows, at most 65535 of them.
+constexpr std::size_t kMaxSamples = std::size_t{65535} * 32;
 
 dim3 Blocks(std::size_t count) {
   return dim3(static_cast<unsigned>((count + kThreads - 1) / kThreads));
@@ -47,6 +50,13 @@ dim3 Blocks(std::size_t count) {
 __device__ inline float Snake(float y, float a) {
   const float s = sinf(a * y);
   return y + (1.0F / (a + 1e-9F)) * (s * s);
+}
+
+/// p[0 .. count) = 0.
+__global__ void ZeroKernel(float* p, std::size_t count) {
+  const std::size_t i = static_cast<std::size_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i < count)
+    p[i] = 0.0F;
 }
 
 /// work = [state (kTaps - 1 rows) | latents (t rows)] of `c` channels.
@@ -658,11 +668,15 @@ int vx_vae_create(vx_vae** vae, const vx_vae_shape* shape, const vx_vae_weights*
       weights->in_pointwise_bias == nullptr || weights->out_alpha == nullptr ||
       weights->out_conv == nullptr)
     return vx::Fail(VX_BAD_ARG, "vx_vae_create: null weights");
+  std::size_t hop = 1;
   for (std::size_t b = 0; b < shape->rate_count; ++b) {
     const vx_vae_block& block = weights->blocks[b];
-    if (shape->rates[b] == 0 || !block.scale || !block.bias || !block.alpha || !block.up ||
+    hop *= shape->rates[b];
+    if (shape->rates[b] == 0 || hop > kMaxSamples)
+      return vx::Fail(VX_BAD_ARG, "vx_vae_create: a zero rate, or over 2096640 samples per frame");
+    if (!block.scale || !block.bias || !block.alpha || !block.up ||
         !block.up_bias)
-      return vx::Fail(VX_BAD_ARG, "vx_vae_create: null block weights or zero rate");
+      return vx::Fail(VX_BAD_ARG, "vx_vae_create: null block weights");
     for (const vx_vae_unit& u : block.units)
       VX_TRY(CheckUnit(u));
   }
@@ -719,7 +733,8 @@ int vx_vae_reset(vx_vae* vae, void* stream) {
     return vx::Fail(VX_BAD_ARG, "vx_vae_reset: null handle");
   hipStream_t s = vx::Stream(stream);
   const auto clear = [&](float* p, std::size_t count) {
-    return hipMemsetAsync(p, 0, count * sizeof(float), s) == hipSuccess;
+    ZeroKernel<<<Blocks(count), kThreads, 0, s>>>(p, count);
+    return hipGetLastError() == hipSuccess;
   };
   bool ok = clear(vae->in_state, (kTaps - 1) * vae->shape.latent_dim) &&
             clear(vae->out_state, (kTaps - 1) * vae->out_channels);
@@ -729,11 +744,16 @@ int vx_vae_reset(vx_vae* vae, void* stream) {
       ok = ok && clear(b.unit_state[u], static_cast<std::size_t>(kTaps - 1) * kDilations[u] * b.out);
   }
   if (!ok)
-    return vx::Fail(VX_HIP_ERROR, "vx_vae_reset: hipMemsetAsync");
+    return vx::Fail(VX_HIP_ERROR, "vx_vae_reset: launch");
   return vx::Succeed();
 }
 
 size_t vx_vae_hop(const vx_vae* vae) { return vae == nullptr ? 0 : vae->hop; }
+
+// Products take one 32-row block per grid row, at most 65535 of them.
+size_t vx_vae_max_frames(const vx_vae* vae) {
+  return vae == nullptr ? 0 : kMaxSamples / vae->hop;
+}
 
 int vx_vae_decode(vx_vae* vae, const float* latents, size_t frames, float* samples,
                   void* stream) {
@@ -741,8 +761,9 @@ int vx_vae_decode(vx_vae* vae, const float* latents, size_t frames, float* sampl
     return vx::Fail(VX_BAD_ARG, "vx_vae_decode: null argument");
   if (frames == 0)
     return VX_OK;
-  if (frames > (1U << 16))
-    return vx::Fail(VX_BAD_ARG, "vx_vae_decode: too many frames in one chunk");
+  if (frames > vx_vae_max_frames(vae))
+    return vx::Fail(VX_BAD_ARG, "vx_vae_decode: too many frames in one chunk "
+                                "(vx_vae_max_frames)");
   hipStream_t s = vx::Stream(stream);
   VX_TRY(vae->Reserve(frames));
   GraphKey key{latents, samples, frames, s};

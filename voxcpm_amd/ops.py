@@ -558,6 +558,7 @@ class Vae:
         self.handle = handle
         self.device = device
         self.hop = lib().vx_vae_hop(handle)
+        self.max_frames = lib().vx_vae_max_frames(handle)
 
     def close(self) -> None:
         if getattr(self, "handle", None):
