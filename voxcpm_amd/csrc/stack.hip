@@ -264,12 +264,29 @@ __global__ __launch_bounds__(kWave) void MergeKernel(AttentionArgs a) {
   const int row = static_cast<int>(blockIdx.x);
   const int head = static_cast<int>(blockIdx.y);
   const int lane = static_cast<int>(threadIdx.x);
-  const int chunks = (KeyCount(a, row) + kChunk - 1) / kChunk;
   const std::size_t stride = static_cast<std::size_t>(D) + 2;
   const float* base =
       a.partials + (static_cast<std::size_t>(row) * a.heads + head) * a.splits * stride;
-  float m = -INFINITY;
-  for (int c = lane; c < chunks; c += kWave)
+  // The first 64 chunk slots' statistics and the first kBatch chunks'
+  // values are loaded with the row's key count (which may come from the
+  // device), not after it: every slot below `splits` lies inside the
+  // partials, and slots past the row's chunks (stale) are masked below.
+  const int slots = min(a.splits, kWave);
+  const float* mine = base + static_cast<std::size_t>(min(lane, slots - 1)) * stride;
+  const float first_m = mine[0];
+  const float first_l = mine[1];
+  float first[kBatch][kPerLane];
+#pragma unroll
+  for (int b = 0; b < kBatch; ++b) {
+    const float* part = base + static_cast<std::size_t>(min(b, slots - 1)) * stride + 2 +
+                        lane * kPerLane;
+#pragma unroll
+    for (int j = 0; j < kPerLane; ++j)
+      first[b][j] = part[j];
+  }
+  const int chunks = (KeyCount(a, row) + kChunk - 1) / kChunk;
+  float m = lane < chunks ? first_m : -INFINITY;
+  for (int c = lane + kWave; c < chunks; c += kWave)
     m = fmaxf(m, base[c * stride]);
   m = WaveMax64(m);
   float o[kPerLane];
@@ -282,19 +299,29 @@ __global__ __launch_bounds__(kWave) void MergeKernel(AttentionArgs a) {
     float factor = 0.0F;
     if (c < chunks) {
       const float* part = base + c * stride;
-      factor = expf(part[0] - m);
-      l += part[1] * factor;
+      const float cm = c0 == 0 ? first_m : part[0];
+      const float cl = c0 == 0 ? first_l : part[1];
+      factor = expf(cm - m);
+      l += cl * factor;
     }
     const int count = min(kWave, chunks - c0);
     for (int i0 = 0; i0 < count; i0 += kBatch) {
       float values[kBatch][kPerLane];
+      if (c0 == 0 && i0 == 0) {
 #pragma unroll
-      for (int b = 0; b < kBatch; ++b) {
-        const float* part =
-            base + (c0 + min(i0 + b, count - 1)) * stride + 2 + lane * kPerLane;
+        for (int b = 0; b < kBatch; ++b)
 #pragma unroll
-        for (int j = 0; j < kPerLane; ++j)
-          values[b][j] = part[j];
+          for (int j = 0; j < kPerLane; ++j)
+            values[b][j] = first[b][j];
+      } else {
+#pragma unroll
+        for (int b = 0; b < kBatch; ++b) {
+          const float* part =
+              base + (c0 + min(i0 + b, count - 1)) * stride + 2 + lane * kPerLane;
+#pragma unroll
+          for (int j = 0; j < kPerLane; ++j)
+            values[b][j] = part[j];
+        }
       }
 #pragma unroll
       for (int b = 0; b < kBatch; ++b) {
