@@ -53,8 +53,12 @@ int vx_stream_read(const void* data, size_t bytes, uint32_t never,
  * UNFUSED (the reference's launch sequence of transformer.cpp:55-100:
  * norm, qkv, rotary, attention, o, norm, gate_up, SwiGLU, down).
  * PERSISTENT (one launch per evaluation, grid barriers between the layer's
- * phases, weights loaded ahead of each barrier) is selected explicitly.
- * Tests pin every path against the same oracle. */
+ * phases, weights loaded ahead of each barrier) is selected explicitly; it
+ * exists only where vx_dit_create found every workgroup of its grid
+ * resident at once. Its evaluations cannot report a grid barrier that gave
+ * up waiting through their own return value (they return before the
+ * device runs them): their results are valid only once vx_dit_status has
+ * returned VX_OK. Tests pin every path against the same oracle. */
 #define VX_DIT_PATH_AUTO 0
 #define VX_DIT_PATH_PERSISTENT 1
 #define VX_DIT_PATH_FUSED 2

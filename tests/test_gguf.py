@@ -95,7 +95,7 @@ def test_voxcpm2_layout(ops, tmp_path):
 @pytest.mark.parametrize("case", [
     "magic", "version", "truncated-header", "truncated-data", "unsupported-type",
     "q8-partial-block", "no-component", "not-voxcpm2", "abbreviation-range",
-    "bad-alignment", "nested-array", "missing-file"])
+    "bad-alignment", "nested-array", "missing-file", "byte-count-wraps"])
 def test_malformed_files_fail_cleanly(ops, tmp_path, case):
     rng = synth.Rng(63, 1)
     path = tmp_path / f"{case}.gguf"
@@ -130,6 +130,10 @@ def test_malformed_files_fail_cleanly(ops, tmp_path, case):
         voxcpm2 = False
     elif case == "missing-file":
         path = tmp_path / "absent.gguf"
+    elif case == "byte-count-wraps":
+        # 4 x (2^60 + 1) float32 values: 4 (2^62 + 4) bytes wrap to 16, which
+        # the file holds; the tensor must still be refused.
+        voxcpm2_file(path, rng, extra=("weights/huge", gf.GGML_F32, [4, 2**60 + 1], b"\0" * 16))
     with pytest.raises(_lib.VxError) as info:
         ops.Gguf(path, voxcpm2=voxcpm2)
     assert info.value.status == _lib.VX_BAD_ARG

@@ -275,6 +275,28 @@ def test_prefill_expansion(vx, oracle, cuda, stream, rows, k, n):
     assert np.array_equal(again, results[2])
 
 
+@pytest.mark.parametrize("n", [2048, 6144, 16384])
+@pytest.mark.parametrize("rows", [129, 256, 512, 1024])
+def test_prefill_benched_shapes(vx, oracle, cuda, stream, rows, n):
+    """Every prefill shape the benchmark times (K = 2048), called as it calls
+    them (with a product scratch), against the expanded arithmetic in double
+    at the reference's 1e-4 (products_test.cpp:279-310). Every 7th output
+    column is checked (7 is prime to the 16-column groups and 128-column
+    tiles, so every lane and tile position is visited)."""
+    k = 2048
+    rng = synth.Rng(7, n * 10 + rows)
+    blocks = synth.q8_blocks(rng, n, k)
+    packed = vx.q8_pack(to_device(blocks, cuda), n, k)
+    x = synth.activations(rng, rows, k)
+    scratch = vx.Scratch(128, 16384)
+    y = run_product(vx, to_device(x, cuda), packed, n, None, None, scratch, cuda)
+    cols = np.arange(0, n, 7)
+    worst = expanded_check(np.ascontiguousarray(y[:, cols]), x,
+                           np.ascontiguousarray(blocks[cols]), oracle)
+    print(f"prefill {rows}x{k}x{n}: worst {worst:.2e}", flush=True)
+    assert worst <= 1e-4
+
+
 def test_stream_read_reads_every_byte(vx, cuda, stream):
     """The read-ceiling kernel loads every 16-byte chunk: the XOR of the
     buffer's words reaches the sink only when it equals `never`."""

@@ -32,6 +32,8 @@ def f32(x):
     (1, 1, 63, True),     # one chunk exactly
     (1, 1, 64, True),     # two chunks, the second of one key
     (1, 1, 700, True),    # eleven chunks merged
+    (1, 1, 4200, True),   # 66 chunks: the merge's second pass over chunks 64..
+    (1, 1, 8300, True),   # 130 chunks: more than two passes of the merge
     (3, 3, 130, True),    # causal rows of one sequence beyond a chunk
     (10, 5, 0, False),    # the encoder: two 5-row sequences, bidirectional
 ])
@@ -223,6 +225,39 @@ def test_stack_decode_replays(vx, oracle, cuda, stream):
         position.fill_(past)
         run.gpu.set_path(_lib.STACK_PATH_UNFUSED if past == 64 else
                          _lib.STACK_PATH_FUSED if past == 129 else _lib.STACK_PATH_AUTO)
+        run.gpu.forward(hidden, output, position, position, 1, 1, past, True, run.k_gpu,
+                        run.v_gpu)
+        torch.cuda.synchronize()
+        at = np.array([past], np.int32)
+        ref_h, ref_out = run.cpu.forward(h, at, at, 1, 1, past, True, run.k_cpu, run.v_cpu)
+        check_close(output.cpu().numpy(), ref_out, f"replay past {past} output")
+        check_close(hidden.cpu().numpy(), ref_h, f"replay past {past} hidden")
+
+
+def test_stack_decode_replays_past_4096(vx, oracle, cuda, stream):
+    """The base LM's long-context decode (4096 cached positions and more:
+    65 and more 64-key chunks, so the chunk merge takes its later passes)
+    replayed from one captured graph, every step against the oracle, over a
+    cache filled with random keys and values."""
+    config = STACKS["gqa-hd64"]
+    capacity = 4300
+    run = Run(vx, oracle, cuda, config, 53, capacity=capacity)
+    rng = synth.Rng(54, 1)
+    filled = 4094
+    filler = rng.normal(2 * config.layers * config.kv_heads * filled * config.head_dim)
+    filler = f32(filler).reshape(2, config.layers, config.kv_heads, filled, config.head_dim)
+    run.k_cpu[:, :, :filled] = filler[0]
+    run.v_cpu[:, :, :filled] = filler[1]
+    run.k_gpu[:, :, :filled] = torch.from_numpy(filler[0]).to(cuda)
+    run.v_gpu[:, :, :filled] = torch.from_numpy(filler[1]).to(cuda)
+    hidden = torch.empty((1, config.hidden), dtype=torch.float32, device=cuda)
+    output = torch.empty_like(hidden)
+    position = torch.empty(1, dtype=torch.int32, device=cuda)
+    run.gpu.set_path(_lib.STACK_PATH_AUTO)
+    for past in range(filled, filled + 8):  # 4095 .. 4102 keys: 64 -> 65 chunks
+        h = rng.normal(config.hidden).astype(np.float32).reshape(1, config.hidden)
+        hidden.copy_(torch.from_numpy(h))
+        position.fill_(past)
         run.gpu.forward(hidden, output, position, position, 1, 1, past, True, run.k_gpu,
                         run.v_gpu)
         torch.cuda.synchronize()

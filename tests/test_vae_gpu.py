@@ -82,3 +82,23 @@ def test_vae_chunk_limit(vx, cuda):
     with pytest.raises(_lib.VxError) as info:
         vae.decode(latents)
     assert info.value.status == _lib.VX_BAD_ARG
+
+
+def test_vae_decode_argument_checks(vx, cuda):
+    """The C ABI takes bare pointers: Vae.decode refuses tensors whose bytes
+    are not float32 [frames][latent] rows (bf16, strided, wrong width) and
+    sample buffers too small for the chunk, before any launch."""
+    config = CONFIGS["small"]
+    vae = vx.Vae(synth.vae_weights(config, 96))
+    good = torch.zeros((4, config.latent), dtype=torch.float32, device=cuda)
+    bad = [good.to(torch.bfloat16),
+           torch.zeros((config.latent, 8), dtype=torch.float32, device=cuda).t()[:4],
+           torch.zeros((4, config.latent + 1), dtype=torch.float32, device=cuda),
+           good.reshape(-1)]
+    for latents in bad:
+        with pytest.raises(ValueError):
+            vae.decode(latents)
+    with pytest.raises(ValueError):
+        vae.decode(good, torch.empty(4 * config.hop - 1, dtype=torch.float32, device=cuda))
+    vae.decode(good, torch.empty(4 * config.hop, dtype=torch.float32, device=cuda))
+    torch.cuda.synchronize()

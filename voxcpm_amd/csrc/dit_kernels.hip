@@ -8,9 +8,11 @@
 #include <algorithm>
 #include <cmath>
 #include <cstdint>
+#include <initializer_list>
 
 #include "common.hpp"
 #include "dit_kernels.hpp"
+#include "q8_tile.hpp"
 
 namespace vx::kernels {
 namespace {
@@ -21,27 +23,157 @@ dim3 Blocks(std::size_t count, int threads = kThreads) {
   return dim3(static_cast<unsigned>((count + threads - 1) / threads));
 }
 
+/// One access per thread over `accesses`, at most 4096 workgroups (the
+/// kernels loop over the rest).
+dim3 Grid(std::size_t accesses) {
+  return dim3(static_cast<unsigned>(std::min<std::size_t>((accesses + kThreads - 1) / kThreads,
+                                                          4096)));
+}
+
+/// Workgroups along a row of `accesses` accesses (grid x of the row copies).
+unsigned RowBlocks(std::size_t accesses) {
+  return static_cast<unsigned>(std::max<std::size_t>(1, (accesses + kThreads - 1) / kThreads));
+}
+
 __device__ inline float Silu(float value) {
   return value / (1.0F + expf(-value));
 }
 
-__global__ void RmsNormKernel(const float* input, const Bf16* weight,
-                              Bf16* output, float* output_f32, int width,
-                              float epsilon) {
-  __shared__ float scratch[kThreads / kWave];
-  const std::size_t row = blockIdx.x;
-  const float* x = input + row * width;
-  float sum = 0.0F;
-  for (int i = threadIdx.x; i < width; i += blockDim.x)
-    sum += x[i] * x[i];
-  sum = BlockSum(sum, scratch);
-  const float inverse = rsqrtf(sum / static_cast<float>(width) + epsilon);
-  for (int i = threadIdx.x; i < width; i += blockDim.x) {
-    const float value = x[i] * inverse * Bf16Value(weight[i]);
-    output[row * width + i] = Bf16Bits(value);
-    if (output_f32 != nullptr)
-      output_f32[row * width + i] = value;
+// ---- vector access -------------------------------------------------------
+//
+// The elementwise kernels move V consecutive values per access: V = 4 when
+// every pointer is aligned for it and the widths are multiples of 4 (16-byte
+// float32 and 8-byte bf16 accesses), else V = 1.
+
+template<int V>
+struct Lanes {
+  float v[V];
+};
+
+template<int V>
+__device__ inline Lanes<V> LoadF(const float* at) {
+  Lanes<V> out;
+  if constexpr (V == 4) {
+    const float4 f = *reinterpret_cast<const float4*>(at);
+    out.v[0] = f.x;
+    out.v[1] = f.y;
+    out.v[2] = f.z;
+    out.v[3] = f.w;
+  } else {
+    out.v[0] = *at;
   }
+  return out;
+}
+
+template<int V>
+__device__ inline void StoreF(float* at, const Lanes<V>& in) {
+  if constexpr (V == 4)
+    *reinterpret_cast<float4*>(at) = float4{in.v[0], in.v[1], in.v[2], in.v[3]};
+  else
+    *at = in.v[0];
+}
+
+/// V bf16 values at `at` as float32.
+template<int V>
+__device__ inline Lanes<V> LoadB(const Bf16* at) {
+  Lanes<V> out;
+  if constexpr (V == 4) {
+    const uint2 b = *reinterpret_cast<const uint2*>(at);
+    out.v[0] = q8::Bf16Lo(b.x);
+    out.v[1] = q8::Bf16Hi(b.x);
+    out.v[2] = q8::Bf16Lo(b.y);
+    out.v[3] = q8::Bf16Hi(b.y);
+  } else {
+    out.v[0] = Bf16Value(*at);
+  }
+  return out;
+}
+
+/// V float32 values rounded to bf16 (nearest even, quiet NaNs) at `at`.
+template<int V>
+__device__ inline void StoreB(Bf16* at, const Lanes<V>& in) {
+  if constexpr (V == 4)
+    *reinterpret_cast<uint2*>(at) =
+        uint2{q8::PackBf16x2(in.v[0], in.v[1]), q8::PackBf16x2(in.v[2], in.v[3])};
+  else
+    *at = Bf16Bits(in.v[0]);
+}
+
+bool Aligned(const void* pointer, std::size_t bytes) {
+  return reinterpret_cast<std::uintptr_t>(pointer) % bytes == 0;
+}
+
+/// Whether float32 arrays (16 bytes) and bf16 arrays (8 bytes) allow V = 4.
+bool Quads(std::initializer_list<const float*> floats, std::initializer_list<const Bf16*> halves,
+           std::size_t width) {
+  if (width % 4 != 0)
+    return false;
+  for (const float* f : floats)
+    if (f != nullptr && !Aligned(f, 16))
+      return false;
+  for (const Bf16* h : halves)
+    if (h != nullptr && !Aligned(h, 8))
+      return false;
+  return true;
+}
+
+// ---- RMSNorm ----------------------------------------------------------------
+
+constexpr int kNormWaves = 4;  // rows per workgroup, one per wave
+
+/// One row per wave. Lane l reads accesses l, l + 64, ... of the row (V
+/// values each) and keeps the first kHeld of them in registers for the
+/// second pass (rows up to 2048 values; longer rows read the rest again).
+/// The lanes' sums of squares meet by a wave butterfly; the output is
+/// bf16((x * inv) * gamma) with inv = rsqrt(mean(x^2) + eps), the
+/// reference's arithmetic (kernels/generator_kernels.hip:91-108), and its
+/// float32 value when asked for.
+template<int V>
+__global__ __launch_bounds__(kNormWaves * kWave) void WaveNormKernel(
+    const float* input, const Bf16* weight, Bf16* output, float* output_f32, int rows,
+    int width, float epsilon) {
+  constexpr int kHeld = 32 / V;
+  const int lane = static_cast<int>(threadIdx.x) % kWave;
+  const int row = static_cast<int>(blockIdx.x) * kNormWaves + static_cast<int>(threadIdx.x) / kWave;
+  if (row >= rows)
+    return;
+  const std::size_t base = static_cast<std::size_t>(row) * width;
+  const int accesses = width / V;
+  Lanes<V> held[kHeld];
+  float squares = 0.0F;
+#pragma unroll
+  for (int j = 0; j < kHeld; ++j) {
+    const int c = lane + kWave * j;
+    held[j] = c < accesses ? LoadF<V>(input + base + V * c) : Lanes<V>{};
+#pragma unroll
+    for (int i = 0; i < V; ++i)
+      squares += held[j].v[i] * held[j].v[i];
+  }
+  for (int c = lane + kWave * kHeld; c < accesses; c += kWave) {
+    const Lanes<V> x = LoadF<V>(input + base + V * c);
+#pragma unroll
+    for (int i = 0; i < V; ++i)
+      squares += x.v[i] * x.v[i];
+  }
+  const float inverse = rsqrtf(WaveSum(squares) / static_cast<float>(width) + epsilon);
+  const auto emit = [&](int c, const Lanes<V>& x) {
+    const Lanes<V> gamma = LoadB<V>(weight + V * c);
+    Lanes<V> y;
+#pragma unroll
+    for (int i = 0; i < V; ++i)
+      y.v[i] = x.v[i] * inverse * gamma.v[i];
+    StoreB<V>(output + base + V * c, y);
+    if (output_f32 != nullptr)
+      StoreF<V>(output_f32 + base + V * c, y);
+  };
+#pragma unroll
+  for (int j = 0; j < kHeld; ++j) {
+    const int c = lane + kWave * j;
+    if (c < accesses)
+      emit(c, held[j]);
+  }
+  for (int c = lane + kWave * kHeld; c < accesses; c += kWave)
+    emit(c, LoadF<V>(input + base + V * c));
 }
 
 /// One workgroup per (row, head of q | k | v), one thread per rotated pair
@@ -155,90 +287,162 @@ __global__ __launch_bounds__(kWave) void AttentionKernel(
   }
 }
 
-__global__ void SwiGluKernel(const float* gate_up, Bf16* output,
-                             std::size_t rows, std::size_t width) {
-  const std::size_t index =
-      static_cast<std::size_t>(blockIdx.x) * blockDim.x + threadIdx.x;
-  if (index >= rows * width)
-    return;
-  const std::size_t row = index / width;
-  const std::size_t i = index % width;
-  const float gate = gate_up[row * 2 * width + i];
-  const float up = gate_up[row * 2 * width + width + i];
-  output[index] = Bf16Bits(Silu(gate) * up);
+// ---- elementwise -------------------------------------------------------------
+//
+// Grid-stride loops over V-value accesses (the grid is sized for one access
+// per thread and capped).
+
+__device__ inline std::size_t FirstIndex() {
+  return static_cast<std::size_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+}
+__device__ inline std::size_t Stride() {
+  return static_cast<std::size_t>(gridDim.x) * blockDim.x;
 }
 
-__global__ void AddBiasKernel(float* data, const Bf16* bias, std::size_t rows,
-                              std::size_t width) {
-  const std::size_t index =
-      static_cast<std::size_t>(blockIdx.x) * blockDim.x + threadIdx.x;
-  if (index < rows * width)
-    data[index] += Bf16Value(bias[index % width]);
-}
-
-__global__ void ToBf16Kernel(const float* input, Bf16* output,
-                             std::size_t count, int silu) {
-  const std::size_t index =
-      static_cast<std::size_t>(blockIdx.x) * blockDim.x + threadIdx.x;
-  if (index >= count)
-    return;
-  float value = input[index];
-  if (silu)
-    value = Silu(value);
-  output[index] = Bf16Bits(value);
-}
-
-__global__ void GatherRowsKernel(const float* input,
-                                 const std::int32_t* indices, float* output,
-                                 int width) {
-  const std::size_t row = blockIdx.x;
-  const std::size_t source = static_cast<std::size_t>(indices[row]);
-  for (int i = threadIdx.x; i < width; i += blockDim.x)
-    output[row * width + i] = input[source * width + i];
-}
-
-__global__ void AssembleDitKernel(const float* mu, const float* time,
-                                  const float* cond, const float* x,
-                                  float* output, int patch, int width) {
-  const int sequence = blockIdx.x;  // 0 conditional, 1 unconditional
-  const int row = blockIdx.y;
-  const int length = 3 + 2 * patch;
-  float* target =
-      output + (static_cast<std::size_t>(sequence) * length + row) * width;
-  for (int i = threadIdx.x; i < width; i += blockDim.x) {
-    float value;
-    if (row < 2)
-      value = sequence == 0 ? mu[row * width + i] : 0.0F;
-    else if (row == 2)
-      value = time[i];
-    else if (row < 3 + patch)
-      value = cond[(row - 3) * width + i];
-    else
-      value = x[(row - 3 - patch) * width + i];
-    target[i] = value;
+/// bf16(silu(gate) * up) over rows of [gate | up] (each `width` wide), the
+/// reference's SwiGLU (kernels/generator_kernels.hip:243-254).
+template<int V>
+__global__ __launch_bounds__(kThreads) void GatedKernel(const float* gate_up, Bf16* output,
+                                                        std::size_t rows, std::size_t width) {
+  const std::size_t per_row = width / V;
+  for (std::size_t e = FirstIndex(); e < rows * per_row; e += Stride()) {
+    const std::size_t row = e / per_row;
+    const std::size_t column = V * (e % per_row);
+    const Lanes<V> gate = LoadF<V>(gate_up + 2 * width * row + column);
+    const Lanes<V> up = LoadF<V>(gate_up + 2 * width * row + width + column);
+    Lanes<V> y;
+#pragma unroll
+    for (int i = 0; i < V; ++i)
+      y.v[i] = Silu(gate.v[i]) * up.v[i];
+    StoreB<V>(output + width * row + column, y);
   }
 }
 
-__global__ void GuidedEulerKernel(const float* velocity, float* x, int count,
-                                  float cfg, float dt, int zero_star) {
-  __shared__ float scratch[kThreads / kWave];
+/// data[r][c] += f32(bias[c]) (kernels/generator_kernels.hip:256-262).
+template<int V>
+__global__ __launch_bounds__(kThreads) void BiasKernel(float* data, const Bf16* bias,
+                                                       std::size_t rows, std::size_t width) {
+  const std::size_t per_row = width / V;
+  for (std::size_t e = FirstIndex(); e < rows * per_row; e += Stride()) {
+    const std::size_t column = V * (e % per_row);
+    Lanes<V> x = LoadF<V>(data + V * e);
+    const Lanes<V> b = LoadB<V>(bias + column);
+#pragma unroll
+    for (int i = 0; i < V; ++i)
+      x.v[i] += b.v[i];
+    StoreF<V>(data + V * e, x);
+  }
+}
+
+/// bf16(x) or bf16(silu(x)) (kernels/generator_kernels.hip:264-274).
+template<int V>
+__global__ __launch_bounds__(kThreads) void RoundKernel(const float* input, Bf16* output,
+                                                        std::size_t count, int silu) {
+  for (std::size_t e = FirstIndex(); e < count / V; e += Stride()) {
+    Lanes<V> x = LoadF<V>(input + V * e);
+    if (silu) {
+#pragma unroll
+      for (int i = 0; i < V; ++i)
+        x.v[i] = Silu(x.v[i]);
+    }
+    StoreB<V>(output + V * e, x);
+  }
+}
+
+/// Row copies: output row blockIdx.y <- `source(row)`, V values per access.
+/// Gather: the source row is indices[row] of `input`
+/// (kernels/generator_kernels.hip:82-89).
+template<int V>
+__global__ __launch_bounds__(kThreads) void GatherKernel(const float* input,
+                                                         const std::int32_t* indices,
+                                                         float* output, int width) {
+  const int row = static_cast<int>(blockIdx.y);
+  const float* from = input + static_cast<std::size_t>(indices[row]) * width;
+  float* to = output + static_cast<std::size_t>(row) * width;
+  for (int c = static_cast<int>(blockIdx.x * blockDim.x + threadIdx.x); c < width / V;
+       c += static_cast<int>(gridDim.x * blockDim.x))
+    StoreF<V>(to + V * c, LoadF<V>(from + V * c));
+}
+
+/// The DiT input rows of both branches (generator.cpp:111-121): each output
+/// row of [2][3 + 2 patch][width] picks its source once (mu halves for the
+/// conditional branch, zeros for the unconditional one, then the time
+/// vector, the condition rows and the projected x rows, the layout of
+/// kernels/generator_kernels.hip:320-340) and its threads copy V values
+/// per access.
+template<int V>
+__global__ __launch_bounds__(kThreads) void InputRowsKernel(const float* mu, const float* time,
+                                                            const float* cond, const float* x,
+                                                            float* output, int patch,
+                                                            int width) {
+  const int length = 3 + 2 * patch;
+  const int branch = static_cast<int>(blockIdx.y) / length;
+  const int row = static_cast<int>(blockIdx.y) % length;
+  const float* from = nullptr;  // null: zeros
+  if (row < 2)
+    from = branch == 0 ? mu + static_cast<std::size_t>(row) * width : nullptr;
+  else if (row == 2)
+    from = time;
+  else if (row < 3 + patch)
+    from = cond + static_cast<std::size_t>(row - 3) * width;
+  else
+    from = x + static_cast<std::size_t>(row - 3 - patch) * width;
+  float* to = output + static_cast<std::size_t>(blockIdx.y) * width;
+  for (int c = static_cast<int>(blockIdx.x * blockDim.x + threadIdx.x); c < width / V;
+       c += static_cast<int>(gridDim.x * blockDim.x))
+    StoreF<V>(to + V * c, from != nullptr ? LoadF<V>(from + V * c) : Lanes<V>{});
+}
+
+/// The guided Euler step over one velocity pair (conditional c, then
+/// unconditional u, `count` values each), in one workgroup:
+/// x -= dt (u s + cfg (c - u s)), with s = <c, u> / (|u|^2 + 1e-8) under
+/// CFG-Zero* and s = 1 otherwise (kernels/generator_kernels.hip:342-360).
+/// Both sums are carried together: lane partials, a wave butterfly each,
+/// then the waves' pairs added in wave order from LDS.
+template<int V>
+__global__ __launch_bounds__(kThreads) void EulerKernel(const float* velocity, float* x,
+                                                        int count, float cfg, float dt,
+                                                        int zero_star) {
+  __shared__ float2 waves[kThreads / kWave];
   const float* c = velocity;
   const float* u = velocity + count;
+  const int accesses = count / V;
   float s = 1.0F;
   if (zero_star) {
     float dot = 0.0F;
     float norm = 0.0F;
-    for (int i = threadIdx.x; i < count; i += blockDim.x) {
-      dot += c[i] * u[i];
-      norm += u[i] * u[i];
+    for (int e = static_cast<int>(threadIdx.x); e < accesses; e += kThreads) {
+      const Lanes<V> cv = LoadF<V>(c + V * e);
+      const Lanes<V> uv = LoadF<V>(u + V * e);
+#pragma unroll
+      for (int i = 0; i < V; ++i) {
+        dot += cv.v[i] * uv.v[i];
+        norm += uv.v[i] * uv.v[i];
+      }
     }
-    dot = BlockSum(dot, scratch);
-    norm = BlockSum(norm, scratch);
-    s = dot / (norm + 1e-8F);
+    dot = WaveSum(dot);
+    norm = WaveSum(norm);
+    if (threadIdx.x % kWave == 0)
+      waves[threadIdx.x / kWave] = float2{dot, norm};
+    __syncthreads();
+    float2 total = waves[0];
+#pragma unroll
+    for (int w = 1; w < kThreads / kWave; ++w) {
+      total.x += waves[w].x;
+      total.y += waves[w].y;
+    }
+    s = total.x / (total.y + 1e-8F);
   }
-  for (int i = threadIdx.x; i < count; i += blockDim.x) {
-    const float guided = u[i] * s + cfg * (c[i] - u[i] * s);
-    x[i] -= dt * guided;
+  for (int e = static_cast<int>(threadIdx.x); e < accesses; e += kThreads) {
+    const Lanes<V> cv = LoadF<V>(c + V * e);
+    const Lanes<V> uv = LoadF<V>(u + V * e);
+    Lanes<V> xv = LoadF<V>(x + V * e);
+#pragma unroll
+    for (int i = 0; i < V; ++i) {
+      const float guided = uv.v[i] * s + cfg * (cv.v[i] - uv.v[i] * s);
+      xv.v[i] -= dt * guided;
+    }
+    StoreF<V>(x + V * e, xv);
   }
 }
 
@@ -257,8 +461,15 @@ void RmsNorm(const float* input, const Bf16* weight, Bf16* output,
              float epsilon, hipStream_t stream) {
   if (rows == 0)
     return;
-  RmsNormKernel<<<static_cast<unsigned>(rows), kThreads, 0, stream>>>(
-      input, weight, output, output_f32, static_cast<int>(width), epsilon);
+  const dim3 grid(static_cast<unsigned>((rows + kNormWaves - 1) / kNormWaves));
+  if (Quads({input, output_f32}, {weight, output}, width))
+    WaveNormKernel<4><<<grid, kNormWaves * kWave, 0, stream>>>(
+        input, weight, output, output_f32, static_cast<int>(rows), static_cast<int>(width),
+        epsilon);
+  else
+    WaveNormKernel<1><<<grid, kNormWaves * kWave, 0, stream>>>(
+        input, weight, output, output_f32, static_cast<int>(rows), static_cast<int>(width),
+        epsilon);
 }
 
 // kernels/generator_kernels.hip:110-158
@@ -301,8 +512,10 @@ void SwiGlu(const float* gate_up, Bf16* output, std::size_t rows,
             std::size_t width, hipStream_t stream) {
   if (rows * width == 0)
     return;
-  SwiGluKernel<<<Blocks(rows * width), kThreads, 0, stream>>>(gate_up, output,
-                                                              rows, width);
+  if (Quads({gate_up}, {output}, width))
+    GatedKernel<4><<<Grid(rows * width / 4), kThreads, 0, stream>>>(gate_up, output, rows, width);
+  else
+    GatedKernel<1><<<Grid(rows * width), kThreads, 0, stream>>>(gate_up, output, rows, width);
 }
 
 // kernels/generator_kernels.hip:256-262
@@ -310,8 +523,10 @@ void AddBias(float* data, const Bf16* bias, std::size_t rows,
              std::size_t width, hipStream_t stream) {
   if (rows * width == 0)
     return;
-  AddBiasKernel<<<Blocks(rows * width), kThreads, 0, stream>>>(data, bias,
-                                                               rows, width);
+  if (Quads({data}, {bias}, width))
+    BiasKernel<4><<<Grid(rows * width / 4), kThreads, 0, stream>>>(data, bias, rows, width);
+  else
+    BiasKernel<1><<<Grid(rows * width), kThreads, 0, stream>>>(data, bias, rows, width);
 }
 
 // kernels/generator_kernels.hip:264-274
@@ -319,35 +534,58 @@ void ToBf16(const float* input, Bf16* output, std::size_t count, bool silu,
             hipStream_t stream) {
   if (count == 0)
     return;
-  ToBf16Kernel<<<Blocks(count), kThreads, 0, stream>>>(input, output, count,
-                                                       silu ? 1 : 0);
+  if (Quads({input}, {output}, count))
+    RoundKernel<4><<<Grid(count / 4), kThreads, 0, stream>>>(input, output, count, silu ? 1 : 0);
+  else
+    RoundKernel<1><<<Grid(count), kThreads, 0, stream>>>(input, output, count, silu ? 1 : 0);
 }
 
 // kernels/generator_kernels.hip:82-89
 void GatherRows(const float* input, const std::int32_t* indices,
                 float* output, std::size_t rows, std::size_t width,
                 hipStream_t stream) {
-  if (rows == 0)
+  if (rows == 0 || width == 0)
     return;
-  GatherRowsKernel<<<static_cast<unsigned>(rows), kThreads, 0, stream>>>(
-      input, indices, output, static_cast<int>(width));
+  const bool quads = Quads({input, output}, {}, width);
+  const dim3 grid(RowBlocks(quads ? width / 4 : width), static_cast<unsigned>(rows));
+  if (quads)
+    GatherKernel<4><<<grid, kThreads, 0, stream>>>(input, indices, output,
+                                                   static_cast<int>(width));
+  else
+    GatherKernel<1><<<grid, kThreads, 0, stream>>>(input, indices, output,
+                                                   static_cast<int>(width));
 }
 
 // kernels/generator_kernels.hip:320-340
 void AssembleDit(const float* mu, const float* time, const float* cond,
                  const float* x, float* output, std::size_t patch,
                  std::size_t width, hipStream_t stream) {
-  AssembleDitKernel<<<dim3(2, static_cast<unsigned>(3 + 2 * patch)), kThreads,
-                      0, stream>>>(mu, time, cond, x, output,
-                                   static_cast<int>(patch),
-                                   static_cast<int>(width));
+  if (width == 0)
+    return;
+  const bool quads = Quads({mu, time, cond, x, output}, {}, width);
+  const dim3 grid(RowBlocks(quads ? width / 4 : width),
+                  static_cast<unsigned>(2 * (3 + 2 * patch)));
+  if (quads)
+    InputRowsKernel<4><<<grid, kThreads, 0, stream>>>(mu, time, cond, x, output,
+                                                      static_cast<int>(patch),
+                                                      static_cast<int>(width));
+  else
+    InputRowsKernel<1><<<grid, kThreads, 0, stream>>>(mu, time, cond, x, output,
+                                                      static_cast<int>(patch),
+                                                      static_cast<int>(width));
 }
 
 // kernels/generator_kernels.hip:342-360
 void GuidedEuler(const float* velocity, float* x, std::size_t count, float cfg,
                  float dt, bool zero_star, hipStream_t stream) {
-  GuidedEulerKernel<<<1, kThreads, 0, stream>>>(
-      velocity, x, static_cast<int>(count), cfg, dt, zero_star ? 1 : 0);
+  if (count == 0)
+    return;
+  if (Quads({velocity, velocity + count, x}, {}, count))
+    EulerKernel<4><<<1, kThreads, 0, stream>>>(velocity, x, static_cast<int>(count), cfg, dt,
+                                               zero_star ? 1 : 0);
+  else
+    EulerKernel<1><<<1, kThreads, 0, stream>>>(velocity, x, static_cast<int>(count), cfg, dt,
+                                               zero_star ? 1 : 0);
 }
 
 void CopyFloats(const float* src, float* dst, std::size_t count,

@@ -1236,7 +1236,25 @@ int GridSize() {
   return std::min(units, kMaxGrid);
 }
 
-bool Prepare(const fused::Shape& s) { return Pick(s) != nullptr; }
+bool Prepare(const fused::Shape& s) {
+  const Kernel kernel = Pick(s);
+  if (kernel == nullptr)
+    return false;
+  // Every workgroup of the grid must be resident at once, or the grid
+  // barriers would wait for workgroups that cannot start: one workgroup
+  // of this size and LDS per compute unit, and the grid no larger than
+  // the compute units.
+  int per_unit = 0;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_unit, kernel, kThreads, kLdsBytes) !=
+      hipSuccess)
+    return false;
+  int device = 0;
+  int units = 0;
+  if (hipGetDevice(&device) != hipSuccess ||
+      hipDeviceGetAttribute(&units, hipDeviceAttributeMultiprocessorCount, device) != hipSuccess)
+    return false;
+  return per_unit >= 1 && GridSize() <= units * per_unit;
+}
 
 std::size_t TraceWords(int layers, int grid) {
   return static_cast<std::size_t>(grid) * 4 * (2 + 4 * static_cast<std::size_t>(layers));

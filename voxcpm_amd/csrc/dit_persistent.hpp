@@ -85,7 +85,8 @@ bool Supported(const fused::Shape& s, int layers, int grid);
 int GridSize();
 
 /// Sets up the kernel for this shape (its LDS size limit) outside any
-/// stream capture; false when there is no kernel for it.
+/// stream capture; false when there is no kernel for it or when its grid
+/// cannot be resident on the device all at once.
 bool Prepare(const fused::Shape& s);
 
 /// 64-bit words of a launch's timestamp trace: [grid][barriers + 1][4]

@@ -5,8 +5,8 @@
 
 #include <hip/hip_runtime.h>
 
-#include <algorithm>
 #include <cstddef>
+#include <memory>
 #include <stdexcept>
 #include <string>
 #include <utility>
@@ -32,50 +32,46 @@ inline void CheckVx(int status, const char* what) {
     throw GpuError(std::string(what) + ": " + vx_last_error());
 }
 
-/// A device allocation of `count` elements of T (device.hpp:33-77).
+/// The deleter of DeviceBuffer's allocation.
+struct DeviceFree {
+  void operator()(void* pointer) const noexcept { (void)hipFree(pointer); }
+};
+
+/// Uninitialised device storage for elements of T with one owner: moved,
+/// never copied, freed with its owner (the ownership of device.hpp:33-77).
+/// The allocation is a unique_ptr with a hipFree deleter, so moves and
+/// destruction come from it; the element count travels beside it and
+/// counts only while an allocation is held.
 template<typename T>
 class DeviceBuffer {
 public:
   DeviceBuffer() = default;
-  explicit DeviceBuffer(std::size_t count) { Resize(count); }
-  ~DeviceBuffer() { Release(); }
-  DeviceBuffer(const DeviceBuffer&) = delete;
-  DeviceBuffer& operator=(const DeviceBuffer&) = delete;
-  DeviceBuffer(DeviceBuffer&& other) noexcept
-      : data_(std::exchange(other.data_, nullptr)),
-        count_(std::exchange(other.count_, 0)) {}
-  DeviceBuffer& operator=(DeviceBuffer&& other) noexcept {
-    Release();
-    data_ = std::exchange(other.data_, nullptr);
-    count_ = std::exchange(other.count_, 0);
-    return *this;
-  }
+  explicit DeviceBuffer(std::size_t count) : memory_(Allocate(count)), count_(count) {}
 
-  /// Reallocates when `count` exceeds the capacity; contents are lost.
+  /// Ensures room for `count` elements. A larger request frees the old
+  /// allocation before making the new one (the contents are not kept); a
+  /// smaller one keeps what is held.
   void Reserve(std::size_t count) {
-    if (count > count_)
-      Resize(count);
-  }
-
-  [[nodiscard]] T* get() const { return data_; }
-  [[nodiscard]] std::size_t size() const { return count_; }
-
-private:
-  void Resize(std::size_t count) {
-    Release();
-    Check(hipMalloc(reinterpret_cast<void**>(&data_),
-                    std::max<std::size_t>(count, 1) * sizeof(T)),
-          "hipMalloc");
+    if (count <= size())
+      return;
+    memory_.reset();
+    memory_.reset(Allocate(count));
     count_ = count;
   }
-  void Release() noexcept {
-    if (data_ != nullptr)
-      (void)hipFree(data_);
-    data_ = nullptr;
-    count_ = 0;
+
+  [[nodiscard]] T* get() const { return memory_.get(); }
+  [[nodiscard]] std::size_t size() const { return memory_ ? count_ : 0; }
+
+private:
+  /// hipMalloc of `count` elements; a zero count still takes one element,
+  /// so that every held buffer has a valid device address.
+  static T* Allocate(std::size_t count) {
+    void* pointer = nullptr;
+    Check(hipMalloc(&pointer, (count == 0 ? 1 : count) * sizeof(T)), "hipMalloc");
+    return static_cast<T*>(pointer);
   }
 
-  T* data_ = nullptr;
+  std::unique_ptr<T, DeviceFree> memory_;
   std::size_t count_ = 0;
 };
 

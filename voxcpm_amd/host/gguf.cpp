@@ -128,10 +128,16 @@ std::string Embedded(const GgufFile& file, std::string_view name) {
 }  // namespace
 
 std::uint64_t GgmlBytes(std::uint32_t type, std::uint64_t elements) {
+  // Zero for a count whose bytes would pass 2^64 - 1 (a wrapped count would
+  // pair a huge shape with a small span of the file).
+  constexpr std::uint64_t kMost = std::numeric_limits<std::uint64_t>::max();
   switch (static_cast<GgmlType>(type)) {
-    case GgmlType::kF32: case GgmlType::kI32: return elements * 4;
-    case GgmlType::kF16: case GgmlType::kBF16: return elements * 2;
-    case GgmlType::kQ8_0: return elements % 32 == 0 ? elements / 32 * 34 : 0;
+    case GgmlType::kF32: case GgmlType::kI32:
+      return elements > kMost / 4 ? 0 : elements * 4;
+    case GgmlType::kF16: case GgmlType::kBF16:
+      return elements > kMost / 2 ? 0 : elements * 2;
+    case GgmlType::kQ8_0:
+      return elements % 32 != 0 || elements / 32 > kMost / 34 ? 0 : elements / 32 * 34;
   }
   return 0;
 }
@@ -216,6 +222,8 @@ std::unique_ptr<GgufFile> GgufFile::Open(const std::string& path, std::string* e
       // Q8_0 rows are whole blocks: the innermost dimension a multiple of 32.
       if (tensor.type == static_cast<std::uint32_t>(GgmlType::kQ8_0) && tensor.dims[0] % 32 != 0)
         throw GgufError("tensor " + tensor.name + " is not whole Q8_0 blocks");
+      if (tensor.bytes == 0 && GgmlBytes(tensor.type, 32) != 0)
+        throw GgufError("tensor " + tensor.name + " is too large");
       if (tensor.bytes == 0)
         throw GgufError("tensor " + tensor.name + " has an unsupported type " +
                         std::to_string(tensor.type));

@@ -531,7 +531,8 @@ class Vae:
         self._keep = []
 
         def up(array) -> int:
-            tensor = array.to(device) if isinstance(array, torch.Tensor) else \
+            tensor = array.to(device, torch.float32).contiguous() \
+                if isinstance(array, torch.Tensor) else \
                 torch.from_numpy(np.ascontiguousarray(array, dtype=np.float32)).to(device)
             self._keep.append(tensor)
             return tensor.data_ptr()
@@ -575,9 +576,23 @@ class Vae:
                stream=None) -> torch.Tensor:
         """latents float32 [frames][latent] on the device -> samples
         [frames * hop], continuing the stream."""
+        # The C ABI takes bare pointers and a frame count: the tensors must
+        # be exactly what it reads and writes.
+        if latents.dtype != torch.float32 or latents.dim() != 2 or not latents.is_contiguous():
+            raise ValueError("latents must be a contiguous float32 [frames][latent] tensor")
+        if latents.shape[1] != self.config.latent:
+            raise ValueError(f"latents have {latents.shape[1]} channels, the decoder "
+                             f"takes {self.config.latent}")
+        if latents.device.type != "cuda" or (self.device.index is not None and
+                                              latents.device.index != self.device.index):
+            raise ValueError(f"latents are on {latents.device}, the decoder on {self.device}")
         frames = latents.shape[0]
         if samples is None:
             samples = torch.empty(frames * self.hop, dtype=torch.float32, device=latents.device)
+        elif (samples.dtype != torch.float32 or not samples.is_contiguous() or
+              samples.numel() < frames * self.hop or samples.device != latents.device):
+            raise ValueError(f"samples must be a contiguous float32 tensor of at least "
+                             f"{frames * self.hop} values on {latents.device}")
         check(lib().vx_vae_decode(self.handle, _ptr(latents), frames, _ptr(samples),
                                   _stream(stream)))
         return samples
