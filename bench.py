@@ -30,6 +30,9 @@ sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBS = 8000.0
 SWEEP_SHAPES = [(1024, 3072), (1024, 8192), (2048, 2048), (2048, 16384)]
+# The single product of the CPU-runnable configuration (M = 22, K = 1024,
+# N = 4096): timed beside the sweep, not part of `value`.
+SINGLE_SHAPE = (1024, 4096)
 SWEEP_ROWS = [1, 2, 22, 44, 128]
 ROWS = 22
 ROTATION_BYTES = 1.1e9
@@ -37,10 +40,12 @@ BF16_PEAK_TFLOPS = 2500.0
 # HBM bytes per launch of the M=22 sweep kernels from two rocprofv3 PMC runs
 # (profiles/q8_skinny_m22_traffic.md): FETCH_SIZE KiB (scaled by 2.0, its
 # reading of a 256 MiB copy of known size) + WRITE_SIZE KiB (scale 1.0).
-# Measured, not computed: re-measure when the product kernel changes.
+# Measured, not computed: re-measure when the product kernel changes. Last
+# measured on the build of commit TRAFFIC_BUILD (the summary names it).
 FETCH_SCALE = 262144 / 131083.5
-TRAFFIC_KIB = {(1024, 3072): (1833.5, 264.0), (1024, 8192): (4553.0, 704.0),
-               (2048, 2048): (2553.5, 176.0), (2048, 16384): (17805.5, 1408.0)}
+TRAFFIC_BUILD = "90ae678"
+TRAFFIC_KIB = {(1024, 3072): (1833.5, 264.0), (1024, 8192): (4551.0, 704.0),
+               (2048, 2048): (2553.5, 176.0), (2048, 16384): (17806.5, 1408.0)}
 # The decode steps' products (tools/bench/gemm_bench.cpp:34-38): the base and
 # residual LMs (hidden 2048, 16 + 2 x 2 heads of 128, MLP 6144) and the
 # local encoder/DiT shapes, at one row (an LM step) and five (the encoder's
@@ -131,6 +136,7 @@ def gpu_products(args, torch, ops, synth, device, stream):
     scratch = ops.Scratch(128, 16384)
     log("building weight pools")
     products = [Product(ops, synth, torch, device, k, n, seed=0) for k, n in SWEEP_SHAPES]
+    single = Product(ops, synth, torch, device, *SINGLE_SHAPE, seed=0, rows=[ROWS])
 
     def step(_):
         for p in products:
@@ -166,6 +172,17 @@ def gpu_products(args, torch, ops, synth, device, stream):
     for row in sweep:
         if row["m"] == ROWS:
             log(f"  M=22 K={row['k']} N={row['n']}: {row['us']} us, {row['gbs']} GB/s")
+    count = max(single.copies, 64)
+    g = graph_of(torch, stream, lambda _i: single.launch(ops, scratch, ROWS), count)
+    g.replay()
+    us = time_graph(torch, stream, g) / count * 1e6
+    del g
+    single_row = {"m": ROWS, "k": single.k, "n": single.n, "us": round(us, 3),
+                  "gbs": round(single.bytes / us / 1e3, 1),
+                  "hbm_frac": round(single.bytes / us / 1e3 / HBM_PEAK_GBS, 4)}
+    log(f"  single product M=22 K={single.k} N={single.n}: {us:.3f} us, "
+        f"{single.bytes / us / 1e3:.1f} GB/s")
+    del single
     # The per-launch read ceiling: each shape's bytes, rotated and replayed
     # from a HIP graph the same way, read once with no arithmetic
     # (vx_stream_read): what one launch of that size can reach on this GPU.
@@ -189,6 +206,7 @@ def gpu_products(args, torch, ops, synth, device, stream):
         "launch_bytes": step_bytes / 4,
         "launch_us": seconds / launches * 1e6,
         "sweep": sweep,
+        "single": single_row,
         "ceiling": ceiling,
     }
     del products
@@ -593,12 +611,21 @@ def gpu_patch(args, torch, ops, synth, device, stream):
                         "22 rows (CFG pair x 11), 10 uniform Euler steps, CFG 2.0"}
 
 
+def host_cores() -> int:
+    """The cores this process may run on (its CPU affinity: the host's share
+    given to this job), every one of which the CPU legs use."""
+    try:
+        return max(1, len(os.sched_getaffinity(0)))
+    except AttributeError:
+        return max(1, os.cpu_count() or 1)
+
+
 def cpu_baseline(synth):
     """The oracle's scalar products on the host's cores: a bounded sample
     (about 10 s) of the same M=22 workload."""
     sys.path.insert(0, os.path.join(ROOT, "tests"))
     import oracle_lib
-    threads = max(1, min(16, os.cpu_count() or 1))
+    threads = host_cores()
     inputs = []
     for k, n in SWEEP_SHAPES:
         rng = synth.Rng(0, k * 31 + n)
@@ -627,7 +654,7 @@ def cpu_baseline(synth):
     single, single_repeats, single_seconds = rate(1, 2.0, 40)
     log(f"CPU oracle: {single:.3f} GB/s on 1 thread")
     return {"value": round(value, 3), "unit": "GB/s", "cores": threads,
-            "kind": "port",
+            "host_cpu_count": os.cpu_count(), "kind": "port",
             "sample": "oracle Q8_0 x bf16 products, M=22, the four sweep shapes, "
                       f"repeats {repeats}, {seconds:.1f} s",
             "value_1_thread": round(single, 4),
@@ -636,25 +663,26 @@ def cpu_baseline(synth):
 
 
 def cpu_patch(synth):
-    """One DiT evaluation of the oracle (the synthetic 12-block DiT) on the
-    host's cores, scaled to the 10 evaluations of a patch."""
+    """One whole 10-step CFG patch of the oracle (the synthetic 12-block
+    DiT: ten evaluations and their Euler steps, vo_dit_patch) on every host
+    core, timed as one call."""
     import oracle_lib
     config = synth.SYNTHETIC_DIT
-    threads = max(1, min(16, os.cpu_count() or 1))
+    threads = host_cores()
     weights = getattr(gpu_patch, "weights", None)
     if weights is None:
         rope = oracle_lib.rope_table(config.rope_theta, config.head_dim, None, 1.0, 11)
         weights = synth.dit_weights(config, 3, rope)
     dit = oracle_lib.OracleDit(weights, threads=threads)
     inputs = synth.patch_inputs(config, 4)
-    cond = dit.cond_rows(inputs.cond_latent)
-    time_vector = dit.time_vector(1.0)
+    t, dt, evaluate = oracle_lib.euler_schedule(config.steps, config.sway, config.skip)
     start = time.perf_counter()
-    dit.eval(inputs.mu, cond, inputs.noise, time_vector)
+    dit.patch(inputs.mu, inputs.cond_latent, inputs.noise, t, dt, evaluate, config.cfg,
+              config.zero_star)
     seconds = time.perf_counter() - start
-    log(f"CPU oracle: one DiT evaluation {seconds * 1e3:.0f} ms on {threads} threads")
-    return {"us_per_patch": round(seconds * 10 * 1e6, 1), "cores": threads,
-            "sample": "one evaluation x 10"}
+    log(f"CPU oracle: one 10-step patch {seconds * 1e3:.0f} ms on {threads} threads")
+    return {"us_per_patch": round(seconds * 1e6, 1), "cores": threads,
+            "sample": f"one whole patch ({int(np.sum(evaluate))} evaluations), timed once"}
 
 
 def main() -> int:
@@ -751,6 +779,8 @@ def main() -> int:
                           / HBM_PEAK_GBS, 4),
             "traffic": round(sum(f * FETCH_SCALE + w for f, w in TRAFFIC_KIB.values())
                              * 1024 / len(TRAFFIC_KIB)),
+            "traffic_source": "profiles/q8_skinny_m22_traffic.md, rocprofv3 PMC on the "
+                              f"build of commit {TRAFFIC_BUILD}",
             "kernel": "EngineKernel<2, RG, kRowMajor, kStore, 1, 3> "
                       "(voxcpm_amd/csrc/q8_tile.hpp) via vx_q8_linear",
             "launch_bytes": products["launch_bytes"],
@@ -765,6 +795,7 @@ def main() -> int:
         "cpu_baseline": baseline,
         "read_probe_gbs": round(probe, 1),
         "sweep": products["sweep"],
+        "single_product": products["single"],
         "lm_decode": lm,
         "vae_decode": vae,
         "bf16_weights": bf16,

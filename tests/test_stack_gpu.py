@@ -57,11 +57,13 @@ def test_split_attention_against_oracle(vx, oracle, cuda, stream, heads, kv_head
     assert diff.max() <= 1, f"max {diff.max()} ulp"
 
 
-def make_stack(vx, oracle, config, seed, bf16_weights=False):
+def make_stack(vx, oracle, config, seed, bf16_weights=False, positions=2048):
+    """`positions`: rows of the rotary table; every position a step uses
+    must index it (the kernels read row `position` of the table)."""
     rope = None
     if config.rope:
         rope = oracle.rope_table(config.rope_theta, config.head_dim, config.rope_factors,
-                                 config.rope_scaling, 2048)
+                                 config.rope_scaling, positions)
     weights = synth.stack_weights(config, seed)
     return (vx.Stack(weights, rope, bf16_weights=bf16_weights),
             oracle.OracleStack(weights, rope, threads=16, bf16_weights=bf16_weights))
@@ -77,7 +79,10 @@ class Run:
     """One stack on the GPU and in the oracle with the same cache history."""
 
     def __init__(self, vx, oracle, cuda, config, seed, capacity, bf16_weights=False):
-        self.gpu, self.cpu = make_stack(vx, oracle, config, seed, bf16_weights)
+        # Positions here are cache rows, so a table of `capacity` rows
+        # covers every step.
+        self.gpu, self.cpu = make_stack(vx, oracle, config, seed, bf16_weights,
+                                        positions=max(2048, capacity))
         self.config = config
         self.k_gpu, self.v_gpu = self.gpu.cache(capacity)
         shape = (config.layers, config.kv_heads, capacity, config.head_dim)
@@ -255,6 +260,7 @@ def test_stack_decode_replays_past_4096(vx, oracle, cuda, stream):
     position = torch.empty(1, dtype=torch.int32, device=cuda)
     run.gpu.set_path(_lib.STACK_PATH_AUTO)
     for past in range(filled, filled + 8):  # 4095 .. 4102 keys: 64 -> 65 chunks
+        assert past < capacity  # the position indexes the cache and the rotary table
         h = rng.normal(config.hidden).astype(np.float32).reshape(1, config.hidden)
         hidden.copy_(torch.from_numpy(h))
         position.fill_(past)
