@@ -109,6 +109,19 @@ int vx_q8_linear_bf16(const uint16_t* x, const void* packed, uint16_t* y,
                       size_t m, size_t k, size_t n, vx_scratch* scratch,
                       void* stream);
 
+/* vx_q8_linear for callers that cannot allocate (code under HIP graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc): no
+ * counterpart in the reference. It allocates nothing and takes no
+ * vx_scratch: the k-split partial sums of products of more than 128 rows
+ * live in a static 12 MiB device array per GPU (held until the process
+ * ends). Same arguments and results as vx_q8_linear with a scratch, bit for
+ * bit; VX_BAD_ARG when a product's split would need more than the array
+ * holds. Every call on one GPU shares that GPU's array, so calls that
+ * overlap on one GPU (two streams at once) race. */
+int vx_q8_linear_noalloc(const uint16_t* x, const void* packed, float* y,
+                         size_t m, size_t k, size_t n, int accumulate,
+                         void* stream);
+
 /* ------------------------------------------------------------------------
  * bfloat16 weights (the HF checkpoint's format): the same products on bf16
  * W, as panels (16 rows x 64 columns per 2048-byte unit, the two 32-column

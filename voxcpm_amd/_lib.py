@@ -119,6 +119,8 @@ _SIGNATURES = {
     "vx_scratch_destroy": ([c_void_p], None),
     "vx_q8_linear": ([c_void_p, c_void_p, c_void_p, c_size, c_size, c_size,
                       c_int, c_void_p, c_void_p], c_int),
+    "vx_q8_linear_noalloc": ([c_void_p, c_void_p, c_void_p, c_size, c_size, c_size,
+                              c_int, c_void_p], c_int),
     "vx_q8_linear_bf16": ([c_void_p, c_void_p, c_void_p, c_size, c_size,
                            c_size, c_void_p, c_void_p], c_int),
     "vx_q8_linear_planned": ([c_void_p, c_void_p, c_void_p, c_size, c_size,

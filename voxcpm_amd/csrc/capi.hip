@@ -80,6 +80,10 @@ bool Aligned(const void* pointer, std::size_t bytes) {
   return reinterpret_cast<std::uintptr_t>(pointer) % bytes == 0;
 }
 
+}  // namespace
+
+namespace vx {
+
 int CheckProduct(const void* x, const void* w, const void* y, std::size_t m,
                  std::size_t k, std::size_t n, const char* what) {
   if (x == nullptr || w == nullptr || y == nullptr)
@@ -98,6 +102,12 @@ int CheckProduct(const void* x, const void* w, const void* y, std::size_t m,
                                         "aligned");
   return VX_OK;
 }
+
+}  // namespace vx
+
+namespace {
+
+using vx::CheckProduct;
 
 int Product(const uint16_t* x, const void* packed, float* y, uint16_t* y_bf16,
             size_t m, size_t k, size_t n, int accumulate, vx_scratch* scratch,

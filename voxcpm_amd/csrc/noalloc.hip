@@ -1,0 +1,87 @@
+// The Q8_0 product for callers that cannot allocate (code under HIP graph
+// capture, serving loops, harnesses that forbid hipMalloc): vx_q8_linear
+// with its split scratch in a file-scope device array instead of a
+// vx_scratch.
+//
+// The array is `scratch` below. Its name in host code is a host-side
+// stand-in, not a device address: each device's address comes from
+// hipGetSymbolAddress, taken once per device (with that device current) on
+// the first call there, and only that address reaches the kernels. Every
+// call on a device shares the device's array; the products write every
+// partial sum they later read, so nothing needs clearing between calls,
+// and calls that overlap on one device (two streams at once) race.
+#include <hip/hip_runtime.h>
+
+#include <array>
+#include <cstdint>
+#include <mutex>
+#include <string>
+
+#include "common.hpp"
+#include "products.hpp"
+#include "q8.hpp"
+
+/// Floats of the array: the k splits of the tiled product (m > 128) store
+/// splits x m x n partial sums here. 12 MiB per device, what the planner's
+/// largest split needs (384 workgroups of 64 x 128 outputs).
+constexpr std::size_t kScratchFloats = std::size_t{3} << 20;
+
+static __device__ __align__(256) float scratch[kScratchFloats];
+
+namespace {
+
+constexpr int kMaxDevices = 64;
+
+struct DeviceScratch {
+  std::once_flag once;
+  hipError_t status = hipSuccess;
+  float* address = nullptr;
+};
+
+std::array<DeviceScratch, kMaxDevices> devices;
+
+/// The current device's address of `scratch` (nullptr and a failed status
+/// when it cannot be had).
+int ScratchAddress(float** address) {
+  int device = 0;
+  VX_HIP(hipGetDevice(&device), "vx_q8_linear_noalloc: hipGetDevice");
+  if (device < 0 || device >= kMaxDevices)
+    return vx::Fail(VX_UNSUPPORTED, "vx_q8_linear_noalloc: device index past 63");
+  DeviceScratch& entry = devices[static_cast<std::size_t>(device)];
+  std::call_once(entry.once, [&entry] {
+    void* found = nullptr;
+    entry.status = hipGetSymbolAddress(&found, HIP_SYMBOL(scratch));
+    entry.address = static_cast<float*>(found);
+  });
+  if (entry.status != hipSuccess || entry.address == nullptr)
+    return vx::FailHip(entry.status != hipSuccess ? entry.status : hipErrorInvalidSymbol,
+                       "vx_q8_linear_noalloc: hipGetSymbolAddress");
+  *address = entry.address;
+  return VX_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int vx_q8_linear_noalloc(const uint16_t* x, const void* packed, float* y, size_t m,
+                         size_t k, size_t n, int accumulate, void* stream) {
+  VX_TRY(vx::CheckProduct(x, packed, y, m, k, n, "vx_q8_linear_noalloc"));
+  if (m <= vx::kExactRows)  // these plans split nothing over workgroups
+    return vx_q8_linear(x, packed, y, m, k, n, accumulate, nullptr, stream);
+  // The partial sums of the split the planner picks with unlimited room
+  // must fit the array.
+  const vx::TiledPlan plan = vx::PlanTiled(m, k, n, SIZE_MAX);
+  const std::size_t need =
+      plan.splits > 1 ? static_cast<std::size_t>(plan.splits) * m * n : 0;
+  if (need > kScratchFloats)
+    return vx::Fail(VX_BAD_ARG, "vx_q8_linear_noalloc: the product's split needs " +
+                                    std::to_string(need) + " floats of scratch, the static " +
+                                    "scratch holds " + std::to_string(kScratchFloats));
+  float* address = nullptr;
+  VX_TRY(ScratchAddress(&address));
+  return vx::RunTiled(x, packed, y, nullptr, m, k, n, accumulate != 0,
+                      vx::TiledMode::kQ8Expanded, address, kScratchFloats, vx::Stream(stream));
+}
+
+}  // extern "C"

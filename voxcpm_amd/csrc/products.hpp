@@ -61,6 +61,26 @@ int RunSkinny(const Bf16* x, const void* w, float* y, Bf16* y_bf16,
 /// arithmetic beyond 128 rows), or bf16 panels.
 enum class TiledMode : int { kQ8Exact = 0, kQ8Expanded = 1, kBf16 = 2 };
 
+/// VX_OK, or VX_BAD_ARG (with the message) for product arguments the
+/// kernels cannot take: null pointers, m, n or k zero, k not a multiple of
+/// 32, shapes past the kernels' 32-bit offsets, x or the weights not 16-byte
+/// aligned. `what` names the entry point in the message.
+int CheckProduct(const void* x, const void* w, const void* y, std::size_t m, std::size_t k,
+                 std::size_t n, const char* what);
+
+/// The tiled product's launch shape: `bm` activation rows per tile,
+/// `m_tiles` row tiles, `splits` workgroups along k (their partial sums
+/// need splits m n floats of scratch when splits > 1).
+struct TiledPlan {
+  int bm = 64;
+  int m_tiles = 1;
+  int splits = 1;
+};
+
+/// The tiled plan of an m x k x n product whose scratch holds
+/// `partial_floats` floats of partial sums.
+TiledPlan PlanTiled(std::size_t m, std::size_t k, std::size_t n, std::size_t partial_floats);
+
 /// Launches the LDS-tiled product (q8_tiled.hip; meant for m > 32). Small
 /// grids split k over workgroups when `partials` holds partial_floats >=
 /// 2 m n floats (a second launch adds the splits in order).

@@ -348,6 +348,28 @@ using Large = TileShape<128, 4, 2, 1>;
 
 }  // namespace
 
+TiledPlan PlanTiled(std::size_t m, std::size_t k, std::size_t n, std::size_t partial_floats) {
+  TiledPlan plan;
+  const std::size_t n_tiles = (n + kTileN - 1) / kTileN;
+  const std::size_t pairs = q8::Pairs(k);
+  // 128-row tiles (8 waves of 32 x 64) once they give at least 192
+  // workgroups, else 64-row tiles (4 waves, two workgroups per compute
+  // unit): the faster of the two at every prefill shape measured on MI355X.
+  const std::size_t tiles128 = (m + 127) / 128 * n_tiles;
+  plan.bm = m > 64 && tiles128 >= 192 ? 128 : 64;
+  plan.m_tiles = static_cast<int>((m + plan.bm - 1) / plan.bm);
+  // Grids of at most 144 tiles split k (powers of two, at least four
+  // steps each, up to 384 workgroups) when the scratch holds the partial
+  // sums: measured faster on MI355X there, slower on larger grids, where
+  // the second launch costs more than the parallelism gains.
+  plan.splits = 1;
+  const std::size_t tiles = static_cast<std::size_t>(plan.m_tiles) * n_tiles;
+  while (tiles <= 144 && tiles * 2 * plan.splits <= 384 && pairs >= 8U * plan.splits &&
+         2 * plan.splits * m * n <= partial_floats)
+    plan.splits *= 2;
+  return plan;
+}
+
 int RunTiled(const Bf16* x, const void* w, float* y, Bf16* y_bf16, std::size_t m,
              std::size_t k, std::size_t n, bool accumulate, TiledMode mode,
              float* partials, std::size_t partial_floats, hipStream_t stream) {
@@ -363,21 +385,10 @@ int RunTiled(const Bf16* x, const void* w, float* y, Bf16* y_bf16, std::size_t m
   args.groups = static_cast<int>(q8::Groups(n));
   args.n_tiles = static_cast<int>((n + kTileN - 1) / kTileN);
   args.accumulate = accumulate ? 1 : 0;
-  // 128-row tiles (8 waves of 32 x 64) once they give at least 192
-  // workgroups, else 64-row tiles (4 waves, two workgroups per compute
-  // unit): the faster of the two at every prefill shape measured on MI355X.
-  const std::size_t tiles128 = (m + 127) / 128 * static_cast<std::size_t>(args.n_tiles);
-  const int bm = m > 64 && tiles128 >= 192 ? 128 : 64;
-  args.m_tiles = static_cast<int>((m + bm - 1) / bm);
-  // Grids of at most 144 tiles split k (powers of two, at least four
-  // steps each, up to 384 workgroups) when the scratch holds the partial
-  // sums: measured faster on MI355X there, slower on larger grids, where
-  // the second launch costs more than the parallelism gains.
-  args.splits = 1;
-  const std::size_t tiles = static_cast<std::size_t>(args.m_tiles) * args.n_tiles;
-  while (tiles <= 144 && tiles * 2 * args.splits <= 384 && args.pairs >= 8 * args.splits &&
-         2 * args.splits * m * n <= partial_floats)
-    args.splits *= 2;
+  const TiledPlan plan = PlanTiled(m, k, n, partial_floats);
+  const int bm = plan.bm;
+  args.m_tiles = plan.m_tiles;
+  args.splits = plan.splits;
   args.pairs_per_split = (args.pairs + args.splits - 1) / args.splits;
   args.partials = partials;
   switch (mode) {
