@@ -37,6 +37,12 @@ SWEEP_ROWS = [1, 2, 22, 44, 128]
 ROWS = 22
 ROTATION_BYTES = 1.1e9
 BF16_PEAK_TFLOPS = 2500.0
+# MFMA utilisation read from rocprofv3 counters for the prefill kernel
+# (SQ_VALU_MFMA_BUSY_CYCLES over the SIMDs' cycles), next to the
+# wall-clock mfma_frac of each prefill row; profiles/q8_gemm_prefill.md.
+PREFILL_MFMA_BUSY = {"source": "profiles/q8_gemm_prefill.md (rocprofv3 --pmc "
+                               "SQ_VALU_MFMA_BUSY_CYCLES, GRBM_GUI_ACTIVE)",
+                     "m512_n16384": 0.283, "m1024_n16384": 0.325}
 # HBM bytes per launch of the M=22 sweep kernels from two rocprofv3 PMC runs
 # (profiles/q8_skinny_m22_traffic.md): FETCH_SIZE KiB (scaled by 2.0, its
 # reading of a 256 MiB copy of known size) + WRITE_SIZE KiB (scale 1.0).
@@ -495,12 +501,34 @@ def gpu_prefill(args, torch, ops, synth, device, stream):
             tflops = 2.0 * m * n * k / seconds / 1e12
             rows.append({"m": m, "k": k, "n": n, "us": round(seconds * 1e6, 2),
                          "tflops": round(tflops, 1),
-                         "mfma_frac": round(tflops / BF16_PEAK_TFLOPS, 4)})
+                         "mfma_frac": round(tflops / BF16_PEAK_TFLOPS, 4),
+                         # vx_q8_linear's dispatch (products.hpp UseGemm)
+                         "kernel": "GemmKernel (q8_gemm.hip)" if m >= 512 and n >= 6144
+                                   else "TiledKernel (q8_tiled.hip)"})
             log(f"  prefill M={m} K={k} N={n}: {seconds * 1e6:.1f} us, {tflops:.1f} TFLOP/s")
             del g
         del pool, packed
     torch.cuda.empty_cache()
     return rows
+
+
+def prefill_workload(torch, ops, synth, device, stream) -> None:
+    """Eager launches for counter runs of the prefill kernel: five products
+    each at m = 512 and 1024 rows, k 2048, n 16384 (the MFMA-bound end of
+    the prefill sweep), weights rotated over four copies."""
+    k, n = PREFILL_K, 16384
+    rng = synth.Rng(7, n)
+    packed = ops.q8_pack(torch.from_numpy(synth.q8_blocks(rng, n, k)).to(device), n, k)
+    pool = packed.repeat(4).view(4, -1)
+    scratch = ops.Scratch(128, 16384)
+    for m in (512, 1024):
+        x = torch.from_numpy(synth.activations(rng, m, k).view(np.int16)).to(
+            device).view(torch.bfloat16)
+        y = torch.empty((m, n), dtype=torch.float32, device=device)
+        for i in range(5):
+            ops.q8_linear(x, pool[i % 4], n, y=y, scratch=scratch)
+        torch.cuda.synchronize()
+        log(f"prefill workload M={m} K={k} N={n}: 5 launches")
 
 
 def pmc_workload(torch, ops, synth, device, stream) -> None:
@@ -702,6 +730,8 @@ def main() -> int:
                         help="skip the prefill-sized products")
     parser.add_argument("--pmc-workload", action="store_true",
                         help="only run the eager launches that counter runs read")
+    parser.add_argument("--prefill-workload", action="store_true",
+                        help="only run eager prefill products (for counter runs)")
     parser.add_argument("--lm-step-workload", action="store_true",
                         help="only run the stacks' decode steps and the AudioVAE "
                              "(for kernel traces)")
@@ -725,6 +755,9 @@ def main() -> int:
     log(f"device {torch.cuda.get_device_properties(0).gcnArchName}")
     if args.pmc_workload:
         pmc_workload(torch, ops, synth, device, stream)
+        return 0
+    if args.prefill_workload:
+        prefill_workload(torch, ops, synth, device, stream)
         return 0
     if args.lm_step_workload:
         gpu_lm_step(args, torch, ops, synth, device, stream)
@@ -800,6 +833,7 @@ def main() -> int:
         "vae_decode": vae,
         "bf16_weights": bf16,
         "prefill": prefill,
+        "prefill_mfma_busy_counters": PREFILL_MFMA_BUSY,
         "patch": patch,
     }
     print(json.dumps(line), flush=True)

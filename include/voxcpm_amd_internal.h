@@ -24,6 +24,28 @@ int vx_q8_linear_planned(const uint16_t* x, const void* packed, float* y,
                          vx_scratch* scratch, int row_groups, int waves,
                          int splits, void* stream);
 
+/* vx_q8_linear's engine (the one-pass skinny kernel) with a forced plan,
+ * 17..32 rows, y = x W^T: `row_groups` row groups per workgroup (1, 2,
+ * 4), `waves` waves per workgroup (4, 8, 16; 16 only up to 2 row groups),
+ * `pairs_per_wave` pairs of k per wave per pass (1, 2), `row_blocks`
+ * blocks of rows per tile (1..4); VX_UNSUPPORTED otherwise. The plan
+ * search behind the default plans, as the reference's PlanWmma is forced
+ * through target_waves (kernels/wmma_products.hpp:82-85). */
+int vx_q8_linear_engine(const uint16_t* x, const void* packed, float* y,
+                        size_t m, size_t k, size_t n, int row_groups,
+                        int waves, int pairs_per_wave, int row_blocks,
+                        void* stream);
+
+/* The prefill product (more than 128 rows, Q8_0 panels expanded) with a
+ * forced plan: tile `shape` 0 (256 x 256, one step prefetched), 1
+ * (128 x 256), 2 (128 x 128), 3 (256 x 128), 4 (256 x 256, two steps),
+ * 5 (128 x 64), k split over `splits` workgroups (the scratch must hold
+ * splits m n floats when splits > 1). VX_UNSUPPORTED for other shapes. The
+ * plan search behind vx_q8_linear's prefill plans. */
+int vx_q8_linear_gemm(const uint16_t* x, const void* packed, float* y,
+                      size_t m, size_t k, size_t n, int shape, int splits,
+                      vx_scratch* scratch, void* stream);
+
 /* The default plan of an m x k x n product (m <= 128):
  * out7 = {activation tiles, row groups per workgroup, waves per workgroup,
  * workgroup tiles, splits, pairs per split, pairs per wave}. Counterpart of

@@ -160,6 +160,39 @@ def test_split_counters_reset(vx, oracle, cuda, stream):
     assert np.array_equal(third, fourth)
 
 
+@pytest.mark.parametrize("rows", [17, 22, 32])
+def test_forced_engine_plans(vx, oracle, cuda, stream, rows):
+    """The engine with forced plans (vx_q8_linear_engine: row groups, waves,
+    pairs per wave, row blocks), the plan search behind the default plans:
+    every plan within 1e-5 of sum |x w| and equal to the default plan's
+    result to float32 rounding."""
+    from voxcpm_amd import _lib
+    k, n = 2048, 1040  # 65 row groups: a ragged last workgroup for 2 and 4
+    rng = synth.Rng(78, rows)
+    blocks = reference_weights(rng, n, k)
+    packed = vx.q8_pack(to_device(blocks, cuda), n, k)
+    x = reference_activations(rng, rows, k)
+    x_dev = to_device(x, cuda)
+    default = run_product(vx, x_dev, packed, n, None, None, None, cuda)
+    handle = torch.cuda.current_stream().cuda_stream
+    for rg, waves, pw, blocks_ in [(1, 16, 1, 1), (2, 8, 2, 2), (4, 8, 1, 4), (1, 4, 2, 3),
+                                   (2, 16, 2, 1), (4, 4, 1, 2)]:
+        y = torch.full((rows, n), float("nan"), dtype=torch.float32, device=cuda)
+        _lib.check(_lib.lib().vx_q8_linear_engine(x_dev.data_ptr(), packed.data_ptr(),
+                                                  y.data_ptr(), rows, k, n, rg, waves, pw,
+                                                  blocks_, handle))
+        torch.cuda.synchronize()
+        got = y.cpu().numpy()
+        worst = oracle.q8_check(got, x, blocks)
+        assert worst <= LIMIT, f"plan {(rg, waves, pw, blocks_)}: {worst:.3e}"
+        assert np.abs(got - default).max() <= 1e-5 * np.abs(default).max()
+    y = torch.empty((rows, n), dtype=torch.float32, device=cuda)
+    with pytest.raises(_lib.VxError) as info:  # 16 waves of 4 row groups: no such kernel
+        _lib.check(_lib.lib().vx_q8_linear_engine(x_dev.data_ptr(), packed.data_ptr(),
+                                                  y.data_ptr(), rows, k, n, 4, 16, 1, 1, handle))
+    assert info.value.status == _lib.VX_UNSUPPORTED
+
+
 @pytest.mark.parametrize("rows", [33, 44, 64, 100, 128])
 def test_products_beyond_32_rows(vx, oracle, cuda, stream, rows):
     """33..128 rows stay exact (the reference's chunks of 32, gemm.cpp:272)."""

@@ -113,6 +113,11 @@ int Product(const uint16_t* x, const void* packed, float* y, uint16_t* y_bf16,
             size_t m, size_t k, size_t n, int accumulate, vx_scratch* scratch,
             int rg, int waves, int splits, void* stream,
             vx::q8::Weights kind = vx::q8::Weights::kQ8) {
+  if (m > vx::kExactRows && vx::UseGemm(m, n))
+    return vx::RunGemm(x, packed, y, y_bf16, m, k, n, accumulate != 0,
+                       kind != vx::q8::Weights::kQ8,
+                       scratch != nullptr ? scratch->partials : nullptr,
+                       scratch != nullptr ? scratch->partial_floats : 0, vx::Stream(stream));
   if (m > vx::kExactRows)
     return vx::RunTiled(x, packed, y, y_bf16, m, k, n, accumulate != 0,
                         kind == vx::q8::Weights::kQ8 ? vx::TiledMode::kQ8Expanded
@@ -233,6 +238,28 @@ int vx_q8_linear_planned(const uint16_t* x, const void* packed, float* y,
                     "vx_q8_linear_planned: plans apply to m <= 128");
   return Product(x, packed, y, nullptr, m, k, n, accumulate, scratch,
                  row_groups, waves, splits, stream);
+}
+
+/* Testing and tuning entry: the engine with a forced plan (17..32 rows). */
+int vx_q8_linear_engine(const uint16_t* x, const void* packed, float* y, size_t m, size_t k,
+                        size_t n, int row_groups, int waves, int pairs_per_wave,
+                        int row_blocks, void* stream) {
+  VX_TRY(CheckProduct(x, packed, y, m, k, n, "vx_q8_linear_engine"));
+  return vx::RunEngineTuned(x, packed, y, m, k, n, row_groups, waves, pairs_per_wave,
+                            row_blocks, vx::Stream(stream));
+}
+
+/* Testing and tuning entry: the prefill product (m > 128) with a forced
+ * tile shape and split. */
+int vx_q8_linear_gemm(const uint16_t* x, const void* packed, float* y, size_t m, size_t k,
+                      size_t n, int shape, int splits, vx_scratch* scratch, void* stream) {
+  VX_TRY(CheckProduct(x, packed, y, m, k, n, "vx_q8_linear_gemm"));
+  if (m <= vx::kExactRows || shape < 0)
+    return vx::Fail(VX_BAD_ARG, "vx_q8_linear_gemm: more than 128 rows and a shape");
+  return vx::RunGemm(x, packed, y, nullptr, m, k, n, false, false,
+                     scratch != nullptr ? scratch->partials : nullptr,
+                     scratch != nullptr ? scratch->partial_floats : 0, vx::Stream(stream),
+                     shape, splits);
 }
 
 int vx_test_pack_bf16(const float* input, uint16_t* output, size_t n,

@@ -21,10 +21,10 @@
 #include "products.hpp"
 #include "q8.hpp"
 
-/// Floats of the array: the k splits of the tiled product (m > 128) store
-/// splits x m x n partial sums here. 12 MiB per device, what the planner's
-/// largest split needs (384 workgroups of 64 x 128 outputs).
-constexpr std::size_t kScratchFloats = std::size_t{3} << 20;
+/// Floats of the array: the k splits of the prefill products (m > 128)
+/// store splits x m x n partial sums here. 12 MiB per device: every default
+/// plan keeps its splits' partial sums within it.
+constexpr std::size_t kScratchFloats = vx::kMaxSplitFloats;
 
 static __device__ __align__(256) float scratch[kScratchFloats];
 
@@ -71,15 +71,23 @@ int vx_q8_linear_noalloc(const uint16_t* x, const void* packed, float* y, size_t
     return vx_q8_linear(x, packed, y, m, k, n, accumulate, nullptr, stream);
   // The partial sums of the split the planner picks with unlimited room
   // must fit the array.
-  const vx::TiledPlan plan = vx::PlanTiled(m, k, n, SIZE_MAX);
-  const std::size_t need =
-      plan.splits > 1 ? static_cast<std::size_t>(plan.splits) * m * n : 0;
+  std::size_t need = 0;
+  if (vx::UseGemm(m, n)) {
+    const vx::GemmPlan plan = vx::PlanGemm(m, k, n, SIZE_MAX);
+    need = plan.splits > 1 ? static_cast<std::size_t>(plan.splits) * m * n : 0;
+  } else {
+    const vx::TiledPlan plan = vx::PlanTiled(m, k, n, SIZE_MAX);
+    need = plan.splits > 1 ? static_cast<std::size_t>(plan.splits) * m * n : 0;
+  }
   if (need > kScratchFloats)
     return vx::Fail(VX_BAD_ARG, "vx_q8_linear_noalloc: the product's split needs " +
                                     std::to_string(need) + " floats of scratch, the static " +
                                     "scratch holds " + std::to_string(kScratchFloats));
   float* address = nullptr;
   VX_TRY(ScratchAddress(&address));
+  if (vx::UseGemm(m, n))
+    return vx::RunGemm(x, packed, y, nullptr, m, k, n, accumulate != 0, false, address,
+                       kScratchFloats, vx::Stream(stream));
   return vx::RunTiled(x, packed, y, nullptr, m, k, n, accumulate != 0,
                       vx::TiledMode::kQ8Expanded, address, kScratchFloats, vx::Stream(stream));
 }

@@ -56,6 +56,48 @@ int RunSkinny(const Bf16* x, const void* w, float* y, Bf16* y_bf16,
               const ProductPlan& plan, float* partials, unsigned* counters,
               hipStream_t stream, q8::Weights kind = q8::Weights::kQ8);
 
+/// The engine on 17..32 row-major rows with a forced plan (tuning and
+/// tests): `rg` row groups per workgroup (1, 2, 4), `waves` waves (4, 8,
+/// 16), `pw` pairs per wave per pass (1, 2), `row_blocks` (1..4).
+int RunEngineTuned(const Bf16* x, const void* w, float* y, std::size_t m, std::size_t k,
+                   std::size_t n, int rg, int waves, int pw, int row_blocks,
+                   hipStream_t stream);
+
+/// Most floats of split partial sums any default plan uses (12 MiB): the
+/// products' k splits stay within it, so that a static scratch of this size
+/// serves every product (vx_q8_linear_noalloc).
+constexpr std::size_t kMaxSplitFloats = std::size_t{3} << 20;
+
+/// Whether an m > 128 product takes the 32 x 32 MFMA kernel (q8_gemm.hip)
+/// rather than the tiled kernel (q8_tiled.hip), which measured faster on the
+/// smaller, latency-bound prefill shapes.
+bool UseGemm(std::size_t m, std::size_t n);
+
+/// The prefill product's launch shape (q8_gemm.hip): `shape` 0 (256 x 256
+/// tiles), 1 (128 x 256) or 2 (128 x 128), `tiles` workgroup tiles,
+/// `splits` workgroups along k (their partial sums need splits m n floats
+/// of scratch when splits > 1).
+struct GemmPlan {
+  int shape = 2;
+  int bm = 128;
+  int bn = 128;
+  int tiles = 1;
+  int splits = 1;
+};
+
+/// The prefill plan of an m x k x n product whose scratch holds
+/// `partial_floats` floats of partial sums.
+/// A non-negative `shape` (0..5) forces that tile shape with `splits` splits.
+GemmPlan PlanGemm(std::size_t m, std::size_t k, std::size_t n, std::size_t partial_floats,
+                  int shape = -1, int splits = 1);
+
+/// The prefill product (m > 128) on the 32 x 32 x 16 matrix cores: Q8_0
+/// panels expanded to bf16(scale * q) (gemm.cpp:305-312) or bf16 panels,
+/// float32 sums over k; y (+)= x W^T, or its bf16 rounding into y_bf16.
+int RunGemm(const Bf16* x, const void* w, float* y, Bf16* y_bf16, std::size_t m, std::size_t k,
+            std::size_t n, bool accumulate, bool bf16_weights, float* partials,
+            std::size_t partial_floats, hipStream_t stream, int shape = -1, int splits = 1);
+
 /// What the tiled kernel multiplies: Q8_0 panels with the exact per-block
 /// arithmetic, Q8_0 panels expanded to bf16(scale * q) (the reference's
 /// arithmetic beyond 128 rows), or bf16 panels.

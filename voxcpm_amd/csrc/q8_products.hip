@@ -374,6 +374,53 @@ EngineLauncher PickEngineFor(int mt, int rg, int pw, int m) {
   }
 }
 
+// ---- forced engine plans (tuning) ----------------------------------------------
+
+template<int RG, int PW, int NW, int JR>
+void LaunchTuned(const q8::TileArgs& args, int tiles, hipStream_t stream) {
+  const std::size_t shared = q8::EngineShared(2, RG, NW, q8::ASource::kRowMajor);
+  q8::EngineKernel<2, RG, q8::ASource::kRowMajor, q8::Output::kStore, PW, JR, q8::Weights::kQ8,
+                   NW><<<tiles * args.row_blocks, NW * kWave, shared, stream>>>(args);
+}
+
+using TunedLauncher = void (*)(const q8::TileArgs&, int, hipStream_t);
+
+template<int RG, int PW, int NW>
+TunedLauncher TunedJr(int m) {
+  return m <= 24 ? LaunchTuned<RG, PW, NW, 3> : LaunchTuned<RG, PW, NW, 4>;
+}
+
+template<int RG, int PW>
+TunedLauncher TunedNw(int waves, int m) {
+  switch (waves) {
+    case 4: return TunedJr<RG, PW, 4>(m);
+    case 8: return TunedJr<RG, PW, 8>(m);
+    case 16:
+      if constexpr (RG <= 2)
+        return TunedJr<RG, PW, 16>(m);
+      return nullptr;
+    default: return nullptr;
+  }
+}
+
+template<int RG>
+TunedLauncher TunedPw(int pw, int waves, int m) {
+  switch (pw) {
+    case 1: return TunedNw<RG, 1>(waves, m);
+    case 2: return TunedNw<RG, 2>(waves, m);
+    default: return nullptr;
+  }
+}
+
+TunedLauncher PickTuned(int rg, int pw, int waves, int m) {
+  switch (rg) {
+    case 1: return TunedPw<1>(pw, waves, m);
+    case 2: return TunedPw<2>(pw, waves, m);
+    case 4: return TunedPw<4>(pw, waves, m);
+    default: return nullptr;
+  }
+}
+
 /// bf16 rows [n][k] are read by the staged engine only (m <= 32).
 EngineLauncher PickEngine(int mt, int rg, int pw, int m, q8::Weights kind) {
   switch (kind) {
@@ -558,6 +605,30 @@ int RunSkinny(const Bf16* x, const void* w, float* y, Bf16* y_bf16,
   args.accumulate = accumulate ? 1 : 0;
   launch(args, plan, stream);
   return LaunchStatus("q8 product");
+}
+
+int RunEngineTuned(const Bf16* x, const void* w, float* y, std::size_t m, std::size_t k,
+                   std::size_t n, int rg, int waves, int pw, int row_blocks,
+                   hipStream_t stream) {
+  if (m <= 16 || m > 32)
+    return Fail(VX_UNSUPPORTED, "tuned engine plans take 17..32 rows");
+  const TunedLauncher launch = PickTuned(rg, pw, waves, static_cast<int>(m));
+  if (launch == nullptr || row_blocks < 1 || row_blocks > 4)
+    return Fail(VX_UNSUPPORTED, "no tuned engine for this plan");
+  q8::TileArgs args{};
+  args.w = static_cast<const std::uint8_t*>(w);
+  args.m = static_cast<int>(m);
+  args.k = static_cast<int>(k);
+  args.n = static_cast<int>(n);
+  args.pairs = static_cast<int>(q8::Pairs(k));
+  args.groups = static_cast<int>(q8::Groups(n));
+  args.group_stride = 1;
+  args.row_blocks = row_blocks;
+  args.rows_per_block = static_cast<int>((m + row_blocks - 1) / row_blocks);
+  args.x = x;
+  args.y = y;
+  launch(args, (args.groups + rg - 1) / rg, stream);
+  return LaunchStatus("tuned q8 product");
 }
 
 }  // namespace vx

@@ -262,7 +262,7 @@ struct PairStage {
 /// block's MFMA straight into the sums, as the reference's bf16 products do
 /// (kernels/wmma_products.hip:210-213).
 template<int MT, int RG, ASource SRC, Output OUT, int PW = 1, int JR = 2 * MT,
-         Weights WK = Weights::kQ8>
+         Weights WK = Weights::kQ8, int NW = 0>
 __device__ __forceinline__ void EngineBody(const TileArgs& a) {
   // One 16-row tile of a fragment-order source per workgroup.
   constexpr bool kOneTile = MT == 1 && SRC == ASource::kFragBf16;
@@ -276,7 +276,8 @@ __device__ __forceinline__ void EngineBody(const TileArgs& a) {
   extern __shared__ float lds[];
   const int lane = threadIdx.x % kWave;
   const int wave = threadIdx.x / kWave;
-  constexpr int waves = EngineThreads(MT, RG) / kWave;
+  // NW > 0: a workgroup of NW waves instead of EngineThreads(MT, RG).
+  constexpr int waves = NW > 0 ? NW : EngineThreads(MT, RG) / kWave;
   const int r16 = lane % 16;
   const int octet = lane / 16;
   const int tiles = static_cast<int>(gridDim.x) / a.row_blocks;
@@ -296,6 +297,11 @@ __device__ __forceinline__ void EngineBody(const TileArgs& a) {
     row_hi = min(a.m, row_lo + a.rows_per_block);
   }
   const auto in_rows = [&](int row) { return row >= row_lo && row < row_hi; };
+  // The workgroup's first activation row: its 16-row tile of a fragment
+  // source, or the first row of its block for one-tile row-major
+  // activations (the block's rows are then the tile's, at most 16).
+  constexpr bool kBlockTile = SRC == ASource::kRowMajor && MT == 1;
+  const int row_base = kBlockTile ? row_lo : 16 * tile_base;
   const int k_blocks = a.k / 32;
 
   constexpr int kUnit = WK == Weights::kQ8 ? kUnitBytes : kBf16UnitBytes;
@@ -310,7 +316,7 @@ __device__ __forceinline__ void EngineBody(const TileArgs& a) {
   bool row_ok[MT];
 #pragma unroll
   for (int t = 0; t < MT; ++t)
-    row_ok[t] = in_rows(16 * (tile_base + t) + r16);
+    row_ok[t] = in_rows(row_base + 16 * t + r16);
   // The activations as buffers: row-major [m][k] bf16, fragment-order bf16
   // (32 rows x pairs x 64 columns), fragment-order float32 or row-major
   // float32 [m][k].
@@ -325,7 +331,7 @@ __device__ __forceinline__ void EngineBody(const TileArgs& a) {
 
   // Output element e of the tile (thread e, e + threads, ...): fragment
   // f = r MT + t, accumulator i, lane l -> (row, column); false past m / n.
-  constexpr int kThreads = EngineThreads(MT, RG);
+  constexpr int kThreads = waves * kWave;
   constexpr int kOutputsPerThread = (RG * MT * 256 + kThreads - 1) / kThreads;
   const auto output_of = [&](int e, int& row, int& column) {
     const int f = e / 256;
@@ -333,7 +339,7 @@ __device__ __forceinline__ void EngineBody(const TileArgs& a) {
     const int l = e % 64;
     const int r = f / MT;
     const int t = f % MT;
-    row = 16 * (tile_base + t) + 4 * (l / 16) + i;
+    row = row_base + 16 * t + 4 * (l / 16) + i;
     const int group = RgGroup(tile, r, a.group_stride, RG);
     column = 16 * group + l % 16;
     return in_rows(row) && group < a.groups && column < a.n;
@@ -393,8 +399,8 @@ __device__ __forceinline__ void EngineBody(const TileArgs& a) {
         uint4 v{0U, 0U, 0U, 0U};
         if constexpr (SRC == ASource::kRowMajor) {
           v = BufferLoad16(x_buffer,
-                           2U * static_cast<std::uint32_t>((16 * t + r16) * a.k + 64 * pair +
-                                                           32 * hf + 8 * octet),
+                           2U * static_cast<std::uint32_t>((row_base + 16 * t + r16) * a.k +
+                                                           64 * pair + 32 * hf + 8 * octet),
                            ok && row_ok[t] && 2 * pair + hf < k_blocks);
         } else if constexpr (SRC == ASource::kFragBf16) {
           v = BufferLoad16(
@@ -424,7 +430,7 @@ __device__ __forceinline__ void EngineBody(const TileArgs& a) {
     const bool column_ok = column < a.k && pair < a.pairs;
 #pragma unroll
     for (int j = 0; j < JR; ++j) {
-      const int row = 8 * j + lane / 8;
+      const int row = row_base + 8 * j + lane / 8;
       raw.v[j] = BufferLoad16(x_buffer, 2U * static_cast<std::uint32_t>(row * a.k + column),
                               column_ok && in_rows(row));
     }
@@ -663,7 +669,10 @@ __device__ __forceinline__ void EngineBody(const TileArgs& a) {
   } else if constexpr (StagesRows(SRC, MT)) {
     // Passes of PW pairs per wave (pair base + p waves + wave), every load
     // of a pass issued before its first product, so that PW pairs per wave
-    // are in flight; plans pick PW so that few passes cover k.
+    // are in flight; plans pick PW so that few passes cover k. (Loading the
+    // next pass before multiplying this one measured slower on MI355X:
+    // 11.3 against 10.9 us at (2048, 16384), and masked loads past k cost
+    // address cycles at one-pass shapes.)
     for (int base = 0; base < a.pairs; base += waves * PW) {
       PairStage<MT, RG> stage[PW];
       RawRows raw[PW];
@@ -764,9 +773,10 @@ __device__ __forceinline__ void EngineBody(const TileArgs& a) {
 }
 
 template<int MT, int RG, ASource SRC, Output OUT, int PW = 1, int JR = 2 * MT,
-         Weights WK = Weights::kQ8>
-__global__ __launch_bounds__(EngineThreads(MT, RG)) void EngineKernel(TileArgs a) {
-  EngineBody<MT, RG, SRC, OUT, PW, JR, WK>(a);
+         Weights WK = Weights::kQ8, int NW = 0>
+__global__ __launch_bounds__(NW > 0 ? NW * kWave : EngineThreads(MT, RG)) void EngineKernel(
+    TileArgs a) {
+  EngineBody<MT, RG, SRC, OUT, PW, JR, WK, NW>(a);
 }
 
 

@@ -364,8 +364,9 @@ TiledPlan PlanTiled(std::size_t m, std::size_t k, std::size_t n, std::size_t par
   // the second launch costs more than the parallelism gains.
   plan.splits = 1;
   const std::size_t tiles = static_cast<std::size_t>(plan.m_tiles) * n_tiles;
+  const std::size_t room = partial_floats < kMaxSplitFloats ? partial_floats : kMaxSplitFloats;
   while (tiles <= 144 && tiles * 2 * plan.splits <= 384 && pairs >= 8U * plan.splits &&
-         2 * plan.splits * m * n <= partial_floats)
+         2 * plan.splits * m * n <= room)
     plan.splits *= 2;
   return plan;
 }
