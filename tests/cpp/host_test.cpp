@@ -1,5 +1,5 @@
-// The C++ host surface (Bf16Gemm::Linear, Generator::Velocity,
-// Generator::Step and ForwardStack over the voxcpm_amd C ABI) against the
+// The C++ host surface (Bf16Gemm::Linear, DitSampler::Velocity,
+// DitSampler::Sample and ForwardStack over the voxcpm_amd C ABI) against the
 // CPU oracle, in the
 // style of the reference's tests/products_test.cpp and
 // tests/generator_test.cpp: random GGML Q8_0 weights, products compared with
@@ -17,7 +17,7 @@
 #include <vector>
 
 #include "../../oracle/oracle.h"
-#include "../../voxcpm_amd/host/generator.hpp"
+#include "../../voxcpm_amd/host/dit_sampler.hpp"
 #include "voxcpm_amd.h"
 
 namespace vc = gufo::models::voxcpm;
@@ -366,12 +366,12 @@ double RelativeMax(const std::vector<float>& a, const std::vector<float>& b) {
   return diff / std::max(scale, 1e-30);
 }
 
-void TestGenerator(Random& rng) {
+void TestDitSampler(Random& rng) {
   SmallDit dit(rng);
   std::string error;
-  auto generator = vc::Generator::Create(dit.config, dit.weights, &error);
-  if (generator == nullptr) {
-    Report(false, "Generator::Create: " + error);
+  auto sampler = vc::DitSampler::Create(dit.config, dit.weights, &error);
+  if (sampler == nullptr) {
+    Report(false, "DitSampler::Create: " + error);
     return;
   }
   std::vector<float> mu(2 * 256), cond(4 * 64), x(4 * 64);
@@ -382,16 +382,16 @@ void TestGenerator(Random& rng) {
   for (auto& v : x)
     v = static_cast<float>(rng.Normal());
   std::vector<float> velocity(2 * 4 * 64), expected(2 * 4 * 64);
-  generator->Velocity(mu.data(), cond.data(), x.data(), 0.63F,
-                      velocity.data());
+  sampler->Velocity(mu.data(), cond.data(), x.data(), 0.63F,
+                    velocity.data());
   vo_dit_velocity(&dit.oracle, mu.data(), cond.data(), x.data(), 0.63F,
                   expected.data());
   const double v_error = RelativeMax(velocity, expected);
   Report(v_error <= 1e-2,
-         "Generator::Velocity against the oracle: " + Scientific(v_error));
+         "DitSampler::Velocity against the oracle: " + Scientific(v_error));
 
   std::vector<float> latent(4 * 64);
-  generator->Step(mu.data(), cond.data(), x.data(), 10, 2.0F, latent.data());
+  sampler->Sample(mu.data(), cond.data(), x.data(), 10, 2.0F, latent.data());
   const std::vector<vc::EulerStep> schedule = vc::EulerSchedule(10);
   std::vector<float> t, dt;
   std::vector<std::int32_t> evaluate;
@@ -413,11 +413,11 @@ void TestGenerator(Random& rng) {
             << RelativeMax(moved, sampled) << "\n";
   const double p_error = RelativeMax(latent, sampled);
   Report(p_error <= 1e-2,
-         "Generator::Step latent against the oracle: " + Scientific(p_error));
+         "DitSampler::Sample latent against the oracle: " + Scientific(p_error));
   Report(!schedule.front().evaluate && schedule.back().evaluate,
          "EulerSchedule skips the first step only");
-  vc::Check(hipEventSynchronize(generator->latent_event()), "latent event");
-  const auto on_device = Download(generator->latent(), latent.size());
+  vc::Check(hipEventSynchronize(sampler->latent_event()), "latent event");
+  const auto on_device = Download(sampler->latent(), latent.size());
   Report(on_device == latent, "latent() holds the returned latent");
 }
 
@@ -572,7 +572,7 @@ int main() {
     TestLinear(1024, 2560, rng, stream);
     TestLinear(4096, 1024, rng, stream);
     TestLinearBf16(1024, 2560, rng, stream);
-    TestGenerator(rng);
+    TestDitSampler(rng);
     TestForwardStack(rng, stream);
     vc::Check(hipStreamDestroy(stream), "stream");
   } catch (const std::exception& failure) {

@@ -1,5 +1,5 @@
 """The C++ host surface (tests/cpp/host_test.cpp: Bf16Gemm::Linear,
-Generator::Velocity and Generator::Step over the C ABI) against the oracle.
+DitSampler::Velocity and DitSampler::Sample over the C ABI) against the oracle.
 The binary is built by __graft_entry__.build(); exit status 77 means no GPU."""
 import pathlib
 import subprocess

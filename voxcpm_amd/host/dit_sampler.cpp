@@ -1,4 +1,4 @@
-#include "generator.hpp"
+#include "dit_sampler.hpp"
 
 #include <cstdint>
 #include <exception>
@@ -28,21 +28,21 @@ std::vector<EulerStep> EulerSchedule(std::size_t timesteps, float sway) {
   return steps;
 }
 
-std::unique_ptr<Generator> Generator::Create(const DitConfig& config,
-                                             const DitWeights& weights,
-                                             std::string* error) {
-  std::unique_ptr<Generator> generator(new Generator());
+std::unique_ptr<DitSampler> DitSampler::Create(const DitConfig& config,
+                                               const DitWeights& weights,
+                                               std::string* error) {
+  std::unique_ptr<DitSampler> sampler(new DitSampler());
   try {
-    generator->config_ = config;
-    Check(hipStreamCreateWithFlags(&generator->stream_, hipStreamNonBlocking),
+    sampler->config_ = config;
+    Check(hipStreamCreateWithFlags(&sampler->stream_, hipStreamNonBlocking),
           "hipStreamCreate");
     const TransformerConfig& stack = config.dit;
     if (weights.dit.layers.size() != stack.layers)
       throw GpuError("the DiT weights do not match its layer count");
     const std::size_t length = 3 + 2 * config.patch_size;
     const std::vector<float> rope = RopeTable(config.rope, length);
-    generator->rope_ = DeviceBuffer<float>(rope.size());
-    Check(hipMemcpy(generator->rope_.get(), rope.data(),
+    sampler->rope_ = DeviceBuffer<float>(rope.size());
+    Check(hipMemcpy(sampler->rope_.get(), rope.data(),
                     rope.size() * sizeof(float), hipMemcpyHostToDevice),
           "hipMemcpy rope");
     std::vector<vx_dit_layer> layers;
@@ -68,7 +68,7 @@ std::unique_ptr<Generator> Generator::Create(const DitConfig& config,
     vx_dit_weights device{};
     device.layers = layers.data();
     device.norm = weights.dit.norm;
-    device.rope = stack.rope ? generator->rope_.get() : nullptr;
+    device.rope = stack.rope ? sampler->rope_.get() : nullptr;
     device.in_proj = Panels(weights.dit_in, "dit_in");
     device.cond_proj = Panels(weights.dit_cond, "dit_cond");
     device.out_proj = Panels(weights.dit_out, "dit_out");
@@ -78,14 +78,14 @@ std::unique_ptr<Generator> Generator::Create(const DitConfig& config,
       device.delta_1 = Panels(weights.delta_time_1, "delta_time_1");
       device.delta_2 = Panels(weights.delta_time_2, "delta_time_2");
     }
-    CheckVx(vx_dit_create(&generator->dit_, &shape, &device), "vx_dit_create");
+    CheckVx(vx_dit_create(&sampler->dit_, &shape, &device), "vx_dit_create");
     const std::size_t values = config.patch_size * config.feat_dim;
-    generator->mu_ = DeviceBuffer<float>(2 * stack.hidden);
-    generator->prefix_cond_ = DeviceBuffer<float>(values);
-    generator->x_ = DeviceBuffer<float>(values);
-    generator->velocity_ = DeviceBuffer<float>(2 * values);
-    generator->latent_ring_ = DeviceBuffer<float>(2 * values);
-    Check(hipEventCreateWithFlags(&generator->latent_event_,
+    sampler->mu_ = DeviceBuffer<float>(2 * stack.hidden);
+    sampler->prefix_cond_ = DeviceBuffer<float>(values);
+    sampler->x_ = DeviceBuffer<float>(values);
+    sampler->velocity_ = DeviceBuffer<float>(2 * values);
+    sampler->latent_ring_ = DeviceBuffer<float>(2 * values);
+    Check(hipEventCreateWithFlags(&sampler->latent_event_,
                                   hipEventDisableTiming),
           "hipEventCreate");
   } catch (const std::exception& failure) {
@@ -93,10 +93,10 @@ std::unique_ptr<Generator> Generator::Create(const DitConfig& config,
       *error = failure.what();
     return nullptr;
   }
-  return generator;
+  return sampler;
 }
 
-Generator::~Generator() {
+DitSampler::~DitSampler() {
   if (stream_ != nullptr)
     (void)hipStreamSynchronize(stream_);
   vx_dit_destroy(dit_);
@@ -106,8 +106,8 @@ Generator::~Generator() {
     (void)hipStreamDestroy(stream_);
 }
 
-void Generator::Velocity(const float* mu, const float* cond, const float* x,
-                         float t, float* velocity) {
+void DitSampler::Velocity(const float* mu, const float* cond, const float* x,
+                          float t, float* velocity) {
   const std::size_t values = config_.patch_size * config_.feat_dim;
   Check(hipMemcpyAsync(mu_.get(), mu, 2 * config_.dit.hidden * sizeof(float),
                        hipMemcpyHostToDevice, stream_),
@@ -127,9 +127,9 @@ void Generator::Velocity(const float* mu, const float* cond, const float* x,
   Check(hipStreamSynchronize(stream_), "hipStreamSynchronize");
 }
 
-void Generator::Step(const float* mu, const float* prefix_cond,
-                     const float* noise, std::size_t timesteps, float cfg,
-                     float* latent, const SamplerOptions& options) {
+void DitSampler::Sample(const float* mu, const float* prefix_cond,
+                        const float* noise, std::size_t timesteps, float cfg,
+                        float* latent, const SamplerOptions& options) {
   const std::size_t values = config_.patch_size * config_.feat_dim;
   std::vector<float> t(timesteps), dt(timesteps);
   std::vector<std::int32_t> evaluate(timesteps);

@@ -1,10 +1,17 @@
-// The local-DiT part of VoxCPM2's Generator (generator.hpp:34-179 of the
-// reference): the Euler schedule, one DiT evaluation (Velocity) and the
-// patch sampler of Step, over the voxcpm_amd C ABI. The text and residual
-// LMs that produce the DiT's condition `mu` are outside this build, so the
-// condition is an argument here.
-#ifndef VOXCPM_AMD_HOST_GENERATOR_HPP_
-#define VOXCPM_AMD_HOST_GENERATOR_HPP_
+// The local-DiT half of VoxCPM2's Generator (generator.hpp:34-179 of the
+// reference) as its own class, DitSampler, over the voxcpm_amd C ABI. It is
+// not the reference's Generator: that class also owns the text-semantic and
+// residual LMs, the local encoder, FSQ and the stop head, which produce the
+// DiT's condition `mu` and consume its latent; those stay in the reference.
+// What matches the reference exactly: EulerSchedule (generator.hpp:34-44),
+// EulerStep, Velocity's signature (generator.hpp:90-91), latent() and
+// latent_event() (generator.hpp:85-86). What differs: Create takes the DiT's
+// shape and device weights instead of Config and ModelFiles, and Sample
+// takes mu and the previous patch as arguments where the reference's
+// Step(noise, timesteps, cfg, latent, stop_logits) reads them from its LM
+// state and also writes the stop logits.
+#ifndef VOXCPM_AMD_HOST_DIT_SAMPLER_HPP_
+#define VOXCPM_AMD_HOST_DIT_SAMPLER_HPP_
 
 #include <hip/hip_runtime.h>
 
@@ -64,41 +71,43 @@ struct SamplerOptions {
 };
 
 /// The local DiT with its CFM sampler on one non-blocking stream. One
-/// sequence at a time; not thread-safe (generator.hpp:55-57).
-class Generator {
+/// sequence at a time; not thread-safe (the reference's Generator,
+/// generator.hpp:55-58, has the same rule).
+class DitSampler {
 public:
-  /// nullptr and the message in `error` on failure (generator.cpp:168-172).
-  [[nodiscard]] static std::unique_ptr<Generator> Create(
+  /// nullptr and the message in `error` on failure, as the reference's
+  /// Generator::Create reports (generator.cpp:168-172).
+  [[nodiscard]] static std::unique_ptr<DitSampler> Create(
       const DitConfig& config, const DitWeights& weights,
       std::string* error = nullptr);
-  ~Generator();
-  Generator(const Generator&) = delete;
-  Generator& operator=(const Generator&) = delete;
+  ~DitSampler();
+  DitSampler(const DitSampler&) = delete;
+  DitSampler& operator=(const DitSampler&) = delete;
 
   [[nodiscard]] const DitConfig& config() const { return config_; }
   [[nodiscard]] hipStream_t stream() const { return stream_; }
 
   /// The CFG pair of velocities [2][patch_size][feat_dim] of one evaluation
   /// at time t; host arrays mu [2 hidden], cond and x [patch][feat]
-  /// (generator.hpp:88-91).
+  /// (generator.hpp:87-91).
   void Velocity(const float* mu, const float* cond, const float* x, float t,
                 float* velocity);
 
-  /// Step's sampler (generator.cpp:448-469): the patch from `noise` with
-  /// `timesteps` Euler steps and guidance `cfg`, conditioned on `mu` and
-  /// the previous patch `prefix_cond` (host arrays). Writes the latent
-  /// [patch][feat] to `latent` when not null; it also stays on the device:
-  /// latent() until the step after next, ready once latent_event()
-  /// completes.
-  void Step(const float* mu, const float* prefix_cond, const float* noise,
-            std::size_t timesteps, float cfg, float* latent,
-            const SamplerOptions& options = SamplerOptions());
+  /// The sampler inside the reference's Generator::Step
+  /// (generator.cpp:448-469): the patch from `noise` with `timesteps` Euler
+  /// steps and guidance `cfg`, conditioned on `mu` and the previous patch
+  /// `prefix_cond` (host arrays). Writes the latent [patch][feat] to
+  /// `latent` when not null; it also stays on the device: latent() until
+  /// the call after next, ready once latent_event() completes.
+  void Sample(const float* mu, const float* prefix_cond, const float* noise,
+              std::size_t timesteps, float cfg, float* latent,
+              const SamplerOptions& options = SamplerOptions());
 
   [[nodiscard]] const float* latent() const { return latent_slot_; }
   [[nodiscard]] hipEvent_t latent_event() const { return latent_event_; }
 
 private:
-  Generator() = default;
+  DitSampler() = default;
 
   DitConfig config_;
   hipStream_t stream_ = nullptr;
@@ -116,4 +125,4 @@ private:
 
 }  // namespace gufo::models::voxcpm
 
-#endif  // VOXCPM_AMD_HOST_GENERATOR_HPP_
+#endif  // VOXCPM_AMD_HOST_DIT_SAMPLER_HPP_
