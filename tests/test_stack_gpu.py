@@ -239,6 +239,31 @@ def test_stack_decode_replays(vx, oracle, cuda, stream):
         check_close(hidden.cpu().numpy(), ref_h, f"replay past {past} hidden")
 
 
+def test_stack_decode_key_bands(vx, oracle, cuda, stream):
+    """Replayed decode steps keep one graph per 256-key band of attended
+    keys: steps across band edges (255 -> 256 -> 257 keys, 512 -> 513),
+    back into an earlier band (its graph replayed again) and forward again
+    all match the oracle."""
+    config = STACKS["gqa-hd64"]
+    run = Run(vx, oracle, cuda, config, 55, capacity=700)
+    rng = synth.Rng(56, 1)
+    hidden = torch.empty((1, config.hidden), dtype=torch.float32, device=cuda)
+    output = torch.empty_like(hidden)
+    position = torch.empty(1, dtype=torch.int32, device=cuda)
+    run.gpu.set_path(_lib.STACK_PATH_AUTO)
+    for past in (10, 254, 255, 256, 300, 511, 512, 100, 513, 698):
+        h = rng.normal(config.hidden).astype(np.float32).reshape(1, config.hidden)
+        hidden.copy_(torch.from_numpy(h))
+        position.fill_(past)
+        run.gpu.forward(hidden, output, position, position, 1, 1, past, True, run.k_gpu,
+                        run.v_gpu)
+        torch.cuda.synchronize()
+        at = np.array([past], np.int32)
+        ref_h, ref_out = run.cpu.forward(h, at, at, 1, 1, past, True, run.k_cpu, run.v_cpu)
+        check_close(output.cpu().numpy(), ref_out, f"band past {past} output")
+        check_close(hidden.cpu().numpy(), ref_h, f"band past {past} hidden")
+
+
 def test_stack_decode_replays_past_4096(vx, oracle, cuda, stream):
     """The base LM's long-context decode (4096 cached positions and more:
     65 and more 64-key chunks, so the chunk merge takes its later passes)

@@ -30,7 +30,11 @@
 //  - kSwiGlu: RG = 2 with the up rows `group_stride` row groups after the
 //    gate rows; bf16(silu(gate) * up) in bf16 fragment order
 //    (kernels/generator_kernels.hip:243-254);
-//  - kSwiGluRows: the same into bf16 [m][n / 2] row-major (y_bf16).
+//  - kSwiGluRows: the same into bf16 [m][n / 2] row-major (y_bf16);
+//  - kQkvCache: RG = 2 with each rotary dimension's partner (head_dim / 2
+//    columns on) `group_stride` row groups after it; the rotary embedding
+//    at each row's position, then q [m][heads][head_dim] and the row's key
+//    and value cache rows (kernels/generator_kernels.hip:110-158).
 #ifndef VOXCPM_AMD_Q8_TILE_HPP_
 #define VOXCPM_AMD_Q8_TILE_HPP_
 
@@ -90,7 +94,7 @@ inline std::size_t FragElements(std::size_t columns) {
 }
 
 enum class ASource : int { kRowMajor = 0, kFragBf16 = 1, kNormF32 = 2, kNormRows = 3 };
-enum class Output : int { kStore = 0, kResidual = 1, kSwiGlu = 2, kSwiGluRows = 3 };
+enum class Output : int { kStore = 0, kResidual = 1, kSwiGlu = 2, kSwiGluRows = 3, kQkvCache = 4 };
 
 struct TileArgs {
   const std::uint8_t* w;  // panels [groups][pairs] units
@@ -126,6 +130,17 @@ struct TileArgs {
   int accumulate;         // kStore float32: y += product
   float* residual;        // kResidual: float32 fragment order [32][n]
   Bf16* frag_out;         // kSwiGlu: bf16 fragment order [32][n / 2]
+  // kQkvCache: n = (heads + 2 kv_heads) head_dim columns q | k | v.
+  float* q_out;                    // [m][heads][head_dim], rotated
+  float* k_cache;                  // [kv_heads][capacity][head_dim]
+  float* v_cache;
+  const float* rope;               // [positions][head_dim] cos | sin, or null
+  const std::int32_t* positions;   // [m] rotary position of each row
+  const std::int32_t* cache_rows;  // [m] cache row of each row
+  int heads;
+  int kv_heads;
+  int head_dim;
+  int capacity;
 };
 
 /// Row group r of workgroup tile b: consecutive groups (stride 1) or a
@@ -268,11 +283,14 @@ __device__ __forceinline__ void EngineBody(const TileArgs& a) {
   constexpr bool kOneTile = MT == 1 && SRC == ASource::kFragBf16;
   constexpr bool kNorm = SRC == ASource::kNormF32 || SRC == ASource::kNormRows;
   constexpr bool kSwish = OUT == Output::kSwiGlu || OUT == Output::kSwiGluRows;
+  constexpr bool kRope = OUT == Output::kQkvCache;
   static_assert(SRC != ASource::kNormF32 || MT == 2, "norm source is 32 rows");
   static_assert(SRC != ASource::kNormRows || MT == 1, "row-major norm source is one tile");
-  static_assert(OUT == Output::kStore || OUT == Output::kSwiGluRows || MT == 2 || kOneTile,
+  static_assert(OUT == Output::kStore || OUT == Output::kSwiGluRows ||
+                    OUT == Output::kQkvCache || MT == 2 || kOneTile,
                 "fragment outputs are 32 rows or one tile of them");
   static_assert(!kSwish || RG == 2, "SwiGLU pairs two groups");
+  static_assert(!kRope || RG == 2, "the rotary embedding pairs two groups");
   extern __shared__ float lds[];
   const int lane = threadIdx.x % kWave;
   const int wave = threadIdx.x / kWave;
@@ -347,6 +365,24 @@ __device__ __forceinline__ void EngineBody(const TileArgs& a) {
   // The values the epilogue adds to (the residual stream, an accumulated
   // y) are loaded now, beside the first weights, instead of after the sums.
   float before[kOutputsPerThread];
+  // kQkvCache: each output's row position and cache row, loaded now by
+  // masked buffer loads (no branch, so nothing waits for them here); the
+  // rotary table entries they select are loaded with the activations.
+  std::uint32_t position[kOutputsPerThread];
+  std::uint32_t cache_row[kOutputsPerThread];
+  if constexpr (kRope) {
+    const __amdgpu_buffer_rsrc_t positions = BufferOf(a.positions, 4U * a.m);
+    const __amdgpu_buffer_rsrc_t cache_rows = BufferOf(a.cache_rows, 4U * a.m);
+#pragma unroll
+    for (int u = 0; u < kOutputsPerThread; ++u) {
+      const int e = static_cast<int>(threadIdx.x) + u * kThreads;
+      int row, column;
+      const bool live = e < RG * MT * 256 && output_of(e, row, column);
+      const std::uint32_t at = 4U * static_cast<std::uint32_t>(live ? row : 0);
+      position[u] = BufferLoad4(positions, at, live);
+      cache_row[u] = BufferLoad4(cache_rows, at, live);
+    }
+  }
 #pragma unroll
   for (int u = 0; u < kOutputsPerThread; ++u) {
     before[u] = 0.0F;
@@ -496,6 +532,34 @@ __device__ __forceinline__ void EngineBody(const TileArgs& a) {
     }
   };
 
+  // kQkvCache: the cos / sin of each output's rotary dimension (the first
+  // group's column within its head). Their loads depend on the positions
+  // loaded at the start, so they are issued after the first activation
+  // loads, whose wait they share.
+  constexpr int kPairedOutputs = MT * 256;
+  float rope_cos[kOutputsPerThread];
+  float rope_sin[kOutputsPerThread];
+  const auto load_rope = [&] {
+#pragma unroll
+    for (int u = 0; u < kOutputsPerThread; ++u) {
+      rope_cos[u] = 1.0F;
+      rope_sin[u] = 0.0F;
+      const int e = static_cast<int>(threadIdx.x) + u * kThreads;
+      int row, column;
+      if (e < kPairedOutputs && output_of(e, row, column) && a.rope != nullptr &&
+          column < (a.heads + a.kv_heads) * a.head_dim) {
+        // The position is used here, not hoisted ahead of the first loads.
+        std::uint32_t at = position[u];
+        asm volatile("" : "+v"(at));
+        const float* table =
+            a.rope + static_cast<std::size_t>(at) * a.head_dim + column % a.head_dim;
+        rope_cos[u] = table[0];
+        rope_sin[u] = table[a.head_dim / 2];
+      }
+    }
+  };
+  static_assert(!kRope || SRC == ASource::kNormRows, "the rotary epilogue takes norm rows");
+
   float* reduce = lds;
   if constexpr (SRC == ASource::kNormRows) {
     // The workgroup's m rows, RMS-normalised once into LDS as bf16 (rows
@@ -518,14 +582,16 @@ __device__ __forceinline__ void EngineBody(const TileArgs& a) {
     const int rows_per_pass = min(kThreads / per_row, waves);
     const int c = t % per_row;
     const uint4 g = *reinterpret_cast<const uint4*>(a.gamma + 8 * c);
-    const float gamma[8] = {Bf16Lo(g.x), Bf16Hi(g.x), Bf16Lo(g.y), Bf16Hi(g.y),
-                            Bf16Lo(g.z), Bf16Hi(g.z), Bf16Lo(g.w), Bf16Hi(g.w)};
     for (int first = 0; first < a.m; first += rows_per_pass) {
       const int r = first + t / per_row;
       const bool live = t < rows_per_pass * per_row && r < a.m;
       const std::uint32_t at = 4U * static_cast<std::uint32_t>(r * a.k + 8 * c);
       const float4 lo = __builtin_bit_cast(float4, BufferLoad16(h_buffer, at, live));
       const float4 hi = __builtin_bit_cast(float4, BufferLoad16(h_buffer, at + 16U, live));
+      if constexpr (kRope) {
+        if (first == 0)
+          load_rope();
+      }
       const float x[8] = {lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
       float square = 0.0F;
 #pragma unroll
@@ -543,6 +609,14 @@ __device__ __forceinline__ void EngineBody(const TileArgs& a) {
       }
       __syncthreads();
       if (live) {
+        // The norm weights are unpacked here, after this pass's loads were
+        // issued: unpacked before the loop, their wait (in order behind the
+        // weights' loads) held back the residual rows' loads by a round
+        // trip.
+        uint4 gw = g;
+        asm volatile("" : "+v"(gw.x), "+v"(gw.y), "+v"(gw.z), "+v"(gw.w));
+        const float gamma[8] = {Bf16Lo(gw.x), Bf16Hi(gw.x), Bf16Lo(gw.y), Bf16Hi(gw.y),
+                                Bf16Lo(gw.z), Bf16Hi(gw.z), Bf16Lo(gw.w), Bf16Hi(gw.w)};
         const float inverse = sums[kThreads + t / per_row];
         float v[8];
 #pragma unroll
@@ -746,7 +820,7 @@ __device__ __forceinline__ void EngineBody(const TileArgs& a) {
       total += parts[w];
     return total;
   };
-  const int outputs = kSwish ? MT * 256 : kFragmentFloats;
+  const int outputs = kSwish || kRope ? MT * 256 : kFragmentFloats;
 #pragma unroll
   for (int u = 0; u < kOutputsPerThread; ++u) {
     const int e = static_cast<int>(threadIdx.x) + u * kThreads;
@@ -765,6 +839,34 @@ __device__ __forceinline__ void EngineBody(const TileArgs& a) {
     } else if constexpr (OUT == Output::kSwiGlu) {
       const float up = total_of(e + MT * 256);
       a.frag_out[BfFragIndex(row, column)] = Bf16Fast(Silu(v) * up);
+    } else if constexpr (kRope) {
+      // (x_i, x_{i + half}) -> (x_i c - x_{i + half} s, x_{i + half} c + x_i s)
+      // on q and k; v is stored as it is.
+      const float partner = total_of(e + MT * 256);
+      const int head = column / a.head_dim;
+      const int i = column % a.head_dim;
+      const int half = a.head_dim / 2;
+      float first = v;
+      float second = partner;
+      if (a.rope != nullptr && head < a.heads + a.kv_heads) {
+        const float c = rope_cos[u];
+        const float sn = rope_sin[u];
+        first = v * c - partner * sn;
+        second = partner * c + v * sn;
+      }
+      float* target;
+      if (head < a.heads)
+        target = a.q_out + (static_cast<std::size_t>(row) * a.heads + head) * a.head_dim;
+      else if (head < a.heads + a.kv_heads)
+        target = a.k_cache + (static_cast<std::size_t>(head - a.heads) * a.capacity +
+                              static_cast<std::size_t>(cache_row[u])) *
+                                 a.head_dim;
+      else
+        target = a.v_cache + (static_cast<std::size_t>(head - a.heads - a.kv_heads) * a.capacity +
+                              static_cast<std::size_t>(cache_row[u])) *
+                                 a.head_dim;
+      target[i] = first;
+      target[half + i] = second;
     } else {
       const float up = total_of(e + MT * 256);
       a.y_bf16[static_cast<std::size_t>(row) * (a.n / 2) + column] = Bf16Fast(Silu(v) * up);

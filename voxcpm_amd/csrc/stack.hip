@@ -16,6 +16,7 @@
 #include <algorithm>
 #include <cmath>
 #include <cstdint>
+#include <utility>
 #include <vector>
 
 #include "common.hpp"
@@ -34,6 +35,9 @@ constexpr int kChunk = 64;     // keys per workgroup of the split attention
 constexpr int kThreads = 256;  // four waves, 16 keys each when scoring
 constexpr int kWaves = kThreads / kWave;
 constexpr int kMaxNormRows = 8;  // rows of the one-tile row-major path
+// The split attention spreads a chunk's query heads over workgroups while
+// its grid stays within this many (one per compute unit).
+constexpr int kSpreadWorkgroups = 256;
 
 struct AttentionArgs {
   const float* q;        // [rows][heads][D], rotated, unscaled
@@ -99,7 +103,9 @@ __device__ inline int KeyCount(const AttentionArgs& a, int row) {
 /// max), the four waves' sums added in wave order. One chunk writes the
 /// output itself; several leave (max, sum, values) for MergeKernel.
 /// Chunks past a row's keys do nothing (the merge reads the row's chunks
-/// only).
+/// only). A workgroup takes G of the KV head's query heads (blockIdx.z:
+/// the KV head, then which G of its group): a short cache spreads its few
+/// chunks' heads over more compute units, each with a G-th of the scoring.
 template<int D, int G>
 __global__ __launch_bounds__(kThreads) void SplitAttentionKernel(AttentionArgs a) {
   constexpr int kQuarter = D / 4;
@@ -111,7 +117,10 @@ __global__ __launch_bounds__(kThreads) void SplitAttentionKernel(AttentionArgs a
   float* parts = stats + 2 * G;    // [waves][G][D]
   const int split = static_cast<int>(blockIdx.x);
   const int row = static_cast<int>(blockIdx.y);
-  const int g = static_cast<int>(blockIdx.z);
+  const int parts_per_kv = a.heads / a.kv_heads / G;
+  const int g = static_cast<int>(blockIdx.z) / parts_per_kv;  // the KV head
+  const int head0 =
+      g * (a.heads / a.kv_heads) + (static_cast<int>(blockIdx.z) % parts_per_kv) * G;
   const int lane = static_cast<int>(threadIdx.x) % kWave;
   const int wave = static_cast<int>(threadIdx.x) / kWave;
   const int first = (row / a.rows_per_sequence) * a.keys_per_sequence;
@@ -148,7 +157,7 @@ __global__ __launch_bounds__(kThreads) void SplitAttentionKernel(AttentionArgs a
   constexpr int kQueryLoads = (G * D / 4 + kThreads - 1) / kThreads;
   float4 qv4[kQueryLoads];
   const float4* qsrc = reinterpret_cast<const float4*>(
-      a.q + (static_cast<std::size_t>(row) * a.heads + g * G) * D);
+      a.q + (static_cast<std::size_t>(row) * a.heads + head0) * D);
 #pragma unroll
   for (int i = 0; i < kQueryLoads; ++i) {
     const int e4 = static_cast<int>(threadIdx.x) + i * kThreads;
@@ -178,17 +187,32 @@ __global__ __launch_bounds__(kThreads) void SplitAttentionKernel(AttentionArgs a
   }
   __syncthreads();
 
-  for (int hh = 0; hh < G; ++hh) {
-    const float4* qrow = reinterpret_cast<const float4*>(qs + hh * D + quarter * kQuarter);
-    float s = 0.0F;
+  // Scores of up to kHeadBlock heads at once: each step reads the heads'
+  // next four query dimensions (one LDS broadcast per head) into
+  // independent sums, so the reads are in flight together and no sum waits
+  // on another's latency; each sum still adds its terms in dimension order.
+  constexpr int kHeadBlock = G < 8 ? G : 8;
+  for (int h0 = 0; h0 < G; h0 += kHeadBlock) {
+    float s[kHeadBlock];
+#pragma unroll
+    for (int hh = 0; hh < kHeadBlock; ++hh)
+      s[hh] = 0.0F;
 #pragma unroll
     for (int i = 0; i < kQuarter / 4; ++i) {
-      const float4 q = qrow[i];
-      s += q.x * kv[i].x + q.y * kv[i].y + q.z * kv[i].z + q.w * kv[i].w;
+      float4 q[kHeadBlock];
+#pragma unroll
+      for (int hh = 0; hh < kHeadBlock; ++hh)
+        q[hh] = reinterpret_cast<const float4*>(qs + (h0 + hh) * D + quarter * kQuarter)[i];
+#pragma unroll
+      for (int hh = 0; hh < kHeadBlock; ++hh)
+        s[hh] += q[hh].x * kv[i].x + q[hh].y * kv[i].y + q[hh].z * kv[i].z + q[hh].w * kv[i].w;
     }
-    s = AddXor32(AddXor16(s));
-    if (quarter == 0)
-      ps[hh * kChunk + key_local] = valid ? s : -INFINITY;
+#pragma unroll
+    for (int hh = 0; hh < kHeadBlock; ++hh) {
+      const float total = AddXor32(AddXor16(s[hh]));
+      if (quarter == 0)
+        ps[(h0 + hh) * kChunk + key_local] = valid ? total : -INFINITY;
+    }
   }
   __syncthreads();
 
@@ -206,26 +230,37 @@ __global__ __launch_bounds__(kThreads) void SplitAttentionKernel(AttentionArgs a
   }
   __syncthreads();
 
-  // Each head's weighted values over the wave's 16 keys into LDS.
-  for (int hh = 0; hh < G; ++hh) {
-    const float4* prow = reinterpret_cast<const float4*>(ps + hh * kChunk + 16 * wave);
-    float p[16];
+  // Each head's weighted values over the wave's 16 keys into LDS, four
+  // keys per step for a block of heads at once (independent sums, each
+  // adding its keys in order).
+  for (int h0 = 0; h0 < G; h0 += kHeadBlock) {
+    float o[kHeadBlock][kPerLane];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const float4 f = prow[i];
-      p[4 * i] = f.x;
-      p[4 * i + 1] = f.y;
-      p[4 * i + 2] = f.z;
-      p[4 * i + 3] = f.w;
+    for (int hh = 0; hh < kHeadBlock; ++hh)
+#pragma unroll
+      for (int j = 0; j < kPerLane; ++j)
+        o[hh][j] = 0.0F;
+#pragma unroll
+    for (int k4 = 0; k4 < 4; ++k4) {
+      float4 p[kHeadBlock];
+#pragma unroll
+      for (int hh = 0; hh < kHeadBlock; ++hh)
+        p[hh] = reinterpret_cast<const float4*>(ps + (h0 + hh) * kChunk + 16 * wave)[k4];
+#pragma unroll
+      for (int hh = 0; hh < kHeadBlock; ++hh)
+#pragma unroll
+        for (int j = 0; j < kPerLane; ++j) {
+          o[hh][j] += p[hh].x * vv[4 * k4][j];
+          o[hh][j] += p[hh].y * vv[4 * k4 + 1][j];
+          o[hh][j] += p[hh].z * vv[4 * k4 + 2][j];
+          o[hh][j] += p[hh].w * vv[4 * k4 + 3][j];
+        }
     }
 #pragma unroll
-    for (int j = 0; j < kPerLane; ++j) {
-      float o = 0.0F;
+    for (int hh = 0; hh < kHeadBlock; ++hh)
 #pragma unroll
-      for (int kk = 0; kk < 16; ++kk)
-        o += p[kk] * vv[kk][j];
-      parts[(wave * G + hh) * D + lane * kPerLane + j] = o;
-    }
+      for (int j = 0; j < kPerLane; ++j)
+        parts[(wave * G + h0 + hh) * D + lane * kPerLane + j] = o[hh][j];
   }
   __syncthreads();
   const int width = a.heads * D;
@@ -238,12 +273,12 @@ __global__ __launch_bounds__(kThreads) void SplitAttentionKernel(AttentionArgs a
     const int hh = e / D;
     const int d = e % D;
     if (a.splits == 1) {
-      a.out[OutIndex(a, row, (g * G + hh) * D + d, width)] =
+      a.out[OutIndex(a, row, (head0 + hh) * D + d, width)] =
           Bf16Bits(total * (1.0F / stats[2 * hh + 1]));
     } else {
       float* target =
           a.partials +
-          ((static_cast<std::size_t>(row) * a.heads + g * G + hh) * a.splits + split) * stride;
+          ((static_cast<std::size_t>(row) * a.heads + head0 + hh) * a.splits + split) * stride;
       target[2 + d] = total;
       if (d == 0) {
         target[0] = stats[2 * hh];
@@ -256,10 +291,14 @@ __global__ __launch_bounds__(kThreads) void SplitAttentionKernel(AttentionArgs a
 /// The chunks of one (row, head) met in chunk order: M = max m_c,
 /// L = sum l_c exp(m_c - M), out = bf16(sum o_c exp(m_c - M) / L), over the
 /// row's chunks only. Lane c takes chunk c's statistics (chunks 64 apart in
-/// turn); the values are loaded eight chunks at a time.
+/// turn). The first kPreload chunks' values are loaded at the start with
+/// the statistics and the row's key count (which may come from the
+/// device), so that a cache of up to 2048 keys takes one memory round
+/// trip; later chunks are loaded eight at a time.
 template<int D>
 __global__ __launch_bounds__(kWave) void MergeKernel(AttentionArgs a) {
   constexpr int kPerLane = D / kWave;
+  constexpr int kPreload = 32;
   constexpr int kBatch = 8;
   const int row = static_cast<int>(blockIdx.x);
   const int head = static_cast<int>(blockIdx.y);
@@ -267,18 +306,16 @@ __global__ __launch_bounds__(kWave) void MergeKernel(AttentionArgs a) {
   const std::size_t stride = static_cast<std::size_t>(D) + 2;
   const float* base =
       a.partials + (static_cast<std::size_t>(row) * a.heads + head) * a.splits * stride;
-  // The first 64 chunk slots' statistics and the first kBatch chunks'
-  // values are loaded with the row's key count (which may come from the
-  // device), not after it: every slot below `splits` lies inside the
-  // partials, and slots past the row's chunks (stale) are masked below.
+  // Every slot below `splits` lies inside the partials; slots past the
+  // row's chunks hold stale values and are masked below.
   const int slots = min(a.splits, kWave);
   const float* mine = base + static_cast<std::size_t>(min(lane, slots - 1)) * stride;
   const float first_m = mine[0];
   const float first_l = mine[1];
-  float first[kBatch][kPerLane];
+  float first[kPreload][kPerLane];
 #pragma unroll
-  for (int b = 0; b < kBatch; ++b) {
-    const float* part = base + static_cast<std::size_t>(min(b, slots - 1)) * stride + 2 +
+  for (int b = 0; b < kPreload; ++b) {
+    const float* part = base + static_cast<std::size_t>(min(b, a.splits - 1)) * stride + 2 +
                         lane * kPerLane;
 #pragma unroll
     for (int j = 0; j < kPerLane; ++j)
@@ -294,6 +331,26 @@ __global__ __launch_bounds__(kWave) void MergeKernel(AttentionArgs a) {
   for (int j = 0; j < kPerLane; ++j)
     o[j] = 0.0F;
   float l = 0.0F;
+  // Chunks i0 .. i0 + kBatch - 1 of the pass at c0, loaded together.
+  const auto add_batch = [&](int c0, int i0, int count, float factor) {
+    float values[kBatch][kPerLane];
+#pragma unroll
+    for (int b = 0; b < kBatch; ++b) {
+      const float* part = base + (c0 + min(i0 + b, count - 1)) * stride + 2 + lane * kPerLane;
+#pragma unroll
+      for (int j = 0; j < kPerLane; ++j)
+        values[b][j] = part[j];
+    }
+#pragma unroll
+    for (int b = 0; b < kBatch; ++b) {
+      const float f = __shfl(factor, i0 + b, kWave);
+      if (i0 + b < count) {
+#pragma unroll
+        for (int j = 0; j < kPerLane; ++j)
+          o[j] += values[b][j] * f;
+      }
+    }
+  };
   for (int c0 = 0; c0 < chunks; c0 += kWave) {
     const int c = c0 + lane;
     float factor = 0.0F;
@@ -305,34 +362,21 @@ __global__ __launch_bounds__(kWave) void MergeKernel(AttentionArgs a) {
       l += cl * factor;
     }
     const int count = min(kWave, chunks - c0);
-    for (int i0 = 0; i0 < count; i0 += kBatch) {
-      float values[kBatch][kPerLane];
-      if (c0 == 0 && i0 == 0) {
+    int i0 = 0;
+    if (c0 == 0) {
 #pragma unroll
-        for (int b = 0; b < kBatch; ++b)
-#pragma unroll
-          for (int j = 0; j < kPerLane; ++j)
-            values[b][j] = first[b][j];
-      } else {
-#pragma unroll
-        for (int b = 0; b < kBatch; ++b) {
-          const float* part =
-              base + (c0 + min(i0 + b, count - 1)) * stride + 2 + lane * kPerLane;
+      for (int b = 0; b < kPreload; ++b) {
+        const float f = __shfl(factor, b, kWave);
+        if (b < count) {
 #pragma unroll
           for (int j = 0; j < kPerLane; ++j)
-            values[b][j] = part[j];
+            o[j] += first[b][j] * f;
         }
       }
-#pragma unroll
-      for (int b = 0; b < kBatch; ++b) {
-        const float f = __shfl(factor, i0 + b, kWave);
-        if (i0 + b < count) {
-#pragma unroll
-          for (int j = 0; j < kPerLane; ++j)
-            o[j] += values[b][j] * f;
-        }
-      }
+      i0 = kPreload;
     }
+    for (; i0 < count; i0 += kBatch)
+      add_batch(c0, i0, count, factor);
   }
   // Lane c's chunks' sums, then the lanes by a fixed tree.
   l = WaveSum64(l);
@@ -346,14 +390,24 @@ __global__ __launch_bounds__(kWave) void MergeKernel(AttentionArgs a) {
 template<int D, int G>
 void LaunchSplit(const AttentionArgs& a, int rows, hipStream_t stream) {
   const std::size_t shared = SharedFloats(G, D) * sizeof(float);
+  const int parts_per_kv = a.heads / a.kv_heads / G;
   SplitAttentionKernel<D, G><<<dim3(static_cast<unsigned>(a.splits), static_cast<unsigned>(rows),
-                                    static_cast<unsigned>(a.kv_heads)),
+                                    static_cast<unsigned>(a.kv_heads * parts_per_kv)),
                                kThreads, shared, stream>>>(a);
+}
+
+/// Query heads per workgroup: the KV head's whole group once the chunks
+/// alone fill the compute units, fewer (down to one) while they do not.
+int HeadsPerWorkgroup(int group, int chunks) {
+  int heads = group;
+  while (heads > 1 && chunks * (group / heads) * 2 <= kSpreadWorkgroups)
+    heads /= 2;
+  return heads;
 }
 
 template<int D>
 void LaunchAttention(const AttentionArgs& a, int rows, hipStream_t stream) {
-  switch (a.heads / a.kv_heads) {
+  switch (HeadsPerWorkgroup(a.heads / a.kv_heads, a.splits * rows * a.kv_heads)) {
     case 1: LaunchSplit<D, 1>(a, rows, stream); break;
     case 2: LaunchSplit<D, 2>(a, rows, stream); break;
     case 4: LaunchSplit<D, 4>(a, rows, stream); break;
@@ -505,6 +559,39 @@ void NormQkvRows(const float* h, const Bf16* gamma, float eps, const void* weigh
                                                                        stream);
 }
 
+/// rmsnorm(h) Wqkv^T with the rotary embedding and the cache writes in the
+/// epilogue (QkvRope's work): each workgroup owns a rotary dimension's two
+/// row groups, head_dim / 2 columns apart. head_dim a multiple of 32.
+void NormQkvCacheRows(const float* h, const Bf16* gamma, float eps, const void* weight,
+                      const float* rope, const std::int32_t* positions,
+                      const std::int32_t* cache_rows, float* q, float* k_cache, float* v_cache,
+                      int rows, int hidden, int heads, int kv_heads, int head_dim, int capacity,
+                      q8::Weights kind, hipStream_t stream) {
+  const int n = (heads + 2 * kv_heads) * head_dim;
+  q8::TileArgs args = RowArgs(weight, rows, hidden, n);
+  args.h = h;
+  args.gamma = gamma;
+  args.eps = eps;
+  args.group_stride = head_dim / 32;
+  args.q_out = q;
+  args.k_cache = k_cache;
+  args.v_cache = v_cache;
+  args.rope = rope;
+  args.positions = positions;
+  args.cache_rows = cache_rows;
+  args.heads = heads;
+  args.kv_heads = kv_heads;
+  args.head_dim = head_dim;
+  args.capacity = capacity;
+  const int tiles = args.groups / 2;
+  if (args.pairs <= 16)
+    LaunchRowEngine<q8::ASource::kNormRows, q8::Output::kQkvCache, 2, 1>(args, tiles, kind,
+                                                                         stream);
+  else
+    LaunchRowEngine<q8::ASource::kNormRows, q8::Output::kQkvCache, 2, 2>(args, tiles, kind,
+                                                                         stream);
+}
+
 void NormGateUpRows(const float* h, const Bf16* gamma, float eps, const void* weight, Bf16* act,
                     int rows, int hidden, int ffn, q8::Weights kind, hipStream_t stream) {
   q8::TileArgs args = RowArgs(weight, rows, hidden, 2 * ffn);
@@ -613,14 +700,23 @@ struct vx_stack {
   Bf16* attention_frag = nullptr;
   Bf16* swiglu_frag = nullptr;
 
-  // The replayed forward of up to 32 rows and the past it reads.
+  // The replayed forwards of up to 32 rows and the past they read: one
+  // graph per band of kBandKeys attended keys, whose attention grid covers
+  // that band's chunks only (a short cache launches no workgroups for the
+  // chunks it does not hold yet).
+  static constexpr std::size_t kBandKeys = 256;
   int* past_device = nullptr;
   ForwardKey graph_key;
-  hipGraphExec_t graph = nullptr;
+  std::vector<std::pair<int, hipGraphExec_t>> graphs;  // (attention splits, graph)
+
+  void DropGraphs() {
+    for (auto& entry : graphs)
+      (void)hipGraphExecDestroy(entry.second);
+    graphs.clear();
+  }
 
   ~vx_stack() {
-    if (graph != nullptr)
-      (void)hipGraphExecDestroy(graph);
+    DropGraphs();
     if (past_device != nullptr)
       (void)hipFree(past_device);
     for (void* pointer :
@@ -680,11 +776,19 @@ struct vx_stack {
         const vx_dit_layer& layer = layers[l];
         float* keys = f.k_cache + l * layer_stride;
         float* values = f.v_cache + l * layer_stride;
-        vx::stack::NormQkvRows(f.hidden, layer.input_norm, shape.eps, layer.qkv, qkv, m,
-                               static_cast<int>(width), static_cast<int>(qkv_width), Kind(),
-                               stream);
-        vx::kernels::QkvRope(qkv, rope, f.positions, f.cache_rows, q, keys, values, rows,
-                             shape.heads, shape.kv_heads, shape.head_dim, f.capacity, stream);
+        if (shape.head_dim % 32 == 0) {
+          vx::stack::NormQkvCacheRows(
+              f.hidden, layer.input_norm, shape.eps, layer.qkv, rope, f.positions, f.cache_rows,
+              q, keys, values, m, static_cast<int>(width), static_cast<int>(shape.heads),
+              static_cast<int>(shape.kv_heads), static_cast<int>(shape.head_dim),
+              static_cast<int>(f.capacity), Kind(), stream);
+        } else {
+          vx::stack::NormQkvRows(f.hidden, layer.input_norm, shape.eps, layer.qkv, qkv, m,
+                                 static_cast<int>(width), static_cast<int>(qkv_width), Kind(),
+                                 stream);
+          vx::kernels::QkvRope(qkv, rope, f.positions, f.cache_rows, q, keys, values, rows,
+                               shape.heads, shape.kv_heads, shape.head_dim, f.capacity, stream);
+        }
         vx::stack::Attention(q, keys, values, bf16, false, attention_partials, rows,
                              f.rows_per_sequence, f.keys_per_sequence, past, f.causal,
                              shape.heads, shape.kv_heads, shape.head_dim, f.capacity, splits,
@@ -753,21 +857,26 @@ struct vx_stack {
     const std::size_t rows = f.rows;
     const std::size_t sequences = rows / f.rows_per_sequence;
     // Up to 32 rows (decode steps, encoder patches: the same buffers call
-    // after call) the launches replay as one graph captured on first use;
-    // its attention grid covers every chunk the cache can hold and reads
-    // past from the device.
+    // after call) the launches replay as a graph captured on first use, one
+    // per band of attended keys: its attention grid covers the band's
+    // chunks and reads past from the device.
     hipStreamCaptureStatus capturing = hipStreamCaptureStatusNone;
     if (f.stream != nullptr)
       VX_HIP(hipStreamIsCapturing(f.stream, &capturing), "vx_stack_forward: capture status");
     const bool graphed = f.stream != nullptr && capturing == hipStreamCaptureStatusNone &&
                          rows <= vx::q8::kFragRows;
-    const int splits =
-        graphed ? vx::stack::AttentionSplits(
-                      f.capacity - (sequences - 1) * f.keys_per_sequence - f.rows_per_sequence,
-                      f.rows_per_sequence)
-                : vx::stack::AttentionSplits(past, f.rows_per_sequence);
-    const std::size_t partials =
-        vx::stack::AttentionPartialFloats(rows, shape.heads, shape.head_dim, splits);
+    // The keys the cache holds for the last sequence bound every band; the
+    // partials are sized for them, so a new band never moves a buffer.
+    const std::size_t most =
+        f.capacity - (sequences - 1) * f.keys_per_sequence - f.rows_per_sequence;
+    const std::size_t need = past + f.rows_per_sequence;
+    const std::size_t banded =
+        std::min(most, (need + kBandKeys - 1) / kBandKeys * kBandKeys - f.rows_per_sequence);
+    const int splits = graphed ? vx::stack::AttentionSplits(banded, f.rows_per_sequence)
+                               : vx::stack::AttentionSplits(past, f.rows_per_sequence);
+    const std::size_t partials = vx::stack::AttentionPartialFloats(
+        rows, shape.heads, shape.head_dim,
+        graphed ? vx::stack::AttentionSplits(most, f.rows_per_sequence) : splits);
     const std::size_t wide = std::max({shape.hidden, qkv_width, shape.ffn});
     const char* what = "vx_stack_forward: hipMalloc";
     // Growing a buffer moves it: a graph that holds the old one is dropped.
@@ -785,11 +894,13 @@ struct vx_stack {
       return Launch(f, past, splits, nullptr, f.stream);
 
     vx::stack::SetPast(past_device, past, f.stream);
-    if (graph == nullptr || moved || !(graph_key == f)) {
-      if (graph != nullptr) {
-        (void)hipGraphExecDestroy(graph);
-        graph = nullptr;
-      }
+    if (moved || !(graph_key == f))
+      DropGraphs();
+    hipGraphExec_t graph = nullptr;
+    for (const auto& entry : graphs)
+      if (entry.first == splits)
+        graph = entry.second;
+    if (graph == nullptr) {
       VX_HIP(hipStreamBeginCapture(f.stream, hipStreamCaptureModeThreadLocal),
              "vx_stack_forward: begin capture");
       const int status = Launch(f, past, splits, past_device, f.stream);
@@ -804,11 +915,10 @@ struct vx_stack {
         return vx::FailHip(ended, "vx_stack_forward: end capture");
       const hipError_t instantiated = hipGraphInstantiate(&graph, captured, nullptr, nullptr, 0);
       (void)hipGraphDestroy(captured);
-      if (instantiated != hipSuccess) {
-        graph = nullptr;
+      if (instantiated != hipSuccess)
         return vx::FailHip(instantiated, "vx_stack_forward: instantiate");
-      }
       graph_key = f;
+      graphs.emplace_back(splits, graph);
     }
     VX_HIP(hipGraphLaunch(graph, f.stream), "vx_stack_forward: graph launch");
     return vx::Succeed();
