@@ -17,9 +17,9 @@ pytestmark = pytest.mark.gpu
 BOUND = 2e-3
 
 # "small" and "odd" take channel counts that are not multiples of 16 (8;
-# 24 and 12): their products go to the library GEMM, and the elementwise
-# kernels make the next inputs (unit windows, a block's input, the output
-# window) in place of the products' epilogues.
+# 24 and 12): their products go to the LDS-tiled float32 kernel
+# (F32TileKernel), whose epilogue makes the next inputs (unit windows, a
+# block's input, the output window) as the 16-column kernel's does.
 CONFIGS = {
     "small": synth.VaeConfig(latent=16, decoder_dim=64, rates=(3, 2, 2)),
     "odd": synth.VaeConfig(latent=16, decoder_dim=48, rates=(2, 2)),

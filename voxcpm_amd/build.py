@@ -58,7 +58,7 @@ def build(jobs: int | None = None, verbose: bool = False) -> pathlib.Path:
         objects = list(pool.map(_compile, srcs))
     tmp = LIBRARY.with_suffix(".so.tmp")
     cmd = [HIPCC, f"--offload-arch={ARCH}", "-shared", "-o", str(tmp),
-           *map(str, objects), "-lrocblas"]
+           *map(str, objects)]
     result = subprocess.run(cmd, capture_output=True, text=True)
     if result.returncode != 0:
         raise RuntimeError(f"link failed:\n{result.stderr}")

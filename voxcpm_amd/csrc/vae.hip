@@ -9,18 +9,16 @@
 // side by side, K = 2 in), and three residual units (Snake, dilated
 // depthwise conv fused with the second Snake, pointwise product added into
 // the stream), then Snake and the 7-tap convolution to mono with tanh.
-// Each bias is applied by the next elementwise kernel as it reads the
-// stream, or by the product itself where the product's epilogue also makes
-// the next residual unit's input window (bias, Snake, history); each state
-// is filled by the kernel that first reads it and refreshed by a later
-// kernel that does not, so no copies remain. The
-// products (the reference calls hipblasSgemm) take a float32 MFMA kernel
-// over 16-column, 32-row tiles that reads the weights in place; a product
-// whose tiles would re-read over 32 MiB of activations between them goes
-// to rocBLAS. Up to 16 latent frames per chunk the launches replay as one
-// HIP graph.
+// Each product's epilogue applies its bias and makes its consumer's input
+// (a residual unit's window: bias, Snake, history; a block's input; the
+// output window); each state is filled by the kernel that first reads it
+// and refreshed by a later kernel that does not, so no copies remain. The
+// products (the reference calls hipblasSgemm) take float32 MFMA kernels:
+// 16-column, 32-row tiles that read the weights in place, or, where those
+// tiles would re-read over 32 MiB of activations between them, 32 x 32
+// tiles staged through LDS. Up to 16 latent frames per chunk the launches
+// replay as one HIP graph.
 #include <hip/hip_runtime.h>
-#include <rocblas/rocblas.h>
 
 #include <algorithm>
 #include <cmath>
@@ -94,62 +92,6 @@ __global__ void DepthwiseKernel(const float* work, const float* w, const float* 
   out[i] = alpha != nullptr ? Snake(sum, alpha[ch]) : sum;
 }
 
-/// The block's input: v = hidden + pending bias, y = Snake(v scale + bias);
-/// x2[f] = [y(f) | y(f - 1)] with y(-1) the state (the last frame of the
-/// previous chunk). The thread of (frame 0, channel c) also recomputes
-/// y(t - 1, c) into the state after reading it.
-__global__ void BlockInputKernel(const float* hidden, const float* pending, const float* scale,
-                                 const float* bias, const float* alpha, float* x2,
-                                 float* state, std::size_t t, std::size_t c) {
-  const std::size_t i = static_cast<std::size_t>(blockIdx.x) * blockDim.x + threadIdx.x;
-  if (i >= t * c)
-    return;
-  const std::size_t f = i / c;
-  const std::size_t ch = i % c;
-  const auto snake_at = [&](std::size_t frame) {
-    const float v = hidden[frame * c + ch] + pending[ch];
-    return Snake(v * scale[ch] + bias[ch], alpha[ch]);
-  };
-  const float y = snake_at(f);
-  x2[f * 2 * c + ch] = y;
-  if (f + 1 < t)
-    x2[(f + 1) * 2 * c + c + ch] = y;
-  if (f == 0) {
-    x2[c + ch] = state[ch];
-    state[ch] = t == 1 ? y : snake_at(t - 1);
-  }
-}
-
-/// A residual unit's input: hidden += pending bias (in place), work =
-/// [state (6 d rows) | Snake(hidden, alpha)].
-__global__ void UnitInputKernel(float* hidden, const float* pending, const float* alpha,
-                                const float* state, float* work, std::size_t t, std::size_t c,
-                                int d) {
-  const std::size_t i = static_cast<std::size_t>(blockIdx.x) * blockDim.x + threadIdx.x;
-  const std::size_t head = static_cast<std::size_t>(kTaps - 1) * d * c;
-  if (i < head)
-    work[i] = state[i];
-  if (i >= t * c)
-    return;
-  const std::size_t ch = i % c;
-  const float v = hidden[i] + (pending != nullptr ? pending[ch] : 0.0F);
-  hidden[i] = v;
-  work[head + i] = Snake(v, alpha[ch]);
-}
-
-/// The output: work = [state (6 rows) | Snake(hidden + pending, alpha)].
-__global__ void OutputInputKernel(const float* hidden, const float* pending, const float* alpha,
-                                  const float* state, float* work, std::size_t t, std::size_t c) {
-  const std::size_t i = static_cast<std::size_t>(blockIdx.x) * blockDim.x + threadIdx.x;
-  const std::size_t head = (kTaps - 1) * c;
-  if (i < head)
-    work[i] = state[i];
-  if (i >= t * c)
-    return;
-  const std::size_t ch = i % c;
-  work[head + i] = Snake(hidden[i] + pending[ch], alpha[ch]);
-}
-
 /// samples[f] = tanh(b + sum_c sum_j w[c][j] work[f + j][c]), one
 /// workgroup per 4 frames, lanes over channels; afterwards state = work's
 /// last 6 rows (this kernel never reads the state).
@@ -190,16 +132,15 @@ __global__ void ToMonoKernel(const float* work, const float* w, float b, float* 
 constexpr int kF32Waves = 16;  // most waves per workgroup
 typedef float F32x4 __attribute__((ext_vector_type(4)));
 
-/// A residual unit's input made in a product's epilogue (what
-/// UnitInputKernel does after a product it cannot see into). y's linear
+/// A residual unit's input made in a product's epilogue. y's linear
 /// element i is (frame i / channels, channel i % channels), also for a
 /// transposed convolution's [t][stride channels] output: v = y[i] +
 /// bias[channel], y[i] = v, window[head + i] = Snake(v, alpha[channel]), and
 /// window[0 .. head) = state (copied by the first row block's workgroups).
 /// Unused when window is null.
 ///
-/// With `scale` set it makes a decoder block's input instead (what
-/// BlockInputKernel does): u = Snake(v scale + shift, alpha) per frame f
+/// With `scale` set it makes a decoder block's input instead:
+/// u = Snake(v scale + shift, alpha) per frame f
 /// and channel c of a [frames][channels] output, window = x2 [frames][2
 /// channels] with x2[f] = [u(f) | u(f - 1)] and u(-1) = state (copied into
 /// x2[0]'s second half by the first row block's workgroups; a later kernel
@@ -371,6 +312,202 @@ __global__ __launch_bounds__(W * kWave) void F32SkinnyKernel(
   }
 }
 
+// ---- float32 products of many rows --------------------------------------------
+//
+// y[t][n] (+)= x[t][k] W[n][k]^T on v_mfma_f32_16x16x4_f32 over 32 x 32
+// output tiles (grid: column tiles x row tiles), for products whose
+// column tiles would each re-read many rows of x. Eight waves, two per
+// SIMD: wave w owns the 16 x 16 quadrant w % 4 and, of each stage's 64
+// columns of k, the half w / 4; the halves' sums meet once, at the end, in
+// LDS. Per stage the workgroup's 512 threads bring both 32 x 64 operand
+// tiles into LDS with one 16-byte load each (the loads of the four stages
+// after it are in flight while one is multiplied; two LDS buffers, one
+// barrier per stage); a wave then reads its rows and columns back as 16-byte chunks,
+// lane (r = L % 16, g = L / 16) the k-slots 16 j + 4 g .. + 3 of row r,
+// and step s of four multiplies slot 16 j + 4 g + s. Rows are 68 floats
+// apart in LDS: the 16 rows of a read fall on two passes of the 32 banks.
+// The epilogue is F32SkinnyKernel's (bias, unit window or block input).
+
+constexpr int kTileRows = 32;
+constexpr int kTileK = 128;
+constexpr int kTileStride = kTileK + 4;
+constexpr int kTileThreads = 512;
+constexpr int kTileDepth = 2;
+
+__global__ __launch_bounds__(kTileThreads) void F32TileKernel(const float* x, const float* w, float* y,
+                                                     int t, int k, int n, int accumulate,
+                                                     UnitWindow unit) {
+  __shared__ float xs[2][kTileRows][kTileStride];
+  __shared__ float ws[2][kTileRows][kTileStride];
+  const int tid = static_cast<int>(threadIdx.x);
+  const int lane = tid % kWave;
+  const int wave = tid / kWave;
+  const int quadrant = wave % 4;
+  const int half = wave / 4;      // the wave's half of each stage's k
+  const int wm = quadrant / 2;    // the quadrant's 16-row half of the tile
+  const int wn = quadrant % 2;    // its 16-column half
+  const int r = lane % 16;
+  const int g = lane / 16;
+  const int n0 = kTileRows * static_cast<int>(blockIdx.x);
+  const int row0 = kTileRows * static_cast<int>(blockIdx.y);
+  const bool block_input = unit.scale != nullptr;
+  if (unit.window != nullptr && blockIdx.y == 0) {
+    float* head = unit.window + (block_input ? unit.channels : 0);
+    for (int e = static_cast<int>(blockIdx.x * blockDim.x) + tid; e < unit.head;
+         e += static_cast<int>(gridDim.x * blockDim.x))
+      head[e] = unit.state[e];
+  }
+  const __amdgpu_buffer_rsrc_t w_buffer =
+      vx::q8::BufferOf(w, 4U * static_cast<std::uint32_t>(n) * static_cast<std::uint32_t>(k));
+  const __amdgpu_buffer_rsrc_t x_buffer =
+      vx::q8::BufferOf(x, 4U * static_cast<std::uint32_t>(t) * static_cast<std::uint32_t>(k));
+  // Thread tid's 16-byte chunks of each operand tile: chunk q = tid + 512 h
+  // is row q / 32, columns 4 (q % 32) .. + 3 of the stage.
+  struct StageRegs {
+    float4 x[2];
+    float4 w[2];
+  };
+  const auto load_stage = [&](int k0, StageRegs& v) {
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const int q = tid + kTileThreads * h;
+      const int row = q / 32;
+      const int column = k0 + 4 * (q % 32);
+      const bool k_ok = column < k;
+      v.x[h] = __builtin_bit_cast(
+          float4, vx::q8::BufferLoad16(
+                      x_buffer, 4U * static_cast<std::uint32_t>((row0 + row) * k + column),
+                      k_ok && row0 + row < t));
+      v.w[h] = __builtin_bit_cast(
+          float4, vx::q8::BufferLoad16(
+                      w_buffer, 4U * static_cast<std::uint32_t>((n0 + row) * k + column),
+                      k_ok && n0 + row < n));
+    }
+  };
+  const auto store_stage = [&](int buffer, const StageRegs& v) {
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const int q = tid + kTileThreads * h;
+      *reinterpret_cast<float4*>(&xs[buffer][q / 32][4 * (q % 32)]) = v.x[h];
+      *reinterpret_cast<float4*>(&ws[buffer][q / 32][4 * (q % 32)]) = v.w[h];
+    }
+  };
+
+  // The epilogue's operands, loaded beside the first stage.
+  const int out_column = n0 + 16 * wn + r;
+  const bool windowed = unit.window != nullptr;
+  const std::uint32_t channel_bytes = 4U * static_cast<std::uint32_t>(unit.channels);
+  const __amdgpu_buffer_rsrc_t y_buffer =
+      vx::q8::BufferOf(y, 4U * static_cast<std::uint32_t>(t) * static_cast<std::uint32_t>(n));
+  const __amdgpu_buffer_rsrc_t bias_buffer =
+      vx::q8::BufferOf(unit.bias, windowed && unit.bias != nullptr ? channel_bytes : 0U);
+  const __amdgpu_buffer_rsrc_t alpha_buffer =
+      vx::q8::BufferOf(unit.alpha, windowed ? channel_bytes : 0U);
+  const __amdgpu_buffer_rsrc_t scale_buffer =
+      vx::q8::BufferOf(unit.scale, windowed && block_input ? channel_bytes : 0U);
+  const __amdgpu_buffer_rsrc_t shift_buffer =
+      vx::q8::BufferOf(unit.shift, windowed && block_input ? channel_bytes : 0U);
+  const bool column_ok = out_column < n;
+  const std::uint32_t channel_at =
+      4U * static_cast<std::uint32_t>(column_ok ? out_column % unit.channels : 0);
+  const float bias = __builtin_bit_cast(
+      float, vx::q8::BufferLoad4(bias_buffer, channel_at,
+                                 column_ok && windowed && unit.bias != nullptr));
+  const float alpha =
+      __builtin_bit_cast(float, vx::q8::BufferLoad4(alpha_buffer, channel_at, column_ok && windowed));
+  const bool block_live = column_ok && windowed && block_input;
+  const float scale =
+      __builtin_bit_cast(float, vx::q8::BufferLoad4(scale_buffer, channel_at, block_live));
+  const float shift =
+      __builtin_bit_cast(float, vx::q8::BufferLoad4(shift_buffer, channel_at, block_live));
+  float prior[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int row = row0 + 16 * wm + 4 * g + i;
+    prior[i] = __builtin_bit_cast(
+        float, vx::q8::BufferLoad4(y_buffer, 4U * static_cast<std::uint32_t>(row * n + out_column),
+                                   row < t && column_ok && accumulate != 0));
+  }
+
+  F32x4 acc = F32x4{0.0F, 0.0F, 0.0F, 0.0F};
+  const int stages = (k + kTileK - 1) / kTileK;
+  // kTileDepth stages' loads in flight: a stage's products take far less
+  // time than a load's round trip.
+  StageRegs regs[kTileDepth];
+#pragma unroll
+  for (int p = 0; p < kTileDepth; ++p)
+    load_stage(p * kTileK, regs[p]);  // stages past k load zeros
+  for (int s0 = 0; s0 < stages; s0 += kTileDepth) {
+#pragma unroll
+    for (int p = 0; p < kTileDepth; ++p) {
+      const int s = s0 + p;
+      if (s >= stages)
+        break;
+      const int buffer = s % 2;
+      store_stage(buffer, regs[p]);
+      __syncthreads();
+      if (s + kTileDepth < stages)
+        load_stage((s + kTileDepth) * kTileK, regs[p]);
+      // The wave's half of the stage: its operand chunks read at once,
+      // then the products.
+      constexpr int kChunks = kTileK / 32;
+      float4 a[kChunks], b[kChunks];
+#pragma unroll
+      for (int jj = 0; jj < kChunks; ++jj) {
+        const int j = kChunks * half + jj;
+        a[jj] = *reinterpret_cast<const float4*>(&xs[buffer][16 * wm + r][16 * j + 4 * g]);
+        b[jj] = *reinterpret_cast<const float4*>(&ws[buffer][16 * wn + r][16 * j + 4 * g]);
+      }
+#pragma unroll
+      for (int jj = 0; jj < kChunks; ++jj) {
+        acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a[jj].x, b[jj].x, acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a[jj].y, b[jj].y, acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a[jj].z, b[jj].z, acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a[jj].w, b[jj].w, acc, 0, 0, 0);
+      }
+    }
+  }
+  // The second halves' sums join the first halves' (through the first LDS
+  // operand buffer, which the last stage no longer reads once every wave
+  // has passed this barrier).
+  __syncthreads();
+  float* meet = &xs[0][0][0];
+  if (half == 1) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      meet[(quadrant * 4 + i) * kWave + lane] = acc[i];
+  }
+  __syncthreads();
+  if (half == 1 || !column_ok)
+    return;
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+    acc[i] += meet[(quadrant * 4 + i) * kWave + lane];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int row = row0 + 16 * wm + 4 * g + i;
+    if (row >= t)
+      continue;
+    float v = accumulate != 0 ? prior[i] + acc[i] : acc[i];
+    const std::size_t at = static_cast<std::size_t>(row) * n + out_column;
+    if (windowed) {
+      if (unit.bias != nullptr)
+        v += bias;
+      if (block_input) {
+        // The output is [frames][channels]: frame `row`, channel out_column.
+        const float u = Snake(v * scale + shift, alpha);
+        const std::size_t c = static_cast<std::size_t>(unit.channels);
+        unit.window[static_cast<std::size_t>(row) * 2 * c + out_column] = u;
+        if (row + 1 < unit.frames)
+          unit.window[static_cast<std::size_t>(row + 1) * 2 * c + c + out_column] = u;
+      } else {
+        unit.window[static_cast<std::size_t>(unit.head) + at] = Snake(v, alpha);
+      }
+    }
+    y[at] = v;
+  }
+}
+
 /// W2[(r out + o)][k]: k < in the tap r of input channel k, k >= in the tap
 /// r + s of channel k - in, from ConvTranspose1d's [in][out][2 s].
 __global__ void RepackUpKernel(const float* up, float* w2, std::size_t in, std::size_t out,
@@ -424,7 +561,6 @@ struct vx_vae {
   std::vector<Block> blocks;
   std::size_t out_channels = 0;
   std::size_t hop = 1;
-  rocblas_handle blas = nullptr;
   float* in_state = nullptr;   // [6][latent]
   float* out_state = nullptr;  // [6][out_channels]
   float* hidden = nullptr;
@@ -434,13 +570,11 @@ struct vx_vae {
   std::size_t capacity_frames = 0;
   GraphKey graph_key;
   hipGraphExec_t graph = nullptr;
-  bool seen = false;  // the key has run once eagerly (the library's lazy setup)
+  bool seen = false;  // the key has run once eagerly before its capture
 
   ~vx_vae() {
     if (graph != nullptr)
       (void)hipGraphExecDestroy(graph);
-    if (blas != nullptr)
-      (void)rocblas_destroy_handle(blas);
     for (Block& b : blocks) {
       (void)hipFree(b.up2);
       (void)hipFree(b.state);
@@ -457,15 +591,15 @@ struct vx_vae {
   /// groups of 16 and its workgroups re-read at most 32 MiB of x between
   /// them (one x read per 16 columns): every product of VoxCPM2's decoder
   /// but block 2's transposed convolution (192 rows x 2048 over 1280
-  /// columns), which rocBLAS tiles in both dimensions.
+  /// columns), which F32TileKernel tiles in both dimensions.
   static bool Skinny(std::size_t t, std::size_t k, std::size_t n) {
     const std::size_t x_reads = t * k * sizeof(float) * ((n + 15) / 16);
     return k % 16 == 0 && n * k * sizeof(float) < (std::size_t{1} << 32) &&
            (t <= 32 || x_reads <= (std::size_t{32} << 20));
   }
 
-  /// With `unit.window` set (and Skinny), the product's epilogue also makes
-  /// the next residual unit's input window.
+  /// With `unit.window` set, the product's epilogue also makes its
+  /// consumer's input. k a multiple of 4 (checked at create).
   int Gemm(const float* x, const float* w, float* y, std::size_t t, std::size_t k, std::size_t n,
            bool accumulate, hipStream_t stream, const UnitWindow& unit = UnitWindow{}) {
     if (Skinny(t, k, n)) {
@@ -495,14 +629,14 @@ struct vx_vae {
       }
       return VX_OK;
     }
-    const float alpha = 1.0F;
-    const float beta = accumulate ? 1.0F : 0.0F;
-    if (rocblas_sgemm(blas, rocblas_operation_transpose, rocblas_operation_none,
-                      static_cast<rocblas_int>(n), static_cast<rocblas_int>(t),
-                      static_cast<rocblas_int>(k), &alpha, w, static_cast<rocblas_int>(k), x,
-                      static_cast<rocblas_int>(k), &beta, y,
-                      static_cast<rocblas_int>(n)) != rocblas_status_success)
-      return vx::Fail(VX_HIP_ERROR, "vx_vae_decode: rocblas_sgemm");
+    if (k % 4 != 0 || std::max(n, t) * k * sizeof(float) >= (std::size_t{1} << 32) ||
+        t * n * sizeof(float) >= (std::size_t{1} << 32))
+      return vx::Fail(VX_UNSUPPORTED, "vx_vae_decode: product shape");
+    const dim3 grid(static_cast<unsigned>((n + kTileRows - 1) / kTileRows),
+                    static_cast<unsigned>((t + kTileRows - 1) / kTileRows));
+    F32TileKernel<<<grid, kTileThreads, 0, stream>>>(x, w, y, static_cast<int>(t),
+                                                     static_cast<int>(k), static_cast<int>(n),
+                                                     accumulate ? 1 : 0, unit);
     return VX_OK;
   }
 
@@ -534,9 +668,6 @@ struct vx_vae {
   }
 
   int Launch(const float* latents, std::size_t frames, float* samples, hipStream_t stream) {
-    VX_TRY(rocblas_set_stream(blas, stream) == rocblas_status_success
-               ? VX_OK
-               : vx::Fail(VX_HIP_ERROR, "vx_vae_decode: rocblas_set_stream"));
     const std::size_t latent = shape.latent_dim;
     // The residual stream and the transposed convolutions' outputs trade
     // buffers block by block (locals: every call starts from the same two).
@@ -548,13 +679,11 @@ struct vx_vae {
     DepthwiseKernel<<<Blocks(std::max(t, std::size_t{kTaps - 1}) * latent), kThreads, 0,
                       stream>>>(work, weights.in_depthwise, weights.in_depthwise_bias, nullptr,
                                 scratch, in_state, t, latent, 1);
-    // Each product's epilogue makes its consumer's input where the product
-    // is ours: a block's input x2 (in work; unit 0's depthwise kernel then
-    // refreshes the block's state from x2's last frame), a unit's window
-    // (in scratch) or the output window (in scratch). Otherwise the
-    // elementwise kernel does, with the product's bias still pending. The
-    // depthwise outputs go to the stream buffer the block's transposed
-    // convolution left behind.
+    // Each product's epilogue makes its consumer's input: a block's input
+    // x2 (in work; unit 0's depthwise kernel then refreshes the block's
+    // state from x2's last frame), a unit's window (in scratch) or the
+    // output window (in scratch). The depthwise outputs go to the stream
+    // buffer the block's transposed convolution left behind.
     const auto block_input_of = [&](const Block& b, const float* bias) {
       UnitWindow unit;
       unit.bias = bias;
@@ -579,63 +708,41 @@ struct vx_vae {
       unit.channels = static_cast<int>(c);
       return unit;
     };
-    // The consumer's input made by the last product, if any.
-    bool made = !blocks.empty() && Skinny(t, latent, shape.decoder_dim);
     VX_TRY(Gemm(scratch, weights.in_pointwise, stream_rows, t, latent, shape.decoder_dim, false,
-                stream,
-                made ? block_input_of(blocks.front(), weights.in_pointwise_bias) : UnitWindow{}));
-    const float* pending = made ? nullptr : weights.in_pointwise_bias;
+                stream, block_input_of(blocks.front(), weights.in_pointwise_bias)));
     for (std::size_t bi = 0; bi < blocks.size(); ++bi) {
       Block& b = blocks[bi];
-      const bool block_made = made;
-      if (!made)
-        BlockInputKernel<<<Blocks(t * b.in), kThreads, 0, stream>>>(
-            stream_rows, pending, b.w.scale, b.w.bias, b.w.alpha, work, b.state, t, b.in);
       const std::size_t t_in = t;
       const std::size_t c = b.out;
-      made = Skinny(t, 2 * b.in, b.stride * c);
       VX_TRY(Gemm(work, b.up2, next_rows, t, 2 * b.in, b.stride * c, false, stream,
-                  made ? window_of(b.w.units[0].alpha_in, b.unit_state[0], kTaps - 1, c,
-                                   b.w.up_bias)
-                       : UnitWindow{}));
+                  window_of(b.w.units[0].alpha_in, b.unit_state[0], kTaps - 1, c, b.w.up_bias)));
       std::swap(stream_rows, next_rows);
-      pending = made ? nullptr : b.w.up_bias;
       t *= b.stride;
       for (int u = 0; u < 3; ++u) {
         const vx_vae_unit& unit = b.w.units[u];
         const int d = kDilations[u];
         const std::size_t rows = static_cast<std::size_t>(kTaps - 1) * d;
-        if (!made)
-          UnitInputKernel<<<Blocks(std::max(t, rows) * c), kThreads, 0, stream>>>(
-              stream_rows, pending, unit.alpha_in, b.unit_state[u], scratch, t, c, d);
-        const bool refresh = u == 0 && block_made;
+        const bool refresh = u == 0;
         DepthwiseKernel<<<Blocks(std::max(t, rows) * c), kThreads, 0, stream>>>(
             scratch, unit.depthwise, unit.depthwise_bias, unit.alpha_out, next_rows,
             b.unit_state[u], t, c, d, refresh ? work + (t_in - 1) * 2 * b.in : nullptr,
             refresh ? b.state : nullptr, refresh ? b.in : 0);
         // The next consumer: unit u + 1, the next block's input or the output.
         UnitWindow next;
-        made = Skinny(t, c, c);
-        if (made && u < 2) {
+        if (u < 2) {
           const int dn = kDilations[u + 1];
           next = window_of(b.w.units[u + 1].alpha_in, b.unit_state[u + 1], (kTaps - 1) * dn, c,
                            unit.pointwise_bias);
-        } else if (made && bi + 1 < blocks.size()) {
+        } else if (bi + 1 < blocks.size()) {
           next = block_input_of(blocks[bi + 1], unit.pointwise_bias);
-        } else if (made) {
+        } else {
           next = window_of(weights.out_alpha, out_state, kTaps - 1, c, unit.pointwise_bias);
         }
         VX_TRY(Gemm(next_rows, unit.pointwise, stream_rows, t, c, c, true, stream, next));
-        pending = made ? nullptr : unit.pointwise_bias;
       }
     }
     const std::size_t c = out_channels;
     float* out_window = scratch;
-    if (!made) {
-      OutputInputKernel<<<Blocks(std::max(t, std::size_t{kTaps - 1}) * c), kThreads, 0,
-                          stream>>>(stream_rows, pending, weights.out_alpha, out_state,
-                                    out_window, t, c);
-    }
     ToMonoKernel<<<static_cast<unsigned>((t + 3) / 4), kThreads, 0, stream>>>(
         out_window, weights.out_conv, weights.out_bias, samples, out_state, t, c);
     return vx::LaunchStatus("vx_vae_decode");
@@ -663,6 +770,10 @@ int vx_vae_create(vx_vae** vae, const vx_vae_shape* shape, const vx_vae_weights*
       shape->rate_count > 8 || (shape->decoder_dim >> shape->rate_count) == 0 ||
       shape->decoder_dim % (std::size_t{1} << shape->rate_count) != 0)
     return vx::Fail(VX_BAD_ARG, "vx_vae_create: bad shape");
+  // The products read x and the weights 16 bytes at a time along k.
+  if (shape->latent_dim % 4 != 0 || (shape->decoder_dim >> shape->rate_count) % 4 != 0)
+    return vx::Fail(VX_UNSUPPORTED,
+                    "vx_vae_create: latent and channel counts must be multiples of 4");
   if (weights->blocks == nullptr || weights->in_depthwise == nullptr ||
       weights->in_depthwise_bias == nullptr || weights->in_pointwise == nullptr ||
       weights->in_pointwise_bias == nullptr || weights->out_alpha == nullptr ||
@@ -714,8 +825,6 @@ int vx_vae_create(vx_vae** vae, const vx_vae_shape* shape, const vx_vae_weights*
     status = Allocate(&created->in_state, (kTaps - 1) * shape->latent_dim, "vx_vae: hipMalloc");
   if (status == VX_OK)
     status = Allocate(&created->out_state, (kTaps - 1) * c, "vx_vae: hipMalloc");
-  if (status == VX_OK && rocblas_create_handle(&created->blas) != rocblas_status_success)
-    status = vx::Fail(VX_HIP_ERROR, "vx_vae_create: rocblas_create_handle");
   if (status == VX_OK && hipDeviceSynchronize() != hipSuccess)
     status = vx::Fail(VX_HIP_ERROR, "vx_vae_create: repack");
   if (status != VX_OK) {
