@@ -99,6 +99,44 @@ __device__ inline void StoreB(Bf16* at, const Lanes<V>& in) {
     *at = Bf16Bits(in.v[0]);
 }
 
+/// V float32 values at byte `offset` of `buffer`, zero (no access) unless
+/// `keep`: a masked buffer load, no branch, so a wave's loads stay in
+/// flight together.
+template<int V>
+__device__ inline Lanes<V> BufferF(__amdgpu_buffer_rsrc_t buffer, std::uint32_t offset,
+                                   bool keep) {
+  Lanes<V> out;
+  if constexpr (V == 4) {
+    const float4 f = __builtin_bit_cast(float4, q8::BufferLoad16(buffer, offset, keep));
+    out.v[0] = f.x;
+    out.v[1] = f.y;
+    out.v[2] = f.z;
+    out.v[3] = f.w;
+  } else {
+    out.v[0] = __builtin_bit_cast(float, q8::BufferLoad4(buffer, offset, keep));
+  }
+  return out;
+}
+
+/// V bf16 values at byte `offset` of `buffer` as float32, zero unless
+/// `keep`.
+template<int V>
+__device__ inline Lanes<V> BufferB(__amdgpu_buffer_rsrc_t buffer, std::uint32_t offset,
+                                   bool keep) {
+  Lanes<V> out;
+  const int at = static_cast<int>(keep ? offset : q8::kPastBuffer);
+  if constexpr (V == 4) {
+    const auto b = __builtin_amdgcn_raw_buffer_load_b64(buffer, at, 0, 0);
+    out.v[0] = q8::Bf16Lo(b[0]);
+    out.v[1] = q8::Bf16Hi(b[0]);
+    out.v[2] = q8::Bf16Lo(b[1]);
+    out.v[3] = q8::Bf16Hi(b[1]);
+  } else {
+    out.v[0] = q8::Bf16Lo(__builtin_amdgcn_raw_buffer_load_b16(buffer, at, 0, 0));
+  }
+  return out;
+}
+
 bool Aligned(const void* pointer, std::size_t bytes) {
   return reinterpret_cast<std::uintptr_t>(pointer) % bytes == 0;
 }
@@ -122,8 +160,10 @@ bool Quads(std::initializer_list<const float*> floats, std::initializer_list<con
 constexpr int kNormWaves = 4;  // rows per workgroup, one per wave
 
 /// One row per wave. Lane l reads accesses l, l + 64, ... of the row (V
-/// values each) and keeps the first kHeld of them in registers for the
-/// second pass (rows up to 2048 values; longer rows read the rest again).
+/// values each) and keeps the first kHeld of them, with their norm weights,
+/// in registers for the second pass (rows up to 2048 values; longer rows
+/// read the rest again). The held accesses are masked buffer loads issued
+/// together, so the row arrives in one memory round trip.
 /// The lanes' sums of squares meet by a wave butterfly; the output is
 /// bf16((x * inv) * gamma) with inv = rsqrt(mean(x^2) + eps), the
 /// reference's arithmetic (kernels/generator_kernels.hip:91-108), and its
@@ -139,16 +179,29 @@ __global__ __launch_bounds__(kNormWaves * kWave) void WaveNormKernel(
     return;
   const std::size_t base = static_cast<std::size_t>(row) * width;
   const int accesses = width / V;
+  const __amdgpu_buffer_rsrc_t row_buffer =
+      q8::BufferOf(input + base, 4U * static_cast<std::uint32_t>(width));
+  const __amdgpu_buffer_rsrc_t gamma_buffer =
+      q8::BufferOf(weight, 2U * static_cast<std::uint32_t>(width));
   Lanes<V> held[kHeld];
-  float squares = 0.0F;
+  Lanes<V> held_gamma[kHeld];
 #pragma unroll
   for (int j = 0; j < kHeld; ++j) {
     const int c = lane + kWave * j;
-    held[j] = c < accesses ? LoadF<V>(input + base + V * c) : Lanes<V>{};
+    held[j] = BufferF<V>(row_buffer, 4U * V * static_cast<std::uint32_t>(c), c < accesses);
+  }
+#pragma unroll
+  for (int j = 0; j < kHeld; ++j) {
+    const int c = lane + kWave * j;
+    held_gamma[j] =
+        BufferB<V>(gamma_buffer, 2U * V * static_cast<std::uint32_t>(c), c < accesses);
+  }
+  float squares = 0.0F;
+#pragma unroll
+  for (int j = 0; j < kHeld; ++j)
 #pragma unroll
     for (int i = 0; i < V; ++i)
       squares += held[j].v[i] * held[j].v[i];
-  }
   for (int c = lane + kWave * kHeld; c < accesses; c += kWave) {
     const Lanes<V> x = LoadF<V>(input + base + V * c);
 #pragma unroll
@@ -156,8 +209,7 @@ __global__ __launch_bounds__(kNormWaves * kWave) void WaveNormKernel(
       squares += x.v[i] * x.v[i];
   }
   const float inverse = rsqrtf(WaveSum(squares) / static_cast<float>(width) + epsilon);
-  const auto emit = [&](int c, const Lanes<V>& x) {
-    const Lanes<V> gamma = LoadB<V>(weight + V * c);
+  const auto emit = [&](int c, const Lanes<V>& x, const Lanes<V>& gamma) {
     Lanes<V> y;
 #pragma unroll
     for (int i = 0; i < V; ++i)
@@ -170,10 +222,10 @@ __global__ __launch_bounds__(kNormWaves * kWave) void WaveNormKernel(
   for (int j = 0; j < kHeld; ++j) {
     const int c = lane + kWave * j;
     if (c < accesses)
-      emit(c, held[j]);
+      emit(c, held[j], held_gamma[j]);
   }
   for (int c = lane + kWave * kHeld; c < accesses; c += kWave)
-    emit(c, LoadF<V>(input + base + V * c));
+    emit(c, LoadF<V>(input + base + V * c), LoadB<V>(weight + V * c));
 }
 
 /// One workgroup per (row, head of q | k | v), one thread per rotated pair
