@@ -12,8 +12,8 @@
 // expand the next step's weights to bf16 once for the whole workgroup and
 // store both into the other half of a double-buffered LDS tile, and
 // multiply the current half. Every 16-byte LDS chunk of a 128-byte row sits
-// at chunk ^ (row % 8), so that the 32 rows of an operand read fall on
-// different banks. Tiles of one weight tile are placed on one compute die
+// at chunk ^ ((row / 2) % 8), so that the 16 rows one 16-lane group reads
+// fall on different banks. Tiles of one weight tile are placed on one compute die
 // (workgroup b runs on die b % 8), whose L2 then serves their shared
 // weights; grids of few tiles split k over workgroups whose partial sums a
 // second launch adds in split order.
@@ -86,8 +86,13 @@ __device__ inline int DieOrdered(int b, int blocks) {
 }
 
 /// LDS index of 16-byte chunk `chunk` (0..7) of row `row` of a 128-byte-row
-/// operand tile.
-__device__ inline int Swizzled(int row, int chunk) { return row * 8 + (chunk ^ (row & 7)); }
+/// operand tile: chunk ^ ((row / 2) % 8). Rows alternate between the two
+/// 128-byte halves of a 256-byte bank line, so the 16 rows of a 16-lane
+/// group land on 16 different 16-byte bank groups (XOR with row % 8 put
+/// rows r and r + 8 on one: measured 2-4 % slower on MI355X).
+__device__ inline int Swizzled(int row, int chunk) {
+  return row * 8 + (chunk ^ ((row >> 1) & 7));
+}
 
 /// MODE: 1 Q8_0 panels expanded, 2 bf16 panels (TiledMode). D: register
 /// sets of prefetched steps (1 or 2).
