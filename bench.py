@@ -110,16 +110,24 @@ def graph_of(torch, stream, body, count: int):
     return graph
 
 
-def time_graph(torch, stream, graph) -> float:
-    """Seconds of one replay, events on the replay stream."""
+def time_graph(torch, stream, graph, repeats: int = 1, warm_seconds: float = 0.0) -> float:
+    """Seconds of one replay (the median of `repeats`), events on the replay
+    stream, after replaying for `warm_seconds` untimed."""
     start = torch.cuda.Event(enable_timing=True)
     stop = torch.cuda.Event(enable_timing=True)
-    stream.synchronize()
-    start.record(stream)
-    graph.replay()
-    stop.record(stream)
-    stop.synchronize()
-    return start.elapsed_time(stop) / 1e3
+    begin = time.perf_counter()
+    while time.perf_counter() - begin < warm_seconds:
+        graph.replay()
+        stream.synchronize()
+    times = []
+    for _ in range(repeats):
+        stream.synchronize()
+        start.record(stream)
+        graph.replay()
+        stop.record(stream)
+        stop.synchronize()
+        times.append(start.elapsed_time(stop) / 1e3)
+    return float(np.median(times))
 
 
 def read_probe(torch, device, stream) -> float:
@@ -496,8 +504,11 @@ def gpu_prefill(args, torch, ops, synth, device, stream):
             g = graph_of(torch, stream,
                          lambda i: ops.q8_linear(x, pool[i % copies], n, y=y, scratch=scratch),
                          count)
-            g.replay()
-            seconds = time_graph(torch, stream, g) / count
+            # Median of five replays after 0.2 s of untimed ones: the
+            # products follow seconds of host-side weight generation, and
+            # the first milliseconds of matrix-core work after an idle GPU
+            # run slower than a prefill's steady state.
+            seconds = time_graph(torch, stream, g, repeats=5, warm_seconds=0.2) / count
             tflops = 2.0 * m * n * k / seconds / 1e12
             rows.append({"m": m, "k": k, "n": n, "us": round(seconds * 1e6, 2),
                          "tflops": round(tflops, 1),
