@@ -174,7 +174,10 @@ __global__ __launch_bounds__(kNormWaves * kWave) void WaveNormKernel(
     int width, float epsilon) {
   constexpr int kHeld = 32 / V;
   const int lane = static_cast<int>(threadIdx.x) % kWave;
-  const int row = static_cast<int>(blockIdx.x) * kNormWaves + static_cast<int>(threadIdx.x) / kWave;
+  // One row per wave: readfirstlane puts the row (and the buffer made from
+  // it) in scalar registers, which buffer loads need.
+  const int row = __builtin_amdgcn_readfirstlane(static_cast<int>(blockIdx.x) * kNormWaves +
+                                                 static_cast<int>(threadIdx.x) / kWave);
   if (row >= rows)
     return;
   const std::size_t base = static_cast<std::size_t>(row) * width;

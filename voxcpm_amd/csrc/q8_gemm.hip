@@ -121,10 +121,12 @@ __global__ __launch_bounds__(WM * WN * kWave) void GemmKernel(GemmArgs a) {
   const int octet = lane / 16;
   const int tiles = a.m_tiles * a.n_tiles;
   const int logical = DieOrdered(static_cast<int>(blockIdx.x), tiles * a.splits);
-  const int split = logical / tiles;
-  const int tile = logical % tiles;
-  const int row0 = (tile % a.m_tiles) * BM;
-  const int group0 = (tile / a.m_tiles) * (BN / 16);
+  // The divisions run on the vector unit: readfirstlane keeps the tile's
+  // coordinates (and the weight buffer made from them) in scalar registers.
+  const int split = __builtin_amdgcn_readfirstlane(logical / tiles);
+  const int tile = __builtin_amdgcn_readfirstlane(logical % tiles);
+  const int row0 = __builtin_amdgcn_readfirstlane((tile % a.m_tiles) * BM);
+  const int group0 = __builtin_amdgcn_readfirstlane((tile / a.m_tiles) * (BN / 16));
   const __amdgpu_buffer_rsrc_t x_buffer = q8::BufferOf(
       a.x, 2U * static_cast<std::uint32_t>(a.m) * static_cast<std::uint32_t>(a.k));
   const int first_pair = split * a.pairs_per_split;
