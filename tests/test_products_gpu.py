@@ -230,13 +230,15 @@ def test_tiled_exact_products(vx, oracle, cuda, stream, rows, k, n):
         assert worst <= LIMIT, f"accumulate {accumulate}: worst {worst:.3e}"
 
 
-def test_bf16_output_is_rounded_float_output(vx, cuda, stream):
-    k, n, rows = 1024, 4096, 22
+@pytest.mark.parametrize("rows,k,n", [(22, 1024, 4096),
+                                      # the prefill kernel, ragged rows and columns
+                                      (600, 1024, 6160)])
+def test_bf16_output_is_rounded_float_output(vx, cuda, stream, rows, k, n):
     rng = synth.Rng(0, 3)
     blocks = synth.q8_blocks(rng, n, k)
     packed = vx.q8_pack(to_device(blocks, cuda), n, k)
     x_dev = to_device(synth.activations(rng, rows, k), cuda)
-    scratch = vx.Scratch(32, n)
+    scratch = vx.Scratch(min(rows, 128), n)
     y32 = vx.q8_linear(x_dev, packed, n, scratch=scratch)
     y16 = vx.q8_linear_bf16(x_dev, packed, n, scratch=scratch)
     torch.cuda.synchronize()
@@ -283,7 +285,10 @@ def expanded_check(y, x, blocks, oracle, before=None):
                                       (700, 1024, 4112),
                                       # columns not a multiple of 4 (the split
                                       # reduction's scalar path)
-                                      (200, 512, 1042)])
+                                      (200, 512, 1042),
+                                      # the prefill kernel's ragged rows and
+                                      # columns (256-row, 128/256-column tiles)
+                                      (700, 1024, 6160)])
 def test_prefill_expansion(vx, oracle, cuda, stream, rows, k, n):
     """More than 128 rows: W as bf16(scale * q), float32 sums; the
     reference allows 1e-4 there (products_test.cpp:301-309)."""

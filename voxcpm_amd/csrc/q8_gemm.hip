@@ -20,6 +20,7 @@
 #include <hip/hip_runtime.h>
 
 #include <cstdint>
+#include <type_traits>
 
 #include "common.hpp"
 #include "products.hpp"
@@ -149,11 +150,14 @@ __global__ __launch_bounds__(WM * WN * kWave) void GemmKernel(GemmArgs a) {
   // so rows past m, columns past k, groups past n and dead steps cost no
   // traffic, and with no branch around them the compiler counts the loads
   // in flight and waits for the oldest step only.
-  const auto fetch = [&](int step, Staging& s) {
+  // Part `part` of 4 (or all parts, part < 0) of a step's loads.
+  const auto fetch = [&](int step, Staging& s, int part = -1) {
     const int pair = first_pair + step;
     const bool live = step < steps;
 #pragma unroll
     for (int i = 0; i < kAPieces; ++i) {
+      if (part >= 0 && i % 4 != part)
+        continue;
       const int piece = tid + kThreads * i;
       const int row = row0 + piece / 8;
       const int column = 64 * pair + 8 * (piece % 8);
@@ -162,6 +166,8 @@ __global__ __launch_bounds__(WM * WN * kWave) void GemmKernel(GemmArgs a) {
     }
 #pragma unroll
     for (int u = 0; u < kUnits; ++u) {
+      if (part >= 0 && (kAPieces + u) % 4 != part)
+        continue;
       const int group = kUnits * wave + u;
       const bool ok = live && group < live_groups;
       const std::uint32_t unit = static_cast<std::uint32_t>(group) * group_bytes +
@@ -215,7 +221,12 @@ __global__ __launch_bounds__(WM * WN * kWave) void GemmKernel(GemmArgs a) {
   // The multiply of one LDS stage with the next stage's store spread over
   // its four 16-column reduction steps (measured 2-7 % faster on MI355X than
   // storing after the multiply).
-  const auto compute_store = [&](int stage, int next, const Staging& s) {
+  // With D = 2 the loads of step `ahead` (into `later`, the other register
+  // set) are issued a quarter at a time after each reduction step's
+  // products, so that their issue overlaps the matrix cores' work instead
+  // of holding every wave before it (ahead < 0: none).
+  const auto compute_store = [&](int stage, int next, const Staging& s, int ahead,
+                                 Staging& later) {
     const uint4* const a_tile = lds_a + stage * BM * 8;
     const uint4* const b_tile = lds_b + stage * BN * 8;
     uint4* const a_next = lds_a + next * BM * 8;
@@ -235,6 +246,8 @@ __global__ __launch_bounds__(WM * WN * kWave) void GemmKernel(GemmArgs a) {
 #pragma unroll
         for (int j = 0; j < FN; ++j)
           acc[i][j] = Mfma32(af[i], bf[j], acc[i][j]);
+      if (ahead >= 0)
+        fetch(ahead, later, kk);
 #pragma unroll
       for (int i = kk; i < kAPieces; i += 4) {
         const int piece = tid + kThreads * i;
@@ -274,14 +287,81 @@ __global__ __launch_bounds__(WM * WN * kWave) void GemmKernel(GemmArgs a) {
       const int q = p + d;
       if (q >= steps)
         break;
-      fetch(q + D, staged[d % D]);
-      compute_store(d, 1 - d, staged[(d + 1) % D]);
+      if constexpr (D == 2) {
+        compute_store(d, 1 - d, staged[(d + 1) % D], q + D, staged[d % D]);
+      } else {
+        fetch(q + D, staged[d % D]);
+        compute_store(d, 1 - d, staged[(d + 1) % D], -1, staged[d % D]);
+      }
       __syncthreads();
     }
   }
 
   // Epilogue: element v of tile (i, j) is row 8 (v / 4) + 4 lk + v % 4 and
-  // column lr of the tile.
+  // column lr of the tile. One uniform branch picks the output; each
+  // element is then one buffer store at the lane's offset plus a constant
+  // of v (accumulation: one load, issued for the whole 32 x 32 tile before
+  // its stores). Rows past m lie past the buffer, whose range check drops
+  // them.
+  const std::size_t count = static_cast<std::size_t>(a.m) * a.n;
+  const auto emit = [&](auto kind, void* base) {
+    constexpr int K = decltype(kind)::value;  // 0 float32, 1 bf16, 2 float32 +=
+    constexpr std::uint32_t width = K == 1 ? 2 : 4;
+    const __amdgpu_buffer_rsrc_t out =
+        q8::BufferOf(base, static_cast<std::uint32_t>(count * width));
+#pragma unroll
+    for (int j = 0; j < FN; ++j) {
+      const int column = 16 * group0 + TN * wn + 32 * j + lr;
+      if (column >= a.n)
+        continue;
+#pragma unroll
+      for (int i = 0; i < FM; ++i) {
+        const std::uint32_t lane_bytes =
+            width * static_cast<std::uint32_t>((row0 + TM * wm + 32 * i + 4 * lk) * a.n + column);
+        std::uint32_t offset[16];
+#pragma unroll
+        for (int v = 0; v < 16; ++v)
+          offset[v] = lane_bytes + width * static_cast<std::uint32_t>((8 * (v / 4) + v % 4) * a.n);
+        if constexpr (K == 2) {
+          float prior[16];
+#pragma unroll
+          for (int v = 0; v < 16; ++v)
+            prior[v] = __builtin_bit_cast(
+                float, __builtin_amdgcn_raw_buffer_load_b32(out, static_cast<int>(offset[v]), 0, 0));
+#pragma unroll
+          for (int v = 0; v < 16; ++v)
+            __builtin_amdgcn_raw_buffer_store_b32(
+                __builtin_bit_cast(std::uint32_t, prior[v] + acc[i][j][v]), out,
+                static_cast<int>(offset[v]), 0, 0);
+        } else {
+#pragma unroll
+          for (int v = 0; v < 16; ++v) {
+            // The element as a value first: hipcc's bit cast of a vector
+            // element taken in place reads element 0.
+            const float value = acc[i][j][v];
+            if constexpr (K == 1)
+              __builtin_amdgcn_raw_buffer_store_b16(q8::Bf16Fast(value), out,
+                                                    static_cast<int>(offset[v]), 0, 0);
+            else
+              __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(std::uint32_t, value), out,
+                                                    static_cast<int>(offset[v]), 0, 0);
+          }
+        }
+      }
+    }
+  };
+  // Offsets stay below 2^31 bytes (rows to the last tile's end included).
+  if ((static_cast<std::size_t>(a.m) + BM) * a.n * 4 < (std::size_t{1} << 31)) {
+    if (a.splits > 1)
+      emit(std::integral_constant<int, 0>{}, a.partials + static_cast<std::size_t>(split) * count);
+    else if (a.y_bf16 != nullptr)
+      emit(std::integral_constant<int, 1>{}, a.y_bf16);
+    else if (a.accumulate)
+      emit(std::integral_constant<int, 2>{}, a.y);
+    else
+      emit(std::integral_constant<int, 0>{}, a.y);
+    return;
+  }
 #pragma unroll
   for (int j = 0; j < FN; ++j) {
     const int column = 16 * group0 + TN * wn + 32 * j + lr;
@@ -296,7 +376,7 @@ __global__ __launch_bounds__(WM * WN * kWave) void GemmKernel(GemmArgs a) {
           continue;
         const std::size_t at = static_cast<std::size_t>(row) * a.n + column;
         if (a.splits > 1)
-          a.partials[static_cast<std::size_t>(split) * a.m * a.n + at] = acc[i][j][v];
+          a.partials[static_cast<std::size_t>(split) * count + at] = acc[i][j][v];
         else if (a.y_bf16 != nullptr)
           a.y_bf16[at] = q8::Bf16Fast(acc[i][j][v]);
         else
