@@ -25,6 +25,7 @@
 #include <hip/hip_runtime.h>
 
 #include <cstdint>
+#include <type_traits>
 
 #include "common.hpp"
 #include "products.hpp"
@@ -274,6 +275,70 @@ __global__ __launch_bounds__(T::kThreads, T::kMinBlocks) void TiledKernel(TiledA
   }
 
   constexpr int kRowsPerWave = BM / (kThreads / kWave / 2);
+  // Epilogue: element e of tile (i, j) is row 4 octet + e and column r16 of
+  // the tile. One uniform branch picks the output; each element is then one
+  // buffer store at the lane's offset plus a constant of e (accumulation:
+  // the tile's loads first). Rows past m lie past the buffer, whose range
+  // check drops them.
+  const std::size_t count = static_cast<std::size_t>(a.m) * a.n;
+  const auto emit = [&](auto kind, void* base) {
+    constexpr int K = decltype(kind)::value;  // 0 float32, 1 bf16, 2 float32 +=
+    constexpr std::uint32_t width = K == 1 ? 2 : 4;
+    const __amdgpu_buffer_rsrc_t out =
+        q8::BufferOf(base, static_cast<std::uint32_t>(count * width));
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int column = 16 * group0 + 64 * wn + 16 * j + r16;
+      if (column >= a.n)
+        continue;
+#pragma unroll
+      for (int i = 0; i < kMi; ++i) {
+        const std::uint32_t lane_bytes = width * static_cast<std::uint32_t>(
+            (row0 + kRowsPerWave * wm + 16 * i + 4 * octet) * a.n + column);
+        std::uint32_t offset[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          offset[e] = lane_bytes + width * static_cast<std::uint32_t>(e * a.n);
+        // Elements as values first: hipcc's bit cast of a vector element
+        // taken in place reads element 0.
+        float value[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          value[e] = acc[i][j][e];
+        if constexpr (K == 2) {
+          float prior[4];
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+            prior[e] = __builtin_bit_cast(
+                float, __builtin_amdgcn_raw_buffer_load_b32(out, static_cast<int>(offset[e]), 0, 0));
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+            value[e] += prior[e];
+        }
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          if constexpr (K == 1)
+            __builtin_amdgcn_raw_buffer_store_b16(q8::Bf16Fast(value[e]), out,
+                                                  static_cast<int>(offset[e]), 0, 0);
+          else
+            __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(std::uint32_t, value[e]), out,
+                                                  static_cast<int>(offset[e]), 0, 0);
+        }
+      }
+    }
+  };
+  // Offsets stay below 2^31 bytes (rows to the last tile's end included).
+  if ((static_cast<std::size_t>(a.m) + BM) * a.n * 4 < (std::size_t{1} << 31)) {
+    if (a.splits > 1)
+      emit(std::integral_constant<int, 0>{}, a.partials + static_cast<std::size_t>(split) * count);
+    else if (a.y_bf16 != nullptr)
+      emit(std::integral_constant<int, 1>{}, a.y_bf16);
+    else if (a.accumulate)
+      emit(std::integral_constant<int, 2>{}, a.y);
+    else
+      emit(std::integral_constant<int, 0>{}, a.y);
+    return;
+  }
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
     const int column = 16 * group0 + 64 * wn + 16 * j + r16;
