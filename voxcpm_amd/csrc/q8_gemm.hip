@@ -150,13 +150,14 @@ __global__ __launch_bounds__(WM * WN * kWave) void GemmKernel(GemmArgs a) {
   // so rows past m, columns past k, groups past n and dead steps cost no
   // traffic, and with no branch around them the compiler counts the loads
   // in flight and waits for the oldest step only.
-  // Part `part` of 4 (or all parts, part < 0) of a step's loads.
-  const auto fetch = [&](int step, Staging& s, int part = -1) {
+  // Part `part` of 4 (or all parts, part < 0) of a step's loads: the
+  // activation pieces (what & 1) and the panel units (what & 2).
+  const auto fetch = [&](int step, Staging& s, int part = -1, int what = 3) {
     const int pair = first_pair + step;
     const bool live = step < steps;
 #pragma unroll
     for (int i = 0; i < kAPieces; ++i) {
-      if (part >= 0 && i % 4 != part)
+      if ((what & 1) == 0 || (part >= 0 && i % 4 != part))
         continue;
       const int piece = tid + kThreads * i;
       const int row = row0 + piece / 8;
@@ -166,7 +167,7 @@ __global__ __launch_bounds__(WM * WN * kWave) void GemmKernel(GemmArgs a) {
     }
 #pragma unroll
     for (int u = 0; u < kUnits; ++u) {
-      if (part >= 0 && (kAPieces + u) % 4 != part)
+      if ((what & 2) == 0 || (part >= 0 && (kAPieces + u) % 4 != part))
         continue;
       const int group = kUnits * wave + u;
       const bool ok = live && group < live_groups;
@@ -179,13 +180,13 @@ __global__ __launch_bounds__(WM * WN * kWave) void GemmKernel(GemmArgs a) {
         s.scales[u] = q8::BufferLoad4(w_buffer, unit + kValueBytes + 4U * r16, ok);
     }
   };
-  const auto store = [&](int stage, const Staging& s) {
+  const auto store = [&](int stage, const Staging& sx, const Staging& s) {
     uint4* const a_tile = lds_a + stage * BM * 8;
     uint4* const b_tile = lds_b + stage * BN * 8;
 #pragma unroll
     for (int i = 0; i < kAPieces; ++i) {
       const int piece = tid + kThreads * i;
-      a_tile[Swizzled(piece / 8, piece % 8)] = s.x[i];
+      a_tile[Swizzled(piece / 8, piece % 8)] = sx.x[i];
     }
 #pragma unroll
     for (int u = 0; u < kUnits; ++u) {
@@ -221,12 +222,12 @@ __global__ __launch_bounds__(WM * WN * kWave) void GemmKernel(GemmArgs a) {
   // The multiply of one LDS stage with the next stage's store spread over
   // its four 16-column reduction steps (measured 2-7 % faster on MI355X than
   // storing after the multiply).
-  // With D = 2 the loads of step `ahead` (into `later`, the other register
+  // With D >= 2 the loads of step `ahead` (into `later`, a free register
   // set) are issued a quarter at a time after each reduction step's
   // products, so that their issue overlaps the matrix cores' work instead
   // of holding every wave before it (ahead < 0: none).
-  const auto compute_store = [&](int stage, int next, const Staging& s, int ahead,
-                                 Staging& later) {
+  const auto compute_store = [&](int stage, int next, const Staging& sx, const Staging& s,
+                                 int ahead_x, Staging& later_x, int ahead, Staging& later) {
     const uint4* const a_tile = lds_a + stage * BM * 8;
     const uint4* const b_tile = lds_b + stage * BN * 8;
     uint4* const a_next = lds_a + next * BM * 8;
@@ -246,12 +247,14 @@ __global__ __launch_bounds__(WM * WN * kWave) void GemmKernel(GemmArgs a) {
 #pragma unroll
         for (int j = 0; j < FN; ++j)
           acc[i][j] = Mfma32(af[i], bf[j], acc[i][j]);
-      if (ahead >= 0)
-        fetch(ahead, later, kk);
+      if (ahead >= 0) {
+        fetch(ahead_x, later_x, kk, 1);
+        fetch(ahead, later, kk, 2);
+      }
 #pragma unroll
       for (int i = kk; i < kAPieces; i += 4) {
         const int piece = tid + kThreads * i;
-        a_next[Swizzled(piece / 8, piece % 8)] = s.x[i];
+        a_next[Swizzled(piece / 8, piece % 8)] = sx.x[i];
       }
 #pragma unroll
       for (int h = kk; h < 2 * kUnits; h += 4) {
@@ -271,27 +274,38 @@ __global__ __launch_bounds__(WM * WN * kWave) void GemmKernel(GemmArgs a) {
     }
   };
 
-  // D register sets: set q % D holds step q from its fetch (D steps ahead)
-  // until its store; LDS stage q % 2 holds step q while it is multiplied.
-  // The stores after the last step write zeros into a stage no later step
-  // reads.
+  // D register sets of panel units and DX = min(D, 2) of activation pieces
+  // (L2-resident, their latency shorter): set q % D (q % DX) holds step q
+  // from its fetch, D (DX) steps ahead, until its store; LDS stage q % 2
+  // holds step q while it is multiplied. The stores after the last step
+  // write zeros into a stage no later step reads.
+  constexpr int DX = D < 2 ? D : 2;
+  Staging staged_x[DX];
   Staging staged[D];
 #pragma unroll
-  for (int d = 0; d < D; ++d)
-    fetch(d, staged[d]);
-  store(0, staged[0]);
-  __syncthreads();
-  for (int p = 0; p < steps; p += 2) {
+  for (int d = 0; d < DX; ++d)
+    fetch(d, staged_x[d], -1, 1);
 #pragma unroll
-    for (int d = 0; d < 2; ++d) {
+  for (int d = 0; d < D; ++d)
+    fetch(d, staged[d], -1, 2);
+  store(0, staged_x[0], staged[0]);
+  __syncthreads();
+  // U steps per iteration (a multiple of 2 and of D), so that every set and
+  // stage index is a constant.
+  constexpr int U = D % 2 == 0 ? D : 2 * D;
+  for (int p = 0; p < steps; p += U) {
+#pragma unroll
+    for (int d = 0; d < U; ++d) {
       const int q = p + d;
       if (q >= steps)
         break;
-      if constexpr (D == 2) {
-        compute_store(d, 1 - d, staged[(d + 1) % D], q + D, staged[d % D]);
+      if constexpr (D >= 2) {
+        compute_store(d % 2, 1 - d % 2, staged_x[(d + 1) % DX], staged[(d + 1) % D], q + DX,
+                      staged_x[d % DX], q + D, staged[d % D]);
       } else {
-        fetch(q + D, staged[d % D]);
-        compute_store(d, 1 - d, staged[(d + 1) % D], -1, staged[d % D]);
+        fetch(q + 1, staged_x[0], -1, 1);
+        fetch(q + 1, staged[0], -1, 2);
+        compute_store(d % 2, 1 - d % 2, staged_x[0], staged[0], -1, staged_x[0], -1, staged[0]);
       }
       __syncthreads();
     }
@@ -445,7 +459,7 @@ struct Shape {
 using Big = Shape<256, 256, 2, 4, 1>;    // 8 waves of 128 x 64
 using Wide = Shape<128, 256, 2, 4, 2>;   // 8 waves of 64 x 64
 using Small = Shape<128, 128, 2, 2, 2>;  // 4 waves of 64 x 64
-using Tall = Shape<256, 128, 4, 2, 2>;   // 8 waves of 64 x 64
+using Tall = Shape<256, 128, 4, 2, 3>;   // 8 waves of 64 x 64, three steps prefetched
 using BigDeep = Shape<256, 256, 2, 4, 2>;
 using Narrow = Shape<128, 64, 2, 1, 2>;  // 2 waves of 64 x 64
 
