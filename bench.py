@@ -42,16 +42,16 @@ BF16_PEAK_TFLOPS = 2500.0
 # wall-clock mfma_frac of each prefill row; profiles/q8_gemm_prefill.md.
 PREFILL_MFMA_BUSY = {"source": "profiles/q8_gemm_prefill.md (rocprofv3 --pmc "
                                "SQ_VALU_MFMA_BUSY_CYCLES, GRBM_GUI_ACTIVE)",
-                     "m512_n16384": 0.283, "m1024_n16384": 0.325}
+                     "m512_n16384": 0.311, "m1024_n16384": 0.412}
 # HBM bytes per launch of the M=22 sweep kernels from two rocprofv3 PMC runs
 # (profiles/q8_skinny_m22_traffic.md): FETCH_SIZE KiB (scaled by 2.0, its
 # reading of a 256 MiB copy of known size) + WRITE_SIZE KiB (scale 1.0).
 # Measured, not computed: re-measure when the product kernel changes. Last
 # measured on the build of commit TRAFFIC_BUILD (the summary names it).
 FETCH_SCALE = 262144 / 131083.5
-TRAFFIC_BUILD = "90ae678"
-TRAFFIC_KIB = {(1024, 3072): (1833.5, 264.0), (1024, 8192): (4551.0, 704.0),
-               (2048, 2048): (2553.5, 176.0), (2048, 16384): (17806.5, 1408.0)}
+TRAFFIC_BUILD = "c79b3d4"
+TRAFFIC_KIB = {(1024, 3072): (1827.5, 264.0), (1024, 8192): (4559.0, 704.0),
+               (2048, 2048): (2547.5, 176.0), (2048, 16384): (17806.0, 1408.0)}
 # The decode steps' products (tools/bench/gemm_bench.cpp:34-38): the base and
 # residual LMs (hidden 2048, 16 + 2 x 2 heads of 128, MLP 6144) and the
 # local encoder/DiT shapes, at one row (an LM step) and five (the encoder's
