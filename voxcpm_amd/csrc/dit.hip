@@ -118,6 +118,11 @@ struct vx_dit {
   float* h_frag = nullptr;
   Bf16* attention_frag = nullptr;
   Bf16* swiglu_frag = nullptr;
+  // The next norm's operand as its producer leaves it: bf16(h gamma) in
+  // fragment order [32][hidden] and the rows' sums of h^2 per 16 columns
+  // [32][hidden / 16].
+  Bf16* norm_frag = nullptr;
+  float* norm_squares = nullptr;
 
   // The persistent evaluation (one launch per evaluation): its write-once
   // workspace and barrier counters.
@@ -154,7 +159,8 @@ struct vx_dit {
           static_cast<void*>(middle), static_cast<void*>(delta),
           static_cast<void*>(bf16), static_cast<void*>(time_bf16),
           static_cast<void*>(h_frag), static_cast<void*>(attention_frag),
-          static_cast<void*>(swiglu_frag), static_cast<void*>(workspace.h),
+          static_cast<void*>(swiglu_frag), static_cast<void*>(norm_frag),
+          static_cast<void*>(norm_squares), static_cast<void*>(workspace.h),
           static_cast<void*>(workspace.qkv),
           static_cast<void*>(workspace.attention),
           static_cast<void*>(workspace.swiglu),
@@ -276,18 +282,29 @@ struct vx_dit {
                                       workspace, mu, time, cond, x, velocity_out,
                                       x_update, cfg, dt, zero_star, trace, stream);
     }
+    // Each residual update also leaves the next RMSNorm's operand
+    // bf16(h gamma) and the rows' sums of squares, which the qkv and
+    // gate_up products read in place of the float32 stream, applying the
+    // rows' rsqrt(mean + eps) to their outputs.
+    const auto operand = [&](const Bf16* gamma) {
+      return vx::fused::NormOperand{norm_frag, gamma, norm_squares};
+    };
     vx::fused::InAssemble(x, weights.in_proj.weight, weights.in_proj.bias, mu,
-                          time, cond, h_frag, fs, stream);
-    for (const vx_dit_layer& layer : layers) {
-      vx::fused::Qkv(h_frag, layer.input_norm, layer.qkv, qkv, fs, stream);
+                          time, cond, h_frag, fs, stream,
+                          layers.empty() ? vx::fused::NormOperand{}
+                                         : operand(layers[0].input_norm));
+    for (std::size_t l = 0; l < layers.size(); ++l) {
+      const vx_dit_layer& layer = layers[l];
+      vx::fused::QkvScaled(operand(nullptr), layer.qkv, qkv, fs, stream);
       vx::fused::Attention(qkv, weights.rope, attention_frag, fs, stream);
       vx::fused::Residual(attention_frag, layer.o,
                           static_cast<int>(q_width), fs.hidden, h_frag, fs,
-                          stream);
-      vx::fused::GateUp(h_frag, layer.post_norm, layer.gate_up, swiglu_frag,
-                        fs, stream);
+                          stream, operand(layer.post_norm));
+      vx::fused::GateUpScaled(operand(nullptr), layer.gate_up, swiglu_frag, fs, stream);
       vx::fused::Residual(swiglu_frag, layer.down, fs.ffn, fs.hidden, h_frag,
-                          fs, stream);
+                          fs, stream,
+                          l + 1 < layers.size() ? operand(layers[l + 1].input_norm)
+                                                : vx::fused::NormOperand{});
     }
     vx::fused::OutEuler(h_frag, weights.norm, weights.out_proj.weight,
                         weights.out_proj.bias, velocity_out, x_update, cfg, dt,
@@ -455,12 +472,19 @@ int Create(vx_dit* dit) {
     VX_TRY(Allocate(&dit->h_frag, h_count));
     VX_TRY(Allocate(&dit->attention_frag, a_count));
     VX_TRY(Allocate(&dit->swiglu_frag, s_count));
+    const std::size_t squares_count = vx::q8::kFragRows * (s.hidden / 16);
+    VX_TRY(Allocate(&dit->norm_frag, h_count));
+    VX_TRY(Allocate(&dit->norm_squares, squares_count));
     // Rows past the pair stay zero (never written, never read).
     VX_HIP(hipMemset(dit->h_frag, 0, h_count * sizeof(float)),
            "vx_dit_create: hipMemset");
     VX_HIP(hipMemset(dit->attention_frag, 0, a_count * sizeof(Bf16)),
            "vx_dit_create: hipMemset");
     VX_HIP(hipMemset(dit->swiglu_frag, 0, s_count * sizeof(Bf16)),
+           "vx_dit_create: hipMemset");
+    VX_HIP(hipMemset(dit->norm_frag, 0, h_count * sizeof(Bf16)),
+           "vx_dit_create: hipMemset");
+    VX_HIP(hipMemset(dit->norm_squares, 0, squares_count * sizeof(float)),
            "vx_dit_create: hipMemset");
 
     dit->grid = vx::persistent::GridSize();

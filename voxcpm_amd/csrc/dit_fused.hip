@@ -45,6 +45,12 @@ struct InArgs {
   const float* time;       // [hidden]
   const float* cond;       // [patch][hidden]
   float* h;                // fragment order [32][hidden]
+  // With norm_out non-null also the first layer's norm operand
+  // bf16(h * norm_gamma) (bf16 fragment order) and each row's sum of h^2
+  // over the wave's 16 columns, norm_squares[row][column / 16].
+  Bf16* norm_out;
+  const Bf16* norm_gamma;
+  float* norm_squares;
   int patch, feat, hidden, length;
 };
 
@@ -106,28 +112,50 @@ __global__ __launch_bounds__(kWave) void InAssembleKernel(InArgs a) {
   }
   const int column = 16 * group + r16;
   const float bias = a.bias != nullptr ? Bf16Value(a.bias[column]) : 0.0F;
+  const int groups = a.hidden / 16;
+  // The norm operand and the row's sum over the wave's 16 columns: the 16
+  // lanes of a DPP row hold one row's 16 columns (uniform control flow;
+  // dead lanes add zeros and write nothing).
+  const auto emit_norm = [&](bool live, int row, int c, float value) {
+    if (a.norm_out == nullptr)
+      return;
+    const float square = RowSum16(live ? value * value : 0.0F);
+    if (live) {
+      a.norm_out[BfFragIndex(row, c)] = q8::Bf16Fast(value * Bf16Value(a.norm_gamma[c]));
+      if (c % 16 == 0)
+        a.norm_squares[row * groups + c / 16] = square;
+    }
+  };
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const int row = 4 * octet + i;
-    if (row >= a.patch)
-      continue;
+    const bool live = row < a.patch;
     const float value = acc[i] + bias;
-    a.h[F32FragIndex(3 + a.patch + row, column)] = value;
-    a.h[F32FragIndex(a.length + 3 + a.patch + row, column)] = value;
+    if (live) {
+      a.h[F32FragIndex(3 + a.patch + row, column)] = value;
+      a.h[F32FragIndex(a.length + 3 + a.patch + row, column)] = value;
+    }
+    emit_norm(live, 3 + a.patch + row, column, value);
+    emit_norm(live, a.length + 3 + a.patch + row, column, value);
   }
   const int fixed = 3 + a.patch;  // mu, mu, time, condition rows
-  for (int e = lane; e < 2 * fixed * 16; e += kWave) {
+  for (int first = 0; first < 2 * fixed * 16; first += kWave) {
+    const int e = first + lane;
+    const bool live = e < 2 * fixed * 16;
     const int branch = e / (fixed * 16);
     const int row = (e / 16) % fixed;
     const int c = 16 * group + e % 16;
-    float value;
-    if (row < 2)
-      value = branch == 0 ? a.mu[static_cast<std::size_t>(row) * a.hidden + c] : 0.0F;
-    else if (row == 2)
-      value = a.time[c];
-    else
-      value = a.cond[static_cast<std::size_t>(row - 3) * a.hidden + c];
-    a.h[F32FragIndex(branch * a.length + row, c)] = value;
+    float value = 0.0F;
+    if (live) {
+      if (row < 2)
+        value = branch == 0 ? a.mu[static_cast<std::size_t>(row) * a.hidden + c] : 0.0F;
+      else if (row == 2)
+        value = a.time[c];
+      else
+        value = a.cond[static_cast<std::size_t>(row - 3) * a.hidden + c];
+      a.h[F32FragIndex(branch * a.length + row, c)] = value;
+    }
+    emit_norm(live, branch * a.length + row, c, value);
   }
 }
 
@@ -546,7 +574,7 @@ bool StackSupported(const Shape& s) {
 
 void InAssemble(const float* x, const void* in_weight, const Bf16* in_bias,
                 const float* mu, const float* time, const float* cond_rows,
-                float* h, const Shape& s, hipStream_t stream) {
+                float* h, const Shape& s, hipStream_t stream, const NormOperand& next) {
   InArgs a{};
   a.x = x;
   a.w = static_cast<const std::uint8_t*>(in_weight);
@@ -555,6 +583,9 @@ void InAssemble(const float* x, const void* in_weight, const Bf16* in_bias,
   a.time = time;
   a.cond = cond_rows;
   a.h = h;
+  a.norm_out = next.x;
+  a.norm_gamma = next.gamma;
+  a.norm_squares = next.squares;
   a.patch = s.patch;
   a.feat = s.feat;
   a.hidden = s.hidden;
@@ -581,6 +612,23 @@ void Qkv(const float* h, const Bf16* norm, const void* weight, float* qkv,
         args, args.groups, kMaxWaves, s.weights, stream);
 }
 
+void QkvScaled(const NormOperand& x, const void* weight, float* qkv, const Shape& s,
+               hipStream_t stream) {
+  const int n = (s.heads + 2 * s.kv_heads) * s.head_dim;
+  q8::TileArgs args = BaseArgs(weight, s.rows, s.hidden, n);
+  args.x = x.x;
+  args.row_squares = x.squares;
+  args.squares_groups = s.hidden / 16;
+  args.eps = s.eps;
+  args.y = qkv;
+  if (args.pairs <= kMaxWaves)
+    LaunchEngine<q8::ASource::kScaledBf16, q8::Output::kStore, 1, 1>(
+        args, args.groups, kMaxWaves, s.weights, stream);
+  else
+    LaunchEngine<q8::ASource::kScaledBf16, q8::Output::kStore, 1, 2>(
+        args, args.groups, kMaxWaves, s.weights, stream);
+}
+
 void Attention(const float* qkv, const float* rope, Bf16* out, const Shape& s,
                hipStream_t stream) {
   AttentionArgs a{};
@@ -601,10 +649,13 @@ void Attention(const float* qkv, const float* rope, Bf16* out, const Shape& s,
 }
 
 void Residual(const Bf16* act, const void* weight, int k, int n, float* h,
-              const Shape& s, hipStream_t stream) {
+              const Shape& s, hipStream_t stream, const NormOperand& next) {
   q8::TileArgs args = BaseArgs(weight, s.rows, k, n);
   args.x = act;
   args.residual = h;
+  args.norm_out = next.x;
+  args.norm_gamma = next.gamma;
+  args.norm_squares = next.squares;
   // o and down have few output groups (hidden / 16): row blocks spread
   // them over the compute units, each loading only its rows' activations.
   // With four or more pairs per wave (down) the operand loads bound the
@@ -636,6 +687,24 @@ void GateUp(const float* h, const Bf16* norm, const void* weight, Bf16* out,
         args, tiles, kMaxWaves, s.weights, stream);
   else
     LaunchEngine<q8::ASource::kNormF32, q8::Output::kSwiGlu, 2, 2>(
+        args, tiles, kMaxWaves, s.weights, stream);
+}
+
+void GateUpScaled(const NormOperand& x, const void* weight, Bf16* out, const Shape& s,
+                  hipStream_t stream) {
+  q8::TileArgs args = BaseArgs(weight, s.rows, s.hidden, 2 * s.ffn);
+  args.x = x.x;
+  args.row_squares = x.squares;
+  args.squares_groups = s.hidden / 16;
+  args.eps = s.eps;
+  args.frag_out = out;
+  args.group_stride = s.ffn / 16;
+  const int tiles = s.ffn / 16;
+  if (args.pairs <= kMaxWaves)
+    LaunchEngine<q8::ASource::kScaledBf16, q8::Output::kSwiGlu, 2, 1>(
+        args, tiles, kMaxWaves, s.weights, stream);
+  else
+    LaunchEngine<q8::ASource::kScaledBf16, q8::Output::kSwiGlu, 2, 2>(
         args, tiles, kMaxWaves, s.weights, stream);
 }
 

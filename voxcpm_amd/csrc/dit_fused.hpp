@@ -41,30 +41,53 @@ bool Supported(const Shape& s);
 /// multiples of 64, hidden <= 2048.
 bool StackSupported(const Shape& s);
 
+/// A norm operand in the form the producing epilogue leaves it: x =
+/// bf16(h * gamma) in bf16 fragment order [32][hidden] and squares[row][g]
+/// = the sum of h^2 over columns 16 g .. 16 g + 15 (float32 [32][hidden /
+/// 16]); the consumer scales its outputs by rsqrt(sum / hidden + eps). With
+/// x null the producer writes no operand.
+struct NormOperand {
+  Bf16* x = nullptr;
+  const Bf16* gamma = nullptr;
+  float* squares = nullptr;
+};
+
 /// Residual stream rows (float32 fragment order [32][hidden]) from in_proj
 /// of x [patch][feat] (bf16 conversion, product, bias) and the assembly of
 /// mu, the time vector and the condition rows (generator.cpp:297-316;
 /// kernels/generator_kernels.hip:320-340).
 void InAssemble(const float* x, const void* in_weight, const Bf16* in_bias,
                 const float* mu, const float* time, const float* cond_rows,
-                float* h, const Shape& s, hipStream_t stream);
+                float* h, const Shape& s, hipStream_t stream,
+                const NormOperand& next = NormOperand{});
 
 /// qkv [rows][(heads + 2 kv_heads) head_dim] = rmsnorm(h) Wqkv^T.
 void Qkv(const float* h, const Bf16* norm, const void* weight, float* qkv,
          const Shape& s, hipStream_t stream);
+
+/// qkv = (bf16(h gamma) Wqkv^T) rsqrt(mean(h^2) + eps) from the norm
+/// operand the producer of h left.
+void QkvScaled(const NormOperand& x, const void* weight, float* qkv, const Shape& s,
+               hipStream_t stream);
 
 /// Rotary embedding and bidirectional attention within each branch from
 /// the qkv rows; output bf16 fragment order [32][heads head_dim].
 void Attention(const float* qkv, const float* rope, Bf16* out, const Shape& s,
                hipStream_t stream);
 
-/// h += a W^T (a bf16 fragment order [32][k]; h float32 fragment order).
+/// h += a W^T (a bf16 fragment order [32][k]; h float32 fragment order);
+/// with next.x non-null also the next norm's operand of the new h.
 void Residual(const Bf16* a, const void* weight, int k, int n, float* h,
-              const Shape& s, hipStream_t stream);
+              const Shape& s, hipStream_t stream, const NormOperand& next = NormOperand{});
 
 /// s = swiglu(rmsnorm(h) Wgate_up^T), bf16 fragment order [32][ffn].
 void GateUp(const float* h, const Bf16* norm, const void* weight, Bf16* out,
             const Shape& s, hipStream_t stream);
+
+/// GateUp from the norm operand the producer of h left (outputs of both
+/// halves scaled by the row's rsqrt(mean(h^2) + eps) before the SwiGLU).
+void GateUpScaled(const NormOperand& x, const void* weight, Bf16* out, const Shape& s,
+                  hipStream_t stream);
 
 /// velocity [2][patch][feat] = out_proj(bf16(rmsnorm(h) of the output rows))
 /// + bias; with `x` non-null also x -= dt (u s + cfg (c - u s))

@@ -22,11 +22,17 @@
 //    is bf16((x * rsqrt(mean + eps)) * gamma), exactly the reference's
 //    normalised bf16 activations;
 //  - kNormRows: the same from a row-major float32 residual stream of up to
-//    16 rows (one tile: the stacks' decode steps and encoder patches).
+//    16 rows (one tile: the stacks' decode steps and encoder patches);
+//  - kScaledBf16: bf16 in fragment order holding bf16(x * gamma) of the
+//    residual stream, written by the epilogue that produced x together with
+//    each row's sums of squares over its 16-column groups; the outputs are
+//    scaled by the row's rsqrt(sum / k + eps): RMSNorm's per-row factor
+//    applied after the product instead of before the rounding to bf16.
 //
 // and leave through one of three epilogues:
 //  - kStore: float32 [m][n] row-major (optionally accumulated) or bf16;
-//  - kResidual: added into the float32 fragment-order residual stream;
+//  - kResidual: added into the float32 fragment-order residual stream
+//    (optionally also the next norm's kScaledBf16 operand and sums);
 //  - kSwiGlu: RG = 2 with the up rows `group_stride` row groups after the
 //    gate rows; bf16(silu(gate) * up) in bf16 fragment order
 //    (kernels/generator_kernels.hip:243-254);
@@ -93,7 +99,13 @@ inline std::size_t FragElements(std::size_t columns) {
   return static_cast<std::size_t>(kFragRows) * ((columns + 63) / 64) * 64;
 }
 
-enum class ASource : int { kRowMajor = 0, kFragBf16 = 1, kNormF32 = 2, kNormRows = 3 };
+enum class ASource : int {
+  kRowMajor = 0,
+  kFragBf16 = 1,
+  kNormF32 = 2,
+  kNormRows = 3,
+  kScaledBf16 = 4
+};
 enum class Output : int { kStore = 0, kResidual = 1, kSwiGlu = 2, kSwiGluRows = 3, kQkvCache = 4 };
 
 struct TileArgs {
@@ -141,6 +153,15 @@ struct TileArgs {
   int kv_heads;
   int head_dim;
   int capacity;
+  // kResidual with norm_out non-null: the next RMSNorm's operand
+  // bf16(x * norm_gamma) in bf16 fragment order [32][n] and each row's sum
+  // of x^2 over the workgroup's 16 columns, norm_squares[row][column / 16].
+  Bf16* norm_out;
+  const Bf16* norm_gamma;
+  float* norm_squares;
+  // kScaledBf16: those sums, [32][squares_groups] (eps above).
+  const float* row_squares;
+  int squares_groups;
 };
 
 /// Row group r of workgroup tile b: consecutive groups (stride 1) or a
@@ -280,7 +301,9 @@ template<int MT, int RG, ASource SRC, Output OUT, int PW = 1, int JR = 2 * MT,
          Weights WK = Weights::kQ8, int NW = 0>
 __device__ __forceinline__ void EngineBody(const TileArgs& a) {
   // One 16-row tile of a fragment-order source per workgroup.
-  constexpr bool kOneTile = MT == 1 && SRC == ASource::kFragBf16;
+  constexpr bool kScaled = SRC == ASource::kScaledBf16;
+  constexpr bool kOneTile = MT == 1 && (SRC == ASource::kFragBf16 || kScaled);
+  static_assert(!kScaled || (MT == 2 && !kOneTile), "scaled rows are the 32 fragment rows");
   constexpr bool kNorm = SRC == ASource::kNormF32 || SRC == ASource::kNormRows;
   constexpr bool kSwish = OUT == Output::kSwiGlu || OUT == Output::kSwiGluRows;
   constexpr bool kRope = OUT == Output::kQkvCache;
@@ -438,7 +461,7 @@ __device__ __forceinline__ void EngineBody(const TileArgs& a) {
                            2U * static_cast<std::uint32_t>((row_base + 16 * t + r16) * a.k +
                                                            64 * pair + 32 * hf + 8 * octet),
                            ok && row_ok[t] && 2 * pair + hf < k_blocks);
-        } else if constexpr (SRC == ASource::kFragBf16) {
+        } else if constexpr (SRC == ASource::kFragBf16 || kScaled) {
           v = BufferLoad16(
               x_buffer,
               16U * static_cast<std::uint32_t>(((pair * 2 + tile_base + t) * 2 + hf) * 64 + lane),
@@ -499,6 +522,28 @@ __device__ __forceinline__ void EngineBody(const TileArgs& a) {
 #pragma unroll
     for (int t = 0; t < MT; ++t)
       acc[r][t] = F32x4{0.0F, 0.0F, 0.0F, 0.0F};
+
+  // kScaledBf16: the rows' sums of squares, loaded with the first operands
+  // (thread t: row t / 32 of each pass of kThreads / 32 rows, groups
+  // t % 32, + 32, + 64, + 96) and added after the products.
+  constexpr int kSquareRows = kThreads / 32;
+  constexpr int kSquarePasses = kScaled ? (32 + kSquareRows - 1) / kSquareRows : 1;
+  float squares[kSquarePasses][4];
+  const auto load_squares = [&]() {
+    const __amdgpu_buffer_rsrc_t buffer = BufferOf(
+        a.row_squares, 4U * 32U * static_cast<std::uint32_t>(a.squares_groups));
+#pragma unroll
+    for (int pass = 0; pass < kSquarePasses; ++pass) {
+      const int row = pass * kSquareRows + static_cast<int>(threadIdx.x) / 32;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int g = static_cast<int>(threadIdx.x) % 32 + 32 * j;
+        squares[pass][j] = __builtin_bit_cast(
+            float, BufferLoad4(buffer, 4U * static_cast<std::uint32_t>(row * a.squares_groups + g),
+                               row < 32 && g < a.squares_groups));
+      }
+    }
+  };
 
   const auto multiply = [&](const PairStage<MT, RG>& s) {
     const F32x4 zero{0.0F, 0.0F, 0.0F, 0.0F};
@@ -775,6 +820,8 @@ __device__ __forceinline__ void EngineBody(const TileArgs& a) {
       load_activations(p * waves + wave, current[p]);
       load_weights(p * waves + wave, current[p]);
     }
+    if constexpr (kScaled)
+      load_squares();
     for (int base = 0; base < a.pairs; base += step) {
       const bool more = base + step < a.pairs;
       if (more) {
@@ -793,6 +840,21 @@ __device__ __forceinline__ void EngineBody(const TileArgs& a) {
 #pragma unroll
       for (int p = 0; p < PW; ++p)
         current[p] = next[p];
+    }
+  }
+
+  // kScaledBf16: each row's RMSNorm factor rsqrt(sum / k + eps), the
+  // groups' sums added per lane and then over the row's 32 lanes in a
+  // fixed order (made visible by the barrier below).
+  __shared__ float row_scale[kScaled ? 32 : 1];
+  if constexpr (kScaled) {
+#pragma unroll
+    for (int pass = 0; pass < kSquarePasses; ++pass) {
+      float total = ((squares[pass][0] + squares[pass][1]) + squares[pass][2]) + squares[pass][3];
+      total = AddXor16(RowSum16(total));
+      const int row = pass * kSquareRows + static_cast<int>(threadIdx.x) / 32;
+      if (threadIdx.x % 32 == 0 && row < 32)
+        row_scale[row] = rsqrtf(total / static_cast<float>(a.k) + a.eps);
     }
   }
 
@@ -821,13 +883,17 @@ __device__ __forceinline__ void EngineBody(const TileArgs& a) {
     return total;
   };
   const int outputs = kSwish || kRope ? MT * 256 : kFragmentFloats;
+  // kResidual with norm_out: each output's new residual value (0 past the
+  // outputs), for the next norm's operand and sums below.
+  float fresh[kOutputsPerThread];
 #pragma unroll
   for (int u = 0; u < kOutputsPerThread; ++u) {
+    fresh[u] = 0.0F;
     const int e = static_cast<int>(threadIdx.x) + u * kThreads;
     int row, column;
     if (e >= outputs || !output_of(e, row, column))
       continue;
-    const float v = total_of(e);
+    const float v = kScaled ? total_of(e) * row_scale[row] : total_of(e);
     if constexpr (OUT == Output::kStore) {
       const std::size_t at = static_cast<std::size_t>(row) * a.n + column;
       if (a.y != nullptr)
@@ -835,9 +901,10 @@ __device__ __forceinline__ void EngineBody(const TileArgs& a) {
       else
         a.y_bf16[at] = Bf16Fast(v);
     } else if constexpr (OUT == Output::kResidual) {
-      a.residual[F32FragIndex(row, column)] = before[u] + v;
+      fresh[u] = before[u] + v;
+      a.residual[F32FragIndex(row, column)] = fresh[u];
     } else if constexpr (OUT == Output::kSwiGlu) {
-      const float up = total_of(e + MT * 256);
+      const float up = kScaled ? total_of(e + MT * 256) * row_scale[row] : total_of(e + MT * 256);
       a.frag_out[BfFragIndex(row, column)] = Bf16Fast(Silu(v) * up);
     } else if constexpr (kRope) {
       // (x_i, x_{i + half}) -> (x_i c - x_{i + half} s, x_{i + half} c + x_i s)
@@ -870,6 +937,27 @@ __device__ __forceinline__ void EngineBody(const TileArgs& a) {
     } else {
       const float up = total_of(e + MT * 256);
       a.y_bf16[static_cast<std::size_t>(row) * (a.n / 2) + column] = Bf16Fast(Silu(v) * up);
+    }
+  }
+  if constexpr (OUT == Output::kResidual) {
+    if (a.norm_out != nullptr) {
+      // The next norm's operand, and each row's sum of squares over the 16
+      // columns of its group: the 16 lanes of a DPP row hold one row's 16
+      // columns, so one row reduction per output slot (uniform control
+      // flow; outputs past the block add zeros and are not written).
+#pragma unroll
+      for (int u = 0; u < kOutputsPerThread; ++u) {
+        const int e = static_cast<int>(threadIdx.x) + u * kThreads;
+        int row = 0, column = 0;
+        const bool live = e < outputs && output_of(e, row, column);
+        const float square = RowSum16(fresh[u] * fresh[u]);
+        if (live) {
+          a.norm_out[BfFragIndex(row, column)] =
+              Bf16Fast(fresh[u] * Bf16Value(a.norm_gamma[column]));
+          if (column % 16 == 0)
+            a.norm_squares[row * (a.n / 16) + column / 16] = square;
+        }
+      }
     }
   }
 }
