@@ -388,6 +388,9 @@ __device__ __forceinline__ void EngineBody(const TileArgs& a) {
   // The values the epilogue adds to (the residual stream, an accumulated
   // y) are loaded now, beside the first weights, instead of after the sums.
   float before[kOutputsPerThread];
+  // kResidual with norm_out: the next norm's gamma of each output's column,
+  // loaded now for the same reason.
+  float next_gamma[kOutputsPerThread];
   // kQkvCache: each output's row position and cache row, loaded now by
   // masked buffer loads (no branch, so nothing waits for them here); the
   // rotary table entries they select are loaded with the activations.
@@ -409,12 +412,15 @@ __device__ __forceinline__ void EngineBody(const TileArgs& a) {
 #pragma unroll
   for (int u = 0; u < kOutputsPerThread; ++u) {
     before[u] = 0.0F;
+    next_gamma[u] = 0.0F;
     const int e = static_cast<int>(threadIdx.x) + u * kThreads;
     int row, column;
     if (e >= RG * MT * 256 || !output_of(e, row, column))
       continue;
     if constexpr (OUT == Output::kResidual) {
       before[u] = a.residual[F32FragIndex(row, column)];
+      if (a.norm_out != nullptr)
+        next_gamma[u] = Bf16Value(a.norm_gamma[column]);
     } else if constexpr (OUT == Output::kStore) {
       if (a.y != nullptr && a.accumulate)
         before[u] = a.y[static_cast<std::size_t>(row) * a.n + column];
@@ -952,8 +958,7 @@ __device__ __forceinline__ void EngineBody(const TileArgs& a) {
         const bool live = e < outputs && output_of(e, row, column);
         const float square = RowSum16(fresh[u] * fresh[u]);
         if (live) {
-          a.norm_out[BfFragIndex(row, column)] =
-              Bf16Fast(fresh[u] * Bf16Value(a.norm_gamma[column]));
+          a.norm_out[BfFragIndex(row, column)] = Bf16Fast(fresh[u] * next_gamma[u]);
           if (column % 16 == 0)
             a.norm_squares[row * (a.n / 16) + column / 16] = square;
         }
