@@ -127,7 +127,7 @@ int Product(const uint16_t* x, const void* packed, float* y, uint16_t* y_bf16,
                         vx::Stream(stream));
   const vx::ProductPlan plan = vx::PlanSkinny(
       m, k, n, scratch != nullptr ? scratch->partial_floats : 0,
-      scratch != nullptr ? scratch->counter_count : 0, rg, waves, splits);
+      scratch != nullptr ? scratch->counter_count : 0, rg, waves, splits, kind);
   return vx::RunSkinny(x, packed, y, y_bf16, m, k, n, accumulate != 0, plan,
                        scratch != nullptr ? scratch->partials : nullptr,
                        scratch != nullptr ? scratch->counters : nullptr,

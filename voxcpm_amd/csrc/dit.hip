@@ -180,7 +180,7 @@ struct vx_dit {
              std::size_t k, std::size_t n, bool accumulate,
              hipStream_t stream) {
     const vx::ProductPlan plan =
-        vx::PlanSkinny(m, k, n, partial_floats, counter_count);
+        vx::PlanSkinny(m, k, n, partial_floats, counter_count, 0, 0, 0, Kind());
     return vx::RunSkinny(x, w, y, nullptr, m, k, n, accumulate, plan,
                          partials, counters, stream, Kind());
   }

@@ -41,12 +41,13 @@ int MaxRowGroups(int mt);
 /// Largest wave count per workgroup of the kernel for (`mt`, `rg`).
 int MaxWaves(int mt, int rg);
 
-/// The plan of an m x k x n product (m <= 128). Positive `rg`, `waves` and
-/// `splits` force those values; the split falls back to 1 when the scratch
-/// cannot hold its partials.
+/// The plan of an m x k x n product (m <= 128) on weights of `kind`.
+/// Positive `rg`, `waves` and `splits` force those values; the split falls
+/// back to 1 when the scratch cannot hold its partials.
 ProductPlan PlanSkinny(std::size_t m, std::size_t k, std::size_t n,
                        std::size_t scratch_floats, std::size_t scratch_counters,
-                       int rg = 0, int waves = 0, int splits = 0);
+                       int rg = 0, int waves = 0, int splits = 0,
+                       q8::Weights kind = q8::Weights::kQ8);
 
 /// Launches the product (m <= 128) with `plan`: Q8_0 panels with the exact
 /// arithmetic, or bf16 weights (panels, or rows [n][k] for m <= 32) on the

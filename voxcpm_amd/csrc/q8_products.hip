@@ -305,11 +305,11 @@ Launcher PickLauncher(int mt, int rg) {
 
 // ---- the one-pass engine on row-major activations ---------------------------
 
-template<int MT, int RG, int PW, int JR, q8::Weights WK>
+template<int MT, int RG, int PW, int JR, q8::Weights WK, int NW = 0>
 void LaunchEngine(const q8::TileArgs& args, int tiles, int waves,
                   hipStream_t stream) {
   const std::size_t shared = q8::EngineShared(MT, RG, waves, q8::ASource::kRowMajor);
-  q8::EngineKernel<MT, RG, q8::ASource::kRowMajor, q8::Output::kStore, PW, JR, WK>
+  q8::EngineKernel<MT, RG, q8::ASource::kRowMajor, q8::Output::kStore, PW, JR, WK, NW>
       <<<tiles, waves * kWave, shared, stream>>>(args);
 }
 
@@ -317,13 +317,13 @@ using EngineLauncher = void (*)(const q8::TileArgs&, int, int, hipStream_t);
 
 /// Up to 32 rows the engine stages the rows through LDS in JR load groups
 /// of 8 rows; more rows load straight into the operands.
-template<int MT, int RG, int PW, q8::Weights WK>
+template<int MT, int RG, int PW, q8::Weights WK, int NW = 0>
 EngineLauncher EngineJr(int m) {
   if constexpr (q8::StagesRows(q8::ASource::kRowMajor, MT)) {
     if (m <= 16 * MT - 8)
-      return LaunchEngine<MT, RG, PW, 2 * MT - 1, WK>;
+      return LaunchEngine<MT, RG, PW, 2 * MT - 1, WK, NW>;
   }
-  return LaunchEngine<MT, RG, PW, 2 * MT, WK>;
+  return LaunchEngine<MT, RG, PW, 2 * MT, WK, NW>;
 }
 
 /// Pairs in flight per wave (`pw`, kMaxPairsInFlight): one 16-row tile
@@ -359,8 +359,23 @@ EngineLauncher EngineRg(int rg, int pw, int m) {
   return nullptr;
 }
 
+/// Eight-wave workgroups of one or two row groups for wide products of
+/// 17-32 rows (PlanEngine's 512-workgroup plans).
 template<q8::Weights WK>
-EngineLauncher PickEngineFor(int mt, int rg, int pw, int m) {
+EngineLauncher EngineEight(int rg, int pw, int m) {
+  if (pw != 1)
+    return nullptr;
+  switch (rg) {
+    case 1: return EngineJr<2, 1, 1, WK, 8>(m);
+    case 2: return EngineJr<2, 2, 1, WK, 8>(m);
+    default: return nullptr;
+  }
+}
+
+template<q8::Weights WK>
+EngineLauncher PickEngineFor(int mt, int rg, int pw, int m, int waves) {
+  if (mt == 2 && waves * kWave != q8::EngineThreads(mt, rg))
+    return waves == 8 ? EngineEight<WK>(rg, pw, m) : nullptr;
   switch (mt) {
     case 1: return EngineRg<1, WK>(rg, pw, m);
     case 2: return EngineRg<2, WK>(rg, pw, m);
@@ -422,11 +437,13 @@ TunedLauncher PickTuned(int rg, int pw, int waves, int m) {
 }
 
 /// bf16 rows [n][k] are read by the staged engine only (m <= 32).
-EngineLauncher PickEngine(int mt, int rg, int pw, int m, q8::Weights kind) {
+EngineLauncher PickEngine(int mt, int rg, int pw, int m, int waves, q8::Weights kind) {
   switch (kind) {
-    case q8::Weights::kQ8: return PickEngineFor<q8::Weights::kQ8>(mt, rg, pw, m);
-    case q8::Weights::kBf16: return PickEngineFor<q8::Weights::kBf16>(mt, rg, pw, m);
+    case q8::Weights::kQ8: return PickEngineFor<q8::Weights::kQ8>(mt, rg, pw, m, waves);
+    case q8::Weights::kBf16: return PickEngineFor<q8::Weights::kBf16>(mt, rg, pw, m, waves);
     case q8::Weights::kBf16Rows:
+      if (mt == 2 && waves * kWave != q8::EngineThreads(mt, rg))
+        return waves == 8 ? EngineEight<q8::Weights::kBf16Rows>(rg, pw, m) : nullptr;
       if (mt == 1)
         return EngineRg<1, q8::Weights::kBf16Rows>(rg, pw, m);
       if (mt == 2)
@@ -442,7 +459,7 @@ constexpr int kMaxPairsInFlight = 4;
 /// share each activation fragment over 2 or 4 row groups (fewer workgroups
 /// read the activations). Waves split the pairs, up to 16 (8 for the larger
 /// register footprints).
-ProductPlan PlanEngine(std::size_t m, std::size_t k, std::size_t n) {
+ProductPlan PlanEngine(std::size_t m, std::size_t k, std::size_t n, q8::Weights kind) {
   ProductPlan plan;
   plan.mt = static_cast<int>((m + 15) / 16);
   if (plan.mt > 4 && (m + 63) / 64 * ((n + 127) / 128) >= 256) {
@@ -476,6 +493,19 @@ ProductPlan PlanEngine(std::size_t m, std::size_t k, std::size_t n) {
   while (plan.tiles % 8 == 0 && plan.row_blocks < 4 && plan.tiles * 2 * plan.row_blocks <= 256 &&
          static_cast<int>(m) >= 10 * plan.row_blocks)
     plan.row_blocks *= 2;
+  if (plan.mt == 2 && groups >= 512 && kind == q8::Weights::kQ8) {
+    // Wide Q8_0 products of 17-32 rows: about 512 workgroups of 8 waves
+    // (two per compute unit), the fewest row groups that keep them at most
+    // 512 (measured on MI355X at M=22: (1024, 8192) 5.49 -> 5.19 us with
+    // one row group instead of two in 16-wave workgroups; (2048, 16384)
+    // the same 11.0-11.1 us with two row groups as with four). bf16
+    // weights keep the 16-wave plans: (1024, 8192) measured 6.3 -> 6.7 us
+    // on panels and 7.5 -> 7.6 us on rows with these.
+    plan.rg = groups <= 512 ? 1 : groups <= 1024 ? 2 : 4;
+    plan.tiles = (groups + plan.rg - 1) / plan.rg;
+    plan.waves = 8;
+    plan.row_blocks = 1;
+  }
   plan.splits = 1;
   plan.pairs_per_split = pairs;
   plan.pairs_per_wave = (pairs + plan.waves - 1) / plan.waves;
@@ -504,9 +534,9 @@ int MaxRowGroups(int mt) {
 ProductPlan PlanSkinny(std::size_t m, std::size_t k, std::size_t n,
                        std::size_t scratch_floats,
                        std::size_t scratch_counters, int rg, int waves,
-                       int splits) {
+                       int splits, q8::Weights kind) {
   if (rg <= 0 && waves <= 0 && splits <= 0)
-    return PlanEngine(m, k, n);
+    return PlanEngine(m, k, n, kind);
   ProductPlan plan;
   plan.mt = static_cast<int>((m + 15) / 16);
   const int groups = static_cast<int>(q8::Groups(n));
@@ -563,7 +593,7 @@ int RunSkinny(const Bf16* x, const void* w, float* y, Bf16* y_bf16,
   }
   if (plan.engine) {
     const EngineLauncher launch =
-        PickEngine(plan.mt, plan.rg, plan.pw, static_cast<int>(m), kind);
+        PickEngine(plan.mt, plan.rg, plan.pw, static_cast<int>(m), plan.waves, kind);
     if (launch == nullptr)
       return Fail(VX_UNSUPPORTED, "no product engine for this plan");
     q8::TileArgs args{};

@@ -743,7 +743,7 @@ struct vx_stack {
                                                          : vx::TiledMode::kBf16,
                           product_partials, product_partial_floats, stream);
     }
-    const vx::ProductPlan plan = vx::PlanSkinny(m, k, n, 0, 0);
+    const vx::ProductPlan plan = vx::PlanSkinny(m, k, n, 0, 0, 0, 0, 0, Kind());
     return vx::RunSkinny(x, w, y, nullptr, m, k, n, accumulate, plan, nullptr, nullptr,
                          stream, Kind());
   }
