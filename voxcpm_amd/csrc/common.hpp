@@ -96,6 +96,7 @@ constexpr int kDppXor1 = 0xB1;         // quad_perm [1, 0, 3, 2]
 constexpr int kDppXor2 = 0x4E;         // quad_perm [2, 3, 0, 1]
 constexpr int kDppHalfMirror = 0x141;  // lane i of 8 <- lane 7 - i
 constexpr int kDppMirror = 0x140;      // lane i of 16 <- lane 15 - i
+constexpr int kDppRotate8 = 0x128;     // lane i of 16 <- lane (i + 8) % 16
 
 /// Sum over each row of 16 lanes by pairs at xor 1 and 2, then the
 /// mirrored halves of 8 and of 16 lanes; every lane of the row receives the

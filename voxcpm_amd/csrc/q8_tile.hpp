@@ -37,10 +37,12 @@
 //    gate rows; bf16(silu(gate) * up) in bf16 fragment order
 //    (kernels/generator_kernels.hip:243-254);
 //  - kSwiGluRows: the same into bf16 [m][n / 2] row-major (y_bf16);
-//  - kQkvCache: RG = 2 with each rotary dimension's partner (head_dim / 2
-//    columns on) `group_stride` row groups after it; the rotary embedding
-//    at each row's position, then q [m][heads][head_dim] and the row's key
-//    and value cache rows (kernels/generator_kernels.hip:110-158).
+//  - kQkvCache: RG = 1, workgroup 2 p + h taking rows 8 h .. 8 h + 7 of
+//    group pair p's two row groups (each rotary dimension's partner,
+//    head_dim / 2 columns on, is `group_stride` row groups after it); the
+//    rotary embedding at each row's position, then q [m][heads][head_dim]
+//    and the row's key and value cache rows
+//    (kernels/generator_kernels.hip:110-158).
 #ifndef VOXCPM_AMD_Q8_TILE_HPP_
 #define VOXCPM_AMD_Q8_TILE_HPP_
 
@@ -312,8 +314,14 @@ __device__ __forceinline__ void EngineBody(const TileArgs& a) {
   static_assert(OUT == Output::kStore || OUT == Output::kSwiGluRows ||
                     OUT == Output::kQkvCache || MT == 2 || kOneTile,
                 "fragment outputs are 32 rows or one tile of them");
+  // kQkvCache: each workgroup takes the same 8 rows of a rotary
+  // dimension's two row groups (lanes r16 < 8 the first group's, r16 >= 8
+  // the second's), so that twice as many workgroups as pairs share the
+  // weights; each output's partner is 8 lanes away.
+  constexpr bool kHalfPairs = kRope;
   static_assert(!kSwish || RG == 2, "SwiGLU pairs two groups");
-  static_assert(!kRope || RG == 2, "the rotary embedding pairs two groups");
+  static_assert(!kRope || RG == 1, "the rotary embedding takes half pairs");
+  static_assert(!kHalfPairs || WK != Weights::kBf16Rows, "half pairs read panels");
   extern __shared__ float lds[];
   const int lane = threadIdx.x % kWave;
   const int wave = threadIdx.x / kWave;
@@ -346,11 +354,22 @@ __device__ __forceinline__ void EngineBody(const TileArgs& a) {
   const int k_blocks = a.k / 32;
 
   constexpr int kUnit = WK == Weights::kQ8 ? kUnitBytes : kBf16UnitBytes;
+  // kHalfPairs: workgroup tile is half tile % 2 (rows 8 half .. + 7) of
+  // the group pair tile / 2; the lane reads its row of its group's panel
+  // (panel lane 16 octet + row holds the row's k chunk octet).
+  const int half_of_pair = kHalfPairs ? tile % 2 : 0;
+  const int pair_tile = kHalfPairs ? tile / 2 : tile;
+  const int panel_row = kHalfPairs ? 8 * half_of_pair + r16 % 8 : r16;
+  const int panel_lane = 16 * octet + panel_row;
+  const auto group_of = [&](int r, int column_lane) {
+    return kHalfPairs ? RgGroup(pair_tile, column_lane >= 8 ? 1 : 0, a.group_stride, 2)
+                      : RgGroup(tile, r, a.group_stride, RG);
+  };
   const std::uint8_t* unit[RG];
   int first_row[RG];  // bf16 rows: the group's first weight row
 #pragma unroll
   for (int r = 0; r < RG; ++r) {
-    const int g = min(RgGroup(tile, r, a.group_stride, RG), a.groups - 1);
+    const int g = min(group_of(r, r16), a.groups - 1);
     unit[r] = a.w + static_cast<std::size_t>(g) * a.pairs * kUnit;
     first_row[r] = 16 * g;
   }
@@ -381,8 +400,8 @@ __device__ __forceinline__ void EngineBody(const TileArgs& a) {
     const int r = f / MT;
     const int t = f % MT;
     row = row_base + 16 * t + 4 * (l / 16) + i;
-    const int group = RgGroup(tile, r, a.group_stride, RG);
-    column = 16 * group + l % 16;
+    const int group = group_of(r, l % 16);
+    column = kHalfPairs ? 16 * group + 8 * half_of_pair + l % 8 : 16 * group + l % 16;
     return in_rows(row) && group < a.groups && column < a.n;
   };
   // The values the epilogue adds to (the residual stream, an accumulated
@@ -447,11 +466,11 @@ __device__ __forceinline__ void EngineBody(const TileArgs& a) {
         s.w2[r] = BufferLoad16(row_buffer, at + 64U, ok && row < a.n && column + 32 < a.k);
       } else {
         const std::uint8_t* u = unit[r] + static_cast<std::size_t>(ok ? pair : 0) * kUnit;
-        s.w[r] = *reinterpret_cast<const uint4*>(u + 16 * lane);
+        s.w[r] = *reinterpret_cast<const uint4*>(u + 16 * panel_lane);
         if constexpr (WK == Weights::kQ8)
-          s.scales[r] = *reinterpret_cast<const std::uint32_t*>(u + kValueBytes + 4 * r16);
+          s.scales[r] = *reinterpret_cast<const std::uint32_t*>(u + kValueBytes + 4 * panel_row);
         else
-          s.w2[r] = *reinterpret_cast<const uint4*>(u + kBf16HalfBytes + 16 * lane);
+          s.w2[r] = *reinterpret_cast<const uint4*>(u + kBf16HalfBytes + 16 * panel_lane);
       }
     }
   };
@@ -583,10 +602,9 @@ __device__ __forceinline__ void EngineBody(const TileArgs& a) {
     }
   };
 
-  // kQkvCache: the cos / sin of each output's rotary dimension (the first
-  // group's column within its head). Their loads depend on the positions
-  // loaded at the start, so they are issued after the first activation
-  // loads, whose wait they share.
+  // kQkvCache: the cos / sin of each output's rotary dimension. Their
+  // loads depend on the positions loaded at the start, so they are issued
+  // after the first activation loads, whose wait they share.
   constexpr int kPairedOutputs = MT * 256;
   float rope_cos[kOutputsPerThread];
   float rope_sin[kOutputsPerThread];
@@ -602,8 +620,9 @@ __device__ __forceinline__ void EngineBody(const TileArgs& a) {
         // The position is used here, not hoisted ahead of the first loads.
         std::uint32_t at = position[u];
         asm volatile("" : "+v"(at));
-        const float* table =
-            a.rope + static_cast<std::size_t>(at) * a.head_dim + column % a.head_dim;
+        // The rotary dimension: the column's index within its half-head.
+        const float* table = a.rope + static_cast<std::size_t>(at) * a.head_dim +
+                             (column % a.head_dim) % (a.head_dim / 2);
         rope_cos[u] = table[0];
         rope_sin[u] = table[a.head_dim / 2];
       }
@@ -896,10 +915,18 @@ __device__ __forceinline__ void EngineBody(const TileArgs& a) {
   for (int u = 0; u < kOutputsPerThread; ++u) {
     fresh[u] = 0.0F;
     const int e = static_cast<int>(threadIdx.x) + u * kThreads;
+    // kHalfPairs: every lane of a wave with outputs takes part in the
+    // exchange with its partner 8 lanes away (outputs are whole waves).
+    float mine = 0.0F;
+    float partner_value = 0.0F;
+    if constexpr (kHalfPairs) {
+      mine = e < outputs ? total_of(e) : 0.0F;
+      partner_value = RowDpp<kDppRotate8>(mine);
+    }
     int row, column;
     if (e >= outputs || !output_of(e, row, column))
       continue;
-    const float v = kScaled ? total_of(e) * row_scale[row] : total_of(e);
+    const float v = kHalfPairs ? mine : kScaled ? total_of(e) * row_scale[row] : total_of(e);
     if constexpr (OUT == Output::kStore) {
       const std::size_t at = static_cast<std::size_t>(row) * a.n + column;
       if (a.y != nullptr)
@@ -914,18 +941,15 @@ __device__ __forceinline__ void EngineBody(const TileArgs& a) {
       a.frag_out[BfFragIndex(row, column)] = Bf16Fast(Silu(v) * up);
     } else if constexpr (kRope) {
       // (x_i, x_{i + half}) -> (x_i c - x_{i + half} s, x_{i + half} c + x_i s)
-      // on q and k; v is stored as it is.
-      const float partner = total_of(e + MT * 256);
+      // on q and k; v is stored as it is. Lanes r16 < 8 hold x_i and
+      // lanes r16 >= 8 x_{i + half}; each received its partner's value.
       const int head = column / a.head_dim;
-      const int i = column % a.head_dim;
-      const int half = a.head_dim / 2;
-      float first = v;
-      float second = partner;
+      const bool second_half = e % 16 >= 8;
+      float out = v;
       if (a.rope != nullptr && head < a.heads + a.kv_heads) {
         const float c = rope_cos[u];
         const float sn = rope_sin[u];
-        first = v * c - partner * sn;
-        second = partner * c + v * sn;
+        out = second_half ? v * c + partner_value * sn : v * c - partner_value * sn;
       }
       float* target;
       if (head < a.heads)
@@ -938,8 +962,7 @@ __device__ __forceinline__ void EngineBody(const TileArgs& a) {
         target = a.v_cache + (static_cast<std::size_t>(head - a.heads - a.kv_heads) * a.capacity +
                               static_cast<std::size_t>(cache_row[u])) *
                                  a.head_dim;
-      target[i] = first;
-      target[half + i] = second;
+      target[column % a.head_dim] = out;
     } else {
       const float up = total_of(e + MT * 256);
       a.y_bf16[static_cast<std::size_t>(row) * (a.n / 2) + column] = Bf16Fast(Silu(v) * up);

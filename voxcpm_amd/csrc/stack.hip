@@ -560,8 +560,11 @@ void NormQkvRows(const float* h, const Bf16* gamma, float eps, const void* weigh
 }
 
 /// rmsnorm(h) Wqkv^T with the rotary embedding and the cache writes in the
-/// epilogue (QkvRope's work): each workgroup owns a rotary dimension's two
-/// row groups, head_dim / 2 columns apart. head_dim a multiple of 32.
+/// epilogue (QkvRope's work): each workgroup owns 8 rows of a rotary
+/// dimension's two row groups, head_dim / 2 columns apart (the halves of
+/// a pair in two workgroups: twice the workgroups of one pair each, which
+/// left most compute units idle: base LM step 1004 -> 980 us at 1024
+/// cached positions on MI355X). head_dim a multiple of 32.
 void NormQkvCacheRows(const float* h, const Bf16* gamma, float eps, const void* weight,
                       const float* rope, const std::int32_t* positions,
                       const std::int32_t* cache_rows, float* q, float* k_cache, float* v_cache,
@@ -583,12 +586,12 @@ void NormQkvCacheRows(const float* h, const Bf16* gamma, float eps, const void* 
   args.kv_heads = kv_heads;
   args.head_dim = head_dim;
   args.capacity = capacity;
-  const int tiles = args.groups / 2;
+  const int tiles = args.groups;  // half pairs
   if (args.pairs <= 16)
-    LaunchRowEngine<q8::ASource::kNormRows, q8::Output::kQkvCache, 2, 1>(args, tiles, kind,
+    LaunchRowEngine<q8::ASource::kNormRows, q8::Output::kQkvCache, 1, 1>(args, tiles, kind,
                                                                          stream);
   else
-    LaunchRowEngine<q8::ASource::kNormRows, q8::Output::kQkvCache, 2, 2>(args, tiles, kind,
+    LaunchRowEngine<q8::ASource::kNormRows, q8::Output::kQkvCache, 1, 2>(args, tiles, kind,
                                                                          stream);
 }
 
@@ -600,6 +603,10 @@ void NormGateUpRows(const float* h, const Bf16* gamma, float eps, const void* we
   args.eps = eps;
   args.y_bf16 = act;
   args.group_stride = ffn / 16;
+  // Whole pairs (gate and up groups in one workgroup): half pairs measured
+  // slower here, in 16-wave workgroups (base LM step +16 us: three
+  // workgroups per compute unit take two rounds) and in 8-wave ones (the
+  // same step time, the 5-row encoder 279 -> 286 us).
   const int tiles = ffn / 16;
   if (args.pairs <= 16)
     LaunchRowEngine<q8::ASource::kNormRows, q8::Output::kSwiGluRows, 2, 1>(args, tiles, kind,
