@@ -604,9 +604,11 @@ void NormGateUpRows(const float* h, const Bf16* gamma, float eps, const void* we
   args.y_bf16 = act;
   args.group_stride = ffn / 16;
   // Whole pairs (gate and up groups in one workgroup): half pairs measured
-  // slower here, in 16-wave workgroups (base LM step +16 us: three
-  // workgroups per compute unit take two rounds) and in 8-wave ones (the
-  // same step time, the 5-row encoder 279 -> 286 us).
+  // slower here, one per 16-wave workgroup (base LM step +16 us: three
+  // workgroups per compute unit take two rounds), one per 8-wave workgroup
+  // (the same step time, the 5-row encoder 279 -> 286 us) and three per
+  // 16-wave workgroup (256 workgroups, each a third of the weights of
+  // three pair halves: +9 us).
   const int tiles = ffn / 16;
   if (args.pairs <= 16)
     LaunchRowEngine<q8::ASource::kNormRows, q8::Output::kSwiGluRows, 2, 1>(args, tiles, kind,
