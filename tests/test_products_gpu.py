@@ -264,6 +264,31 @@ def test_sweep_shapes_baseline_law(vx, oracle, cuda, stream, k, n, rows):
                            np.ascontiguousarray(blocks[cols])) <= LIMIT
 
 
+@pytest.mark.parametrize("k,n", [(1024, 8192), (2048, 16384), (1024, 16400)])
+@pytest.mark.parametrize("rows", [17, 22, 32])
+def test_wide_plans_accumulate(vx, oracle, cuda, stream, k, n, rows):
+    """17-32 rows over 512 or more row groups take the eight-wave plans (one
+    or two row groups per workgroup, two pairs in flight with two; four
+    row groups past 1024, here with a partial last tile): y += x W^T and
+    the plain store both within the bound, checked on every 7th column
+    (all lanes and row groups are visited)."""
+    rng = synth.Rng(31, 100 * rows + n + k)
+    blocks = reference_weights(rng, n, k)
+    packed = vx.q8_pack(to_device(blocks, cuda), n, k)
+    plan = vx.q8_plan(rows, k, n)
+    assert plan["waves"] == 8, plan
+    x = reference_activations(rng, rows, k)
+    x_dev = to_device(x, cuda)
+    before = rng.normal(rows * n).astype(np.float32).reshape(rows, n)
+    cols = np.arange(0, n, 7)
+    for accumulate in (False, True):
+        y = run_product(vx, x_dev, packed, n, before if accumulate else None, None, None, cuda)
+        worst = oracle.q8_check(np.ascontiguousarray(y[:, cols]), x,
+                                np.ascontiguousarray(blocks[cols]),
+                                np.ascontiguousarray(before[:, cols]) if accumulate else None)
+        assert worst <= LIMIT, (rows, k, n, accumulate, worst)
+
+
 def expanded_check(y, x, blocks, oracle, before=None):
     """Error of y against the reference's expansion (gemm.cpp:305-312):
     x . bf16(scale q) in double, relative to sum |x w|."""
