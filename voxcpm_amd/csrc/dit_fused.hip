@@ -662,10 +662,16 @@ void Residual(const Bf16* act, const void* weight, int k, int n, float* h,
   // workgroup: its blocks then lie within one 16-row tile, which halves
   // them (5.9 -> 4.9 us for k = 4096 on MI355X; o, k = 1024, measured
   // 3.35 us with 32-row blocks against 3.50 us).
-  if (args.pairs > 2 * kMaxWaves) {  // two pairs per wave per pass
+  if (args.pairs > 2 * kMaxWaves) {
+    // Q8_0: four pairs per wave per pass (k = 4096 in one pass: 2598 ->
+    // 2588 us per patch); bf16 panels two (four spill 36 registers).
     SetTileBlocks(args, args.groups, s.rows);
-    LaunchEngine<q8::ASource::kFragBf16, q8::Output::kResidual, 1, 2, 1>(
-        args, args.groups * args.row_blocks, kMaxWaves, s.weights, stream);
+    if (s.weights == q8::Weights::kQ8)
+      LaunchEngine<q8::ASource::kFragBf16, q8::Output::kResidual, 1, 4, 1>(
+          args, args.groups * args.row_blocks, kMaxWaves, s.weights, stream);
+    else
+      LaunchEngine<q8::ASource::kFragBf16, q8::Output::kResidual, 1, 2, 1>(
+          args, args.groups * args.row_blocks, kMaxWaves, s.weights, stream);
   } else {
     SetRowBlocks(args, args.groups, s.rows);
     LaunchEngine<q8::ASource::kFragBf16, q8::Output::kResidual, 1, 1>(
