@@ -622,6 +622,17 @@ def gpu_patch(args, torch, ops, synth, device, stream):
     stop.record(stream)
     stop.synchronize()
     unfused_us = start.elapsed_time(stop) * 1e3 / patches
+    # The fused kernels in the reference's norm rounding order.
+    dit.set_path(_lib.DIT_PATH_FUSED_REFERENCE_ORDER)
+    for _ in range(2):
+        dit.patch(mu, cond, x, t, dt, evaluate, config.cfg, config.zero_star)
+    torch.cuda.synchronize()
+    start.record(stream)
+    for _ in range(patches):
+        dit.patch(mu, cond, x, t, dt, evaluate, config.cfg, config.zero_star)
+    stop.record(stream)
+    stop.synchronize()
+    reference_order_us = start.elapsed_time(stop) * 1e3 / patches
     dit.set_path(_lib.DIT_PATH_AUTO)
     dit.close()
     # The same DiT on bf16 weights (bf16(scale q) panels, twice the bytes).
@@ -648,11 +659,13 @@ def gpu_patch(args, torch, ops, synth, device, stream):
     log(f"patch: {warm_us:.1f} us warm, {cold_us:.1f} us cold "
         f"({patch_bytes / 1e6:.1f} MB of weights per patch); "
         f"persistent evaluation {persistent_us:.1f} us; per-kernel {unfused_us:.1f} us; "
+        f"fused in the reference's norm order {reference_order_us:.1f} us; "
         f"bf16 weights {bf16_us:.1f} us warm")
     gpu_patch.weights = weights
     return {"us_warm": round(warm_us, 2), "us_cold": round(cold_us, 2),
             "us_warm_persistent": round(persistent_us, 2),
             "us_warm_per_kernel": round(unfused_us, 2),
+            "us_warm_fused_reference_order": round(reference_order_us, 2),
             "us_warm_bf16_weights": round(bf16_us, 2),
             "patches_timed": patches, "evaluations": evaluations,
             "bytes": patch_bytes,

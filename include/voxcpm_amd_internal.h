@@ -85,6 +85,11 @@ int vx_stream_read(const void* data, size_t bytes, uint32_t never,
 #define VX_DIT_PATH_PERSISTENT 1
 #define VX_DIT_PATH_FUSED 2
 #define VX_DIT_PATH_UNFUSED 3
+/* The fused kernels with each RMSNorm applied before its product's bf16
+ * rounding (the reference's order: bf16((x * r) * gamma)); VX_DIT_PATH_FUSED
+ * has the residual updates write bf16(x * gamma) and scales the products'
+ * outputs by r instead, which is faster and within the same tolerance. */
+#define VX_DIT_PATH_FUSED_REFERENCE_ORDER 4
 
 /* Selects the evaluation path of later calls (VX_UNSUPPORTED when the
  * shape has no such path). No reference counterpart: the reference has one

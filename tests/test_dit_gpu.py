@@ -282,8 +282,10 @@ def test_dit_velocity(vx, oracle, cuda, stream, config):
 ], ids=["synthetic-block", "voxcpm2-2layers"])
 def test_dit_paths_agree(vx, oracle, cuda, stream, config):
     """The persistent evaluation (one launch, grid barriers), the fused
-    kernels (four or five launches per layer) and the per-kernel path each match the
-    oracle; the fused path is the default for these shapes."""
+    kernels (five launches per layer, with the norms' row factors after the
+    products or, in the reference's order, before them) and the per-kernel
+    path each match the oracle; the fused path is the default for these
+    shapes."""
     from voxcpm_amd import _lib
     weights, dit, odit = make_dit(config, 38, vx, oracle, cuda)
     assert dit.path == _lib.DIT_PATH_FUSED
@@ -291,7 +293,8 @@ def test_dit_paths_agree(vx, oracle, cuda, stream, config):
     mu, cond, x = (dev(a, cuda) for a in (inputs.mu, inputs.cond_latent, inputs.noise))
     ref = odit.velocity(inputs.mu, inputs.cond_latent, inputs.noise, 0.63)
     results = {}
-    for path in (_lib.DIT_PATH_PERSISTENT, _lib.DIT_PATH_FUSED, _lib.DIT_PATH_UNFUSED):
+    for path in (_lib.DIT_PATH_PERSISTENT, _lib.DIT_PATH_FUSED, _lib.DIT_PATH_UNFUSED,
+                 _lib.DIT_PATH_FUSED_REFERENCE_ORDER):
         dit.set_path(path)
         assert dit.path == path
         got = dit.velocity(mu, cond, x, 0.63).cpu().numpy()
@@ -304,6 +307,11 @@ def test_dit_paths_agree(vx, oracle, cuda, stream, config):
     # four k splits, attention's dot products); each is ~2e-3 from the
     # oracle, so they stay within twice that of each other.
     assert rel_max(results[_lib.DIT_PATH_PERSISTENT], results[_lib.DIT_PATH_FUSED]) < 5e-3
+    # The paths that round the normalised activations as the reference does
+    # (persistent, per-kernel, fused in the reference's order) differ from
+    # each other only in float32 summation orders.
+    for path in (_lib.DIT_PATH_PERSISTENT, _lib.DIT_PATH_FUSED_REFERENCE_ORDER):
+        assert rel_max(results[path], results[_lib.DIT_PATH_UNFUSED]) < 2e-3, path
 
 
 def test_persistent_repeated_launches(vx, oracle, cuda, stream):

@@ -20,6 +20,7 @@ DIT_PATH_AUTO = 0
 DIT_PATH_PERSISTENT = 1
 DIT_PATH_FUSED = 2
 DIT_PATH_UNFUSED = 3
+DIT_PATH_FUSED_REFERENCE_ORDER = 4
 
 c_size = ctypes.c_size_t
 c_int = ctypes.c_int

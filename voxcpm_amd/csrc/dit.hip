@@ -249,7 +249,8 @@ struct vx_dit {
   }
 
   /// The evaluation path that runs: VX_DIT_PATH_PERSISTENT,
-  /// VX_DIT_PATH_FUSED or VX_DIT_PATH_UNFUSED.
+  /// VX_DIT_PATH_FUSED, VX_DIT_PATH_FUSED_REFERENCE_ORDER or
+  /// VX_DIT_PATH_UNFUSED.
   int Resolved() const {
     if (path == VX_DIT_PATH_AUTO)
       return fused ? VX_DIT_PATH_FUSED : VX_DIT_PATH_UNFUSED;
@@ -281,6 +282,24 @@ struct vx_dit {
       return vx::persistent::Evaluate(fs, static_cast<int>(shape.layers), grid, w,
                                       workspace, mu, time, cond, x, velocity_out,
                                       x_update, cfg, dt, zero_star, trace, stream);
+    }
+    if (Resolved() == VX_DIT_PATH_FUSED_REFERENCE_ORDER) {
+      // The norm products normalise the float32 stream in their prologue
+      // (bf16((h r) gamma), the reference's rounding).
+      vx::fused::InAssemble(x, weights.in_proj.weight, weights.in_proj.bias, mu,
+                            time, cond, h_frag, fs, stream);
+      for (const vx_dit_layer& layer : layers) {
+        vx::fused::Qkv(h_frag, layer.input_norm, layer.qkv, qkv, fs, stream);
+        vx::fused::Attention(qkv, weights.rope, attention_frag, fs, stream);
+        vx::fused::Residual(attention_frag, layer.o, static_cast<int>(q_width), fs.hidden,
+                            h_frag, fs, stream);
+        vx::fused::GateUp(h_frag, layer.post_norm, layer.gate_up, swiglu_frag, fs, stream);
+        vx::fused::Residual(swiglu_frag, layer.down, fs.ffn, fs.hidden, h_frag, fs, stream);
+      }
+      vx::fused::OutEuler(h_frag, weights.norm, weights.out_proj.weight,
+                          weights.out_proj.bias, velocity_out, x_update, cfg, dt,
+                          zero_star, fs, stream);
+      return vx::LaunchStatus("vx_dit_eval");
     }
     // Each residual update also leaves the next RMSNorm's operand
     // bf16(h gamma) and the rows' sums of squares, which the qkv and
@@ -708,10 +727,11 @@ int vx_dit_set_path(vx_dit* dit, int path) {
     return vx::Fail(VX_BAD_ARG, "vx_dit_set_path: null handle");
   if (path == VX_DIT_PATH_PERSISTENT && !dit->persistent)
     return vx::Fail(VX_UNSUPPORTED, "vx_dit_set_path: no persistent kernel for this shape");
-  if (path == VX_DIT_PATH_FUSED && !dit->fused)
+  if ((path == VX_DIT_PATH_FUSED || path == VX_DIT_PATH_FUSED_REFERENCE_ORDER) && !dit->fused)
     return vx::Fail(VX_UNSUPPORTED, "vx_dit_set_path: no fused kernels for this shape");
   if (path != VX_DIT_PATH_AUTO && path != VX_DIT_PATH_PERSISTENT &&
-      path != VX_DIT_PATH_FUSED && path != VX_DIT_PATH_UNFUSED)
+      path != VX_DIT_PATH_FUSED && path != VX_DIT_PATH_UNFUSED &&
+      path != VX_DIT_PATH_FUSED_REFERENCE_ORDER)
     return vx::Fail(VX_BAD_ARG, "vx_dit_set_path: unknown path");
   dit->path = path;
   return vx::Succeed();
