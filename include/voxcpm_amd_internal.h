@@ -70,6 +70,19 @@ int vx_test_pack_bf16(const float* input, uint16_t* output, size_t n,
 int vx_stream_read(const void* data, size_t bytes, uint32_t never,
                    uint32_t* sink, void* stream);
 
+/* One launch of `workgroups` workgroups of `threads` threads in which every
+ * workgroup reads all `bytes` (a multiple of 16) of `in` and the workgroups
+ * together write `out` = in + 1 per 32-bit word (workgroup b its b-th
+ * share); `sink` [1] receives the XOR of what was read only if it equals
+ * `never`. With bytes = 0 it is an empty launch of that grid: the
+ * per-launch floor. Launches alternating two buffers form a chain of
+ * dependent hand-offs, the pattern of the DiT's kernels, each of which reads
+ * the whole activation block the previous one wrote. Timed the way the
+ * reference's benchmark times its launches (event-timed repeats,
+ * tools/bench/gemm_bench.cpp:50-84). */
+int vx_handoff(const void* in, void* out, size_t bytes, int workgroups, int threads,
+               uint32_t never, uint32_t* sink, void* stream);
+
 /* The DiT evaluation paths. AUTO (the default) takes FUSED where the shape
  * allows (five launches per layer on fragment-order activations), else
  * UNFUSED (the reference's launch sequence of transformer.cpp:55-100:

@@ -141,6 +141,8 @@ _SIGNATURES = {
                              c_int, c_void_p], c_int),
     "vx_test_pack_bf16": ([c_void_p, c_void_p, c_size, c_void_p], c_int),
     "vx_stream_read": ([c_void_p, c_size, ctypes.c_uint32, c_void_p, c_void_p], c_int),
+    "vx_handoff": ([c_void_p, c_void_p, c_size, c_int, c_int, ctypes.c_uint32, c_void_p,
+                    c_void_p], c_int),
     "vx_rms_norm": ([c_void_p, c_void_p, c_void_p, c_void_p, c_size, c_size,
                      c_float, c_void_p], c_int),
     "vx_qkv_rope": ([c_void_p] * 7 + [c_size] * 5 + [c_void_p], c_int),

@@ -36,20 +36,22 @@ int Allocate(T** pointer, std::size_t count) {
   return VX_OK;
 }
 
-/// SinusoidalPosEmb(width)(t) with scale 1000 in float32 (generator.cpp:40-53).
-std::vector<float> Sinusoid(float t, std::size_t width) {
-  const std::size_t half = width / 2;
-  const auto exponent =
-      static_cast<float>(std::log(10000.0) / static_cast<double>(half - 1));
-  std::vector<float> embedding(width);
-  const float scaled = 1000.0F * t;
-  for (std::size_t i = 0; i < half; ++i) {
-    const float frequency = std::exp(static_cast<float>(i) * -exponent);
-    const float angle = scaled * frequency;
-    embedding[i] = std::sin(angle);
-    embedding[half + i] = std::cos(angle);
+/// The time embedding's input features for time t, already rounded to the
+/// bf16 operand of time_mlp: width / 2 sines and then the cosines of the
+/// same phases, phase j = (1000 t) * e^(-j d) with d = ln(10000) / (width / 2 - 1)
+/// rounded to float32 once. Each step is one float32 operation, so the
+/// values are those of the reference's SinusoidalPosEmb (generator.cpp:40-53).
+std::vector<Bf16> TimeFeatures(float t, std::size_t width) {
+  const std::size_t count = width / 2;
+  const float decay = static_cast<float>(std::log(10000.0) / static_cast<double>(count - 1));
+  const float time_scaled = t * 1000.0F;
+  std::vector<Bf16> features(2 * count);
+  for (std::size_t j = 0; j < count; ++j) {
+    const float phase = time_scaled * std::exp(-decay * static_cast<float>(j));
+    features[j] = vx::Bf16Bits(std::sin(phase));
+    features[count + j] = vx::Bf16Bits(std::cos(phase));
   }
-  return embedding;
+  return features;
 }
 
 struct GraphKey {
@@ -164,7 +166,8 @@ struct vx_dit {
           static_cast<void*>(workspace.qkv),
           static_cast<void*>(workspace.attention),
           static_cast<void*>(workspace.swiglu),
-          static_cast<void*>(workspace.partials),
+          static_cast<void*>(workspace.norm),
+          static_cast<void*>(workspace.squares),
           static_cast<void*>(workspace.sync)})
       if (pointer != nullptr)
         (void)hipFree(pointer);
@@ -199,10 +202,7 @@ struct vx_dit {
   int TimeVector(float t, float* vector, hipStream_t stream) {
     const std::size_t width = shape.hidden;
     const std::size_t in = shape.time_in;
-    const std::vector<float> sinusoid = Sinusoid(t, in);
-    std::vector<Bf16> host(in);
-    for (std::size_t i = 0; i < in; ++i)
-      host[i] = vx::Bf16Bits(sinusoid[i]);
+    const std::vector<Bf16> host = TimeFeatures(t, in);
     VX_HIP(hipMemcpyAsync(time_bf16, host.data(), in * sizeof(Bf16),
                           hipMemcpyHostToDevice, stream),
            "time embedding upload");
@@ -516,23 +516,29 @@ int Create(vx_dit* dit) {
   if (dit->persistent) {
     vx::persistent::Workspace& ws = dit->workspace;
     const int layers = static_cast<int>(s.layers);
-    const std::size_t counts[4] = {vx::persistent::HElements(fs, layers),
-                                   vx::persistent::QkvElements(fs, layers),
-                                   vx::persistent::AttentionElements(fs, layers),
-                                   vx::persistent::SwigluElements(fs, layers)};
-    VX_TRY(Allocate(&ws.h, counts[0]));
-    VX_TRY(Allocate(&ws.qkv, counts[1]));
-    VX_TRY(Allocate(&ws.attention, counts[2]));
-    VX_TRY(Allocate(&ws.swiglu, counts[3]));
+    const std::size_t h_count = vx::persistent::HElements(fs, layers);
+    const std::size_t norm_count = vx::persistent::NormElements(fs, layers);
+    const std::size_t squares_count = vx::persistent::SquaresElements(fs, layers);
+    const std::size_t qkv_count = vx::persistent::QkvElements(fs, layers);
+    const std::size_t attention_count = vx::persistent::AttentionElements(fs, layers);
+    const std::size_t swiglu_count = vx::persistent::SwigluElements(fs, layers);
+    VX_TRY(Allocate(&ws.h, h_count));
+    VX_TRY(Allocate(&ws.norm, norm_count));
+    VX_TRY(Allocate(&ws.squares, squares_count));
+    VX_TRY(Allocate(&ws.qkv, qkv_count));
+    VX_TRY(Allocate(&ws.attention, attention_count));
+    VX_TRY(Allocate(&ws.swiglu, swiglu_count));
     const std::size_t sync_words = vx::persistent::SyncWords(fs, layers);
-    VX_TRY(Allocate(&ws.partials, vx::persistent::PartialElements(fs, layers)));
     VX_TRY(Allocate(&ws.sync, sync_words));
     // Rows past the pair are never written and read as zeros.
-    VX_HIP(hipMemset(ws.h, 0, counts[0] * sizeof(float)), "vx_dit_create: hipMemset");
-    VX_HIP(hipMemset(ws.qkv, 0, counts[1] * sizeof(float)), "vx_dit_create: hipMemset");
-    VX_HIP(hipMemset(ws.attention, 0, counts[2] * sizeof(Bf16)),
+    VX_HIP(hipMemset(ws.h, 0, h_count * sizeof(float)), "vx_dit_create: hipMemset");
+    VX_HIP(hipMemset(ws.norm, 0, norm_count * sizeof(Bf16)), "vx_dit_create: hipMemset");
+    VX_HIP(hipMemset(ws.squares, 0, squares_count * sizeof(float)),
            "vx_dit_create: hipMemset");
-    VX_HIP(hipMemset(ws.swiglu, 0, counts[3] * sizeof(Bf16)), "vx_dit_create: hipMemset");
+    VX_HIP(hipMemset(ws.qkv, 0, qkv_count * sizeof(float)), "vx_dit_create: hipMemset");
+    VX_HIP(hipMemset(ws.attention, 0, attention_count * sizeof(Bf16)),
+           "vx_dit_create: hipMemset");
+    VX_HIP(hipMemset(ws.swiglu, 0, swiglu_count * sizeof(Bf16)), "vx_dit_create: hipMemset");
     VX_HIP(hipMemset(ws.sync, 0, sync_words * sizeof(unsigned)), "vx_dit_create: hipMemset");
   }
 
@@ -563,10 +569,7 @@ int Create(vx_dit* dit) {
     hipStream_t stream = nullptr;
     VX_HIP(hipStreamCreateWithFlags(&stream, hipStreamNonBlocking),
            "vx_dit_create: stream");
-    const std::vector<float> zero = Sinusoid(0.0F, s.time_in);
-    std::vector<Bf16> host(s.time_in);
-    for (std::size_t i = 0; i < s.time_in; ++i)
-      host[i] = vx::Bf16Bits(zero[i]);
+    const std::vector<Bf16> host = TimeFeatures(0.0F, s.time_in);
     int status = VX_OK;
     hipError_t error = hipMemcpyAsync(dit->time_bf16, host.data(),
                                       s.time_in * sizeof(Bf16),

@@ -1,8 +1,13 @@
 // One DiT evaluation (the CFG pair through every layer, the output
 // projection and the guided Euler step) as a single persistent launch: one
-// workgroup per compute unit, the layer's phases separated by grid
-// barriers, and every phase's Q8_0 weights loaded into registers before the
-// barrier that precedes it, so weight latency overlaps the barrier.
+// workgroup of 16 waves per compute unit running the fused path's kernel
+// bodies as phases (input assembly; per layer qkv, attention, o, gate_up,
+// down; the output projection with the Euler step), separated by grid
+// barriers. Each product phase's first Q8_0 weights are loaded into
+// registers as soon as the previous product phase has stored its outputs,
+// so that their latency overlaps the barriers in between. The arithmetic
+// and the work split of every phase are the fused launches' (dit_fused.hip),
+// so the two paths give the same bits.
 //
 // Workspace buffers are written once per launch (one buffer per layer and
 // phase). Producers store with device-scope (relaxed atomic) stores, which
@@ -51,19 +56,21 @@ struct Weights {
 /// Workspace of one handle: write-once buffers per launch, the barrier
 /// counters and the error word.
 struct Workspace {
-  float* h;         // [2 layers + 1][32 hidden] float32 fragment order
-  float* qkv;       // [layers][qkv width / 16][32][16] tile-major
-  Bf16* attention;  // [layers][32 q width] bf16 fragment order
-  Bf16* swiglu;     // [layers][32 ffn] bf16 fragment order
-  float* partials;  // [layers][4 splits][hidden / 16][32][16] of the down product
-  unsigned* sync;   // SyncWords() words, zero at creation
+  float* h;          // [2 layers + 1][32 hidden] float32 fragment order: the
+                     // assembly, then per layer after o and after down
+  Bf16* norm;        // [2 layers][32 hidden] bf16 fragment order: the norm
+                     // operands bf16(h gamma) of layer l's input norm (2 l)
+                     // and post-attention norm (2 l + 1)
+  float* squares;    // [2 layers][32][hidden / 16] their rows' sums of h^2
+  float* qkv;        // [layers][32][qkv width] row-major
+  Bf16* attention;   // [layers][32 q width] bf16 fragment order
+  Bf16* swiglu;      // [layers][32 ffn] bf16 fragment order
+  unsigned* sync;    // SyncWords() words, zero at creation
 };
 
 /// Words of the synchronisation area: the barrier slot counters, the
-/// launch generation, the error word and the down product's arrival
-/// counters.
+/// launch generation and the error word.
 std::size_t SyncWords(const fused::Shape& s, int layers);
-std::size_t PartialElements(const fused::Shape& s, int layers);
 /// Offset (in words) of the error word in the synchronisation area; it
 /// turns non-zero when a barrier wait times out, and every later launch
 /// returns at once until the host clears the area.
@@ -71,13 +78,15 @@ std::size_t ErrorWord();
 
 /// Elements of each workspace buffer for `layers` layers.
 std::size_t HElements(const fused::Shape& s, int layers);
+std::size_t NormElements(const fused::Shape& s, int layers);
+std::size_t SquaresElements(const fused::Shape& s, int layers);
 std::size_t QkvElements(const fused::Shape& s, int layers);
 std::size_t AttentionElements(const fused::Shape& s, int layers);
 std::size_t SwigluElements(const fused::Shape& s, int layers);
 
 /// Whether the persistent kernel takes this shape on a grid of `grid`
-/// workgroups (every phase's tiles fit the grid, one pass of pairs per
-/// wave, at most 32 rows).
+/// workgroups (every phase's workgroups fit the grid, one pass of pairs
+/// per wave, at most 32 rows).
 bool Supported(const fused::Shape& s, int layers, int grid);
 
 /// Workgroups of the launch on the current device: one per compute unit,
@@ -91,9 +100,13 @@ bool Prepare(const fused::Shape& s);
 
 /// 64-bit words of a launch's timestamp trace: [grid][barriers + 1][4]
 /// (slot 0: kernel start and end; slot b: arrival at and exit from grid
-/// barrier b, and in the phase before it the times its activations and
-/// its products were done), s_memrealtime ticks of 10 ns.
+/// barrier b, and in the phase before it the times its products and its
+/// stores were done), s_memrealtime ticks of 10 ns.
 std::size_t TraceWords(int layers, int grid);
+
+/// Grid barriers of one launch: one after the input assembly and five per
+/// layer.
+int Barriers(int layers);
 
 /// One evaluation: x [patch][feat] -> velocity [2][patch][feat]; with
 /// x_update non-null also x_update -= dt (u s + cfg (c - u s)). `trace`

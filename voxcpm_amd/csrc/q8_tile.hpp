@@ -143,6 +143,7 @@ struct TileArgs {
                           // kSwiGluRows bf16 [m][n / 2]
   int accumulate;         // kStore float32: y += product
   float* residual;        // kResidual: float32 fragment order [32][n]
+  const float* residual_in;  // kResidual: the stream added to (null: residual)
   Bf16* frag_out;         // kSwiGlu: bf16 fragment order [32][n / 2]
   // kQkvCache: n = (heads + 2 kv_heads) head_dim columns q | k | v.
   float* q_out;                    // [m][heads][head_dim], rotated
@@ -292,16 +293,77 @@ struct PairStage {
   uint4 a[MT][2];
 };
 
+/// Stores of the engine's epilogues: ordinary, or (kCoherent) device-scope
+/// relaxed atomic stores, which write through the compute die's L2 so that
+/// workgroups on other dies read them after a grid barrier.
+template<bool kCoherent, typename T>
+__device__ inline void Put(T* p, T v) {
+  if constexpr (kCoherent)
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  else
+    *p = v;
+}
+
+/// LDS bytes EnginePrefetch stages: one panel unit per wave, pass slot and
+/// row group.
+__host__ __device__ constexpr int PrefetchBytes(int rg, int pw, int waves) {
+  return waves * pw * rg * kUnitBytes;
+}
+
+/// The Q8_0 weights of the first pass of pairs (pair p waves + wave of
+/// slot p) of workgroup `block_id` of a `grid`-workgroup launch, copied
+/// into the LDS at `stage` (PrefetchBytes bytes, 16-byte aligned) by the
+/// vector memory unit's LDS loads (no registers hold them), unit (wave, p,
+/// r) at ((wave PW + p) RG + r) units: a persistent kernel issues them
+/// before the grid barriers that precede the product, and EngineBody's kPre
+/// reads them from there. Each wave waits for its own copies
+/// (s_waitcnt) before reading them.
+template<int MT, int RG, Output OUT, int PW, int NW = 0>
+__device__ __forceinline__ void EnginePrefetch(const TileArgs& a, int block_id, int grid,
+                                               int thread, std::uint8_t* stage) {
+  static_assert(OUT != Output::kQkvCache, "half pairs are not prefetched");
+  constexpr int waves = NW > 0 ? NW : EngineThreads(MT, RG) / kWave;
+  typedef __attribute__((address_space(3))) void LdsVoid;
+  const int lane = thread % kWave;
+  const int wave = __builtin_amdgcn_readfirstlane(thread / kWave);
+  const int tiles = grid / a.row_blocks;
+  const int tile = block_id % tiles;
+#pragma unroll
+  for (int r = 0; r < RG; ++r) {
+    const int g = min(RgGroup(tile, r, a.group_stride, RG), a.groups - 1);
+    const std::uint8_t* unit = a.w + static_cast<std::size_t>(g) * a.pairs * kUnitBytes;
+#pragma unroll
+    for (int p = 0; p < PW; ++p) {
+      const int pair = p * waves + wave;
+      const std::uint8_t* u = unit + static_cast<std::size_t>(pair < a.pairs ? pair : 0) * kUnitBytes;
+      std::uint8_t* dst = stage + ((wave * PW + p) * RG + r) * kUnitBytes;
+      // 1024 bytes of values, lane L's 16 at 16 L; then the 64 bytes of
+      // scales from lanes 0..3.
+      __builtin_amdgcn_global_load_lds(u + 16 * lane, (LdsVoid*)(dst), 16, 0, 0);
+      if (lane < 4)
+        __builtin_amdgcn_global_load_lds(u + kValueBytes + 16 * lane,
+                                         (LdsVoid*)(dst + kValueBytes), 16, 0, 0);
+    }
+  }
+}
+
 /// The engine. Grid: one workgroup per tile (RG row groups); blockDim.x =
 /// EngineThreads(MT, RG) (waves without pairs add zeros). PW pairs per wave
 /// per pass; kNormF32 needs every pair in one pass (pairs <= waves * PW).
 /// Staged row-major sources load JR groups of 8 rows (8 JR >= m). WK: the
 /// weights' format; bf16 weights (panels or rows [n][k]) accumulate each
 /// block's MFMA straight into the sums, as the reference's bf16 products do
-/// (kernels/wmma_products.hip:210-213).
+/// (kernels/wmma_products.hip:210-213). The workgroup is `block_id` of a
+/// `grid`-workgroup launch (a kernel's blockIdx.x and gridDim.x, or a phase
+/// of a persistent kernel), `thread` its thread (threadIdx.x, or a value
+/// the compiler cannot follow, so that a persistent kernel does not keep
+/// the engine's per-lane index arithmetic in registers across its phases). kCoherent: the epilogue's stores are
+/// device-scope (Put). kPre: fragment-order sources over Q8_0 panels whose
+/// first pass's weights EnginePrefetch staged in the LDS at `pre`.
 template<int MT, int RG, ASource SRC, Output OUT, int PW = 1, int JR = 2 * MT,
-         Weights WK = Weights::kQ8, int NW = 0>
-__device__ __forceinline__ void EngineBody(const TileArgs& a) {
+         Weights WK = Weights::kQ8, int NW = 0, bool kCoherent = false, bool kPre = false>
+__device__ __forceinline__ void EngineBody(const TileArgs& a, int block_id, int grid, int thread,
+                                           const std::uint8_t* pre = nullptr) {
   // One 16-row tile of a fragment-order source per workgroup.
   constexpr bool kScaled = SRC == ASource::kScaledBf16;
   constexpr bool kOneTile = MT == 1 && (SRC == ASource::kFragBf16 || kScaled);
@@ -323,15 +385,18 @@ __device__ __forceinline__ void EngineBody(const TileArgs& a) {
   static_assert(!kRope || RG == 1, "the rotary embedding takes half pairs");
   static_assert(!kHalfPairs || WK != Weights::kBf16Rows, "half pairs read panels");
   extern __shared__ float lds[];
-  const int lane = threadIdx.x % kWave;
-  const int wave = threadIdx.x / kWave;
+  const int lane = thread % kWave;
+  const int wave = __builtin_amdgcn_readfirstlane(thread / kWave);
   // NW > 0: a workgroup of NW waves instead of EngineThreads(MT, RG).
   constexpr int waves = NW > 0 ? NW : EngineThreads(MT, RG) / kWave;
   const int r16 = lane % 16;
   const int octet = lane / 16;
-  const int tiles = static_cast<int>(gridDim.x) / a.row_blocks;
-  const int tile = static_cast<int>(blockIdx.x) % tiles;
-  const int block = static_cast<int>(blockIdx.x) / tiles;
+  static_assert(!kPre || ((SRC == ASource::kFragBf16 || SRC == ASource::kScaledBf16) &&
+                          WK == Weights::kQ8 && OUT != Output::kQkvCache),
+                "prefetched weights are Q8_0 panels of the fragment-order passes");
+  const int tiles = grid / a.row_blocks;
+  const int tile = block_id % tiles;
+  const int block = block_id / tiles;
   int row_lo, row_hi;
   int tile_base = 0;  // the workgroup's first 16-row tile
   if constexpr (kOneTile) {
@@ -346,6 +411,11 @@ __device__ __forceinline__ void EngineBody(const TileArgs& a) {
     row_hi = min(a.m, row_lo + a.rows_per_block);
   }
   const auto in_rows = [&](int row) { return row >= row_lo && row < row_hi; };
+  // kPre: the first pass's weights were staged in the LDS by this wave's
+  // own copies; they are complete once nothing of the wave is in flight,
+  // which costs nothing more here, before its first loads.
+  if constexpr (kPre)
+    __builtin_amdgcn_s_waitcnt(0);
   // The workgroup's first activation row: its 16-row tile of a fragment
   // source, or the first row of its block for one-tile row-major
   // activations (the block's rows are then the tile's, at most 16).
@@ -420,7 +490,7 @@ __device__ __forceinline__ void EngineBody(const TileArgs& a) {
     const __amdgpu_buffer_rsrc_t cache_rows = BufferOf(a.cache_rows, 4U * a.m);
 #pragma unroll
     for (int u = 0; u < kOutputsPerThread; ++u) {
-      const int e = static_cast<int>(threadIdx.x) + u * kThreads;
+      const int e = thread + u * kThreads;
       int row, column;
       const bool live = e < RG * MT * 256 && output_of(e, row, column);
       const std::uint32_t at = 4U * static_cast<std::uint32_t>(live ? row : 0);
@@ -432,12 +502,12 @@ __device__ __forceinline__ void EngineBody(const TileArgs& a) {
   for (int u = 0; u < kOutputsPerThread; ++u) {
     before[u] = 0.0F;
     next_gamma[u] = 0.0F;
-    const int e = static_cast<int>(threadIdx.x) + u * kThreads;
+    const int e = thread + u * kThreads;
     int row, column;
     if (e >= RG * MT * 256 || !output_of(e, row, column))
       continue;
     if constexpr (OUT == Output::kResidual) {
-      before[u] = a.residual[F32FragIndex(row, column)];
+      before[u] = (a.residual_in != nullptr ? a.residual_in : a.residual)[F32FragIndex(row, column)];
       if (a.norm_out != nullptr)
         next_gamma[u] = Bf16Value(a.norm_gamma[column]);
     } else if constexpr (OUT == Output::kStore) {
@@ -559,10 +629,10 @@ __device__ __forceinline__ void EngineBody(const TileArgs& a) {
         a.row_squares, 4U * 32U * static_cast<std::uint32_t>(a.squares_groups));
 #pragma unroll
     for (int pass = 0; pass < kSquarePasses; ++pass) {
-      const int row = pass * kSquareRows + static_cast<int>(threadIdx.x) / 32;
+      const int row = pass * kSquareRows + thread / 32;
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
-        const int g = static_cast<int>(threadIdx.x) % 32 + 32 * j;
+        const int g = thread % 32 + 32 * j;
         squares[pass][j] = __builtin_bit_cast(
             float, BufferLoad4(buffer, 4U * static_cast<std::uint32_t>(row * a.squares_groups + g),
                                row < 32 && g < a.squares_groups));
@@ -613,7 +683,7 @@ __device__ __forceinline__ void EngineBody(const TileArgs& a) {
     for (int u = 0; u < kOutputsPerThread; ++u) {
       rope_cos[u] = 1.0F;
       rope_sin[u] = 0.0F;
-      const int e = static_cast<int>(threadIdx.x) + u * kThreads;
+      const int e = thread + u * kThreads;
       int row, column;
       if (e < kPairedOutputs && output_of(e, row, column) && a.rope != nullptr &&
           column < (a.heads + a.kv_heads) * a.head_dim) {
@@ -646,7 +716,7 @@ __device__ __forceinline__ void EngineBody(const TileArgs& a) {
     for (int p = 0; p < PW; ++p)
       load_weights(wave + p * waves, stage[p]);
     __builtin_amdgcn_sched_barrier(0);
-    const int t = static_cast<int>(threadIdx.x);
+    const int t = thread;
     const int per_row = a.k / 8;
     // A wave adds each row's sums: at most one row per wave per pass.
     const int rows_per_pass = min(kThreads / per_row, waves);
@@ -843,7 +913,20 @@ __device__ __forceinline__ void EngineBody(const TileArgs& a) {
 #pragma unroll
     for (int p = 0; p < PW; ++p) {
       load_activations(p * waves + wave, current[p]);
-      load_weights(p * waves + wave, current[p]);
+      if constexpr (!kPre)
+        load_weights(p * waves + wave, current[p]);
+    }
+    if constexpr (kPre) {
+      // The staged weights, read from the LDS once the activations' loads
+      // are in flight.
+#pragma unroll
+      for (int p = 0; p < PW; ++p)
+#pragma unroll
+        for (int r = 0; r < RG; ++r) {
+          const std::uint8_t* unit = pre + ((wave * PW + p) * RG + r) * kUnitBytes;
+          current[p].w[r] = *reinterpret_cast<const uint4*>(unit + 16 * lane);
+          current[p].scales[r] = *reinterpret_cast<const std::uint32_t*>(unit + kValueBytes + 4 * r16);
+        }
     }
     if constexpr (kScaled)
       load_squares();
@@ -877,8 +960,8 @@ __device__ __forceinline__ void EngineBody(const TileArgs& a) {
     for (int pass = 0; pass < kSquarePasses; ++pass) {
       float total = ((squares[pass][0] + squares[pass][1]) + squares[pass][2]) + squares[pass][3];
       total = AddXor16(RowSum16(total));
-      const int row = pass * kSquareRows + static_cast<int>(threadIdx.x) / 32;
-      if (threadIdx.x % 32 == 0 && row < 32)
+      const int row = pass * kSquareRows + thread / 32;
+      if (thread % 32 == 0 && row < 32)
         row_scale[row] = rsqrtf(total / static_cast<float>(a.k) + a.eps);
     }
   }
@@ -914,7 +997,7 @@ __device__ __forceinline__ void EngineBody(const TileArgs& a) {
 #pragma unroll
   for (int u = 0; u < kOutputsPerThread; ++u) {
     fresh[u] = 0.0F;
-    const int e = static_cast<int>(threadIdx.x) + u * kThreads;
+    const int e = thread + u * kThreads;
     // kHalfPairs: every lane of a wave with outputs takes part in the
     // exchange with its partner 8 lanes away (outputs are whole waves).
     float mine = 0.0F;
@@ -930,15 +1013,15 @@ __device__ __forceinline__ void EngineBody(const TileArgs& a) {
     if constexpr (OUT == Output::kStore) {
       const std::size_t at = static_cast<std::size_t>(row) * a.n + column;
       if (a.y != nullptr)
-        a.y[at] = a.accumulate ? before[u] + v : v;
+        Put<kCoherent>(a.y + at, a.accumulate ? before[u] + v : v);
       else
-        a.y_bf16[at] = Bf16Fast(v);
+        Put<kCoherent>(a.y_bf16 + at, Bf16Fast(v));
     } else if constexpr (OUT == Output::kResidual) {
       fresh[u] = before[u] + v;
-      a.residual[F32FragIndex(row, column)] = fresh[u];
+      Put<kCoherent>(a.residual + F32FragIndex(row, column), fresh[u]);
     } else if constexpr (OUT == Output::kSwiGlu) {
       const float up = kScaled ? total_of(e + MT * 256) * row_scale[row] : total_of(e + MT * 256);
-      a.frag_out[BfFragIndex(row, column)] = Bf16Fast(Silu(v) * up);
+      Put<kCoherent>(a.frag_out + BfFragIndex(row, column), Bf16Fast(Silu(v) * up));
     } else if constexpr (kRope) {
       // (x_i, x_{i + half}) -> (x_i c - x_{i + half} s, x_{i + half} c + x_i s)
       // on q and k; v is stored as it is. Lanes r16 < 8 hold x_i and
@@ -976,14 +1059,14 @@ __device__ __forceinline__ void EngineBody(const TileArgs& a) {
       // flow; outputs past the block add zeros and are not written).
 #pragma unroll
       for (int u = 0; u < kOutputsPerThread; ++u) {
-        const int e = static_cast<int>(threadIdx.x) + u * kThreads;
+        const int e = thread + u * kThreads;
         int row = 0, column = 0;
         const bool live = e < outputs && output_of(e, row, column);
         const float square = RowSum16(fresh[u] * fresh[u]);
         if (live) {
-          a.norm_out[BfFragIndex(row, column)] = Bf16Fast(fresh[u] * next_gamma[u]);
+          Put<kCoherent>(a.norm_out + BfFragIndex(row, column), Bf16Fast(fresh[u] * next_gamma[u]));
           if (column % 16 == 0)
-            a.norm_squares[row * (a.n / 16) + column / 16] = square;
+            Put<kCoherent>(a.norm_squares + row * (a.n / 16) + column / 16, square);
         }
       }
     }
@@ -994,7 +1077,9 @@ template<int MT, int RG, ASource SRC, Output OUT, int PW = 1, int JR = 2 * MT,
          Weights WK = Weights::kQ8, int NW = 0>
 __global__ __launch_bounds__(NW > 0 ? NW * kWave : EngineThreads(MT, RG)) void EngineKernel(
     TileArgs a) {
-  EngineBody<MT, RG, SRC, OUT, PW, JR, WK, NW>(a);
+  EngineBody<MT, RG, SRC, OUT, PW, JR, WK, NW>(a, static_cast<int>(blockIdx.x),
+                                              static_cast<int>(gridDim.x),
+                                              static_cast<int>(threadIdx.x));
 }
 
 

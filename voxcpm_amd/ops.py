@@ -19,7 +19,7 @@ from ._lib import (VX_WEIGHTS_BF16, VX_WEIGHTS_Q8_0, DitLayer, DitProjection, Di
 __all__ = [
     "Scratch", "Dit", "q8_pack", "q8_unpack_blocks", "q8_unpack_bf16",
     "q8_linear", "q8_linear_bf16", "q8_plan", "bf16_pack", "bf16_unpack", "bf16_linear",
-    "bf16_linear_rows", "stream_read", "euler_schedule", "rope_table", "Stack",
+    "bf16_linear_rows", "stream_read", "handoff", "euler_schedule", "rope_table", "Stack",
     "split_attention", "Gguf", "Vae",
 ]
 
@@ -166,6 +166,17 @@ def stream_read(data: torch.Tensor, sink: torch.Tensor, never: int = 0x9E3779B9,
     `sink` (int32 [1]) changes only if the bytes' XOR equals `never`."""
     check(lib().vx_stream_read(_ptr(data), data.numel() * data.element_size(), never,
                                _ptr(sink), _stream(stream)))
+
+
+def handoff(data_in: torch.Tensor | None, data_out: torch.Tensor | None, nbytes: int,
+            workgroups: int, threads: int, sink: torch.Tensor, never: int = 0x9E3779B9,
+            stream=None) -> None:
+    """One launch of the hand-off probe (vx_handoff): every workgroup reads
+    `nbytes` of data_in, together they write data_out = data_in + 1; with
+    nbytes = 0 an empty launch of that grid."""
+    check(lib().vx_handoff(_ptr(data_in) if data_in is not None else None,
+                           _ptr(data_out) if data_out is not None else None, nbytes,
+                           workgroups, threads, never, _ptr(sink), _stream(stream)))
 
 
 def q8_plan(m: int, k: int, n: int, scratch: Scratch | None = None) -> dict:
