@@ -50,6 +50,44 @@ def _compile(source: pathlib.Path) -> pathlib.Path:
     return obj
 
 
+def resource_report(jobs: int | None = None) -> dict[str, dict[str, int]]:
+    """Compiles every csrc/*.hip for the device only with the compiler's
+    kernel resource remarks and returns {kernel symbol: {"vgprs", "sgprs",
+    "scratch", "vgpr_spill", "sgpr_spill"}} (scratch in bytes per lane)."""
+    import re
+    import tempfile
+    fields = {"VGPRs": "vgprs", "TotalSGPRs": "sgprs", "ScratchSize [bytes/lane]": "scratch",
+              "VGPRs Spill": "vgpr_spill", "SGPRs Spill": "sgpr_spill"}
+
+    def remarks(source: pathlib.Path) -> dict[str, dict[str, int]]:
+        with tempfile.TemporaryDirectory() as tmp:
+            cmd = [HIPCC, *FLAGS, "--cuda-device-only", "-Rpass-analysis=kernel-resource-usage",
+                   "-c", str(source), "-o", str(pathlib.Path(tmp) / "device.o")]
+            result = subprocess.run(cmd, capture_output=True, text=True)
+        if result.returncode != 0:
+            raise RuntimeError(f"hipcc failed on {source.name}:\n{result.stderr}")
+        kernels: dict[str, dict[str, int]] = {}
+        current = None
+        for line in result.stderr.splitlines():
+            match = re.search(r"remark: +Function Name: (\S+)", line)
+            if match:
+                current = kernels.setdefault(match.group(1), {})
+                continue
+            for label, key in fields.items():
+                match = re.search(r"remark: +" + re.escape(label) + r": (\d+)", line)
+                if match and current is not None:
+                    current[key] = int(match.group(1))
+        return kernels
+
+    srcs = sorted(CSRC.glob("*.hip"))
+    jobs = jobs or min(len(srcs), os.cpu_count() or 4, 8)
+    report: dict[str, dict[str, int]] = {}
+    with concurrent.futures.ThreadPoolExecutor(jobs) as pool:
+        for kernels in pool.map(remarks, srcs):
+            report.update(kernels)
+    return report
+
+
 def build(jobs: int | None = None, verbose: bool = False) -> pathlib.Path:
     BUILD.mkdir(parents=True, exist_ok=True)
     srcs = sources()

@@ -43,16 +43,27 @@ __global__ __launch_bounds__(1024) void OutEulerKernel(OutArgs a) {
 
 // ---- the engine's fused instantiations -------------------------------------
 
+/// One launch of the engine on weights of format WK. The norm products with
+/// two pairs per wave (k = hidden of 1025-2048 columns, one pass by
+/// Supported) take the one-pass kernel, which holds no registers for a next
+/// pass: the two-pass kernel there needs more registers than 16 waves have.
+/// The others keep the kernel with a next pass in flight, which measured
+/// faster on MI355X even where one pass covers k (patch 2611 -> 2586 us).
+template<q8::ASource SRC, q8::Output OUT, int RG, int PW, int MT, q8::Weights WK>
+void LaunchEngineAs(const q8::TileArgs& args, int tiles, int waves, hipStream_t stream) {
+  const std::size_t shared = q8::EngineShared(MT, RG, waves, SRC);
+  constexpr bool kOnePass = SRC == q8::ASource::kScaledBf16 && PW >= 2;
+  q8::EngineKernel<MT, RG, SRC, OUT, PW, 2 * MT, WK, 0, kOnePass>
+      <<<tiles, waves * kWave, shared, stream>>>(args);
+}
+
 template<q8::ASource SRC, q8::Output OUT, int RG, int PW, int MT = 2>
 void LaunchEngine(const q8::TileArgs& args, int tiles, int waves, q8::Weights kind,
                   hipStream_t stream) {
-  const std::size_t shared = q8::EngineShared(MT, RG, waves, SRC);
   if (kind == q8::Weights::kQ8)
-    q8::EngineKernel<MT, RG, SRC, OUT, PW, 2 * MT, q8::Weights::kQ8>
-        <<<tiles, waves * kWave, shared, stream>>>(args);
+    LaunchEngineAs<SRC, OUT, RG, PW, MT, q8::Weights::kQ8>(args, tiles, waves, stream);
   else
-    q8::EngineKernel<MT, RG, SRC, OUT, PW, 2 * MT, q8::Weights::kBf16>
-        <<<tiles, waves * kWave, shared, stream>>>(args);
+    LaunchEngineAs<SRC, OUT, RG, PW, MT, q8::Weights::kBf16>(args, tiles, waves, stream);
 }
 
 }  // namespace
@@ -163,11 +174,11 @@ void Residual(const Bf16* act, const void* weight, int k, int n, float* h,
     // 2588 us per patch); bf16 panels two (four spill 36 registers).
     SetTileBlocks(args, args.groups, s.rows);
     if (s.weights == q8::Weights::kQ8)
-      LaunchEngine<q8::ASource::kFragBf16, q8::Output::kResidual, 1, 4, 1>(
-          args, args.groups * args.row_blocks, kMaxWaves, s.weights, stream);
+      LaunchEngineAs<q8::ASource::kFragBf16, q8::Output::kResidual, 1, 4, 1, q8::Weights::kQ8>(
+          args, args.groups * args.row_blocks, kMaxWaves, stream);
     else
-      LaunchEngine<q8::ASource::kFragBf16, q8::Output::kResidual, 1, 2, 1>(
-          args, args.groups * args.row_blocks, kMaxWaves, s.weights, stream);
+      LaunchEngineAs<q8::ASource::kFragBf16, q8::Output::kResidual, 1, 2, 1, q8::Weights::kBf16>(
+          args, args.groups * args.row_blocks, kMaxWaves, stream);
   } else {
     SetRowBlocks(args, args.groups, s.rows);
     LaunchEngine<q8::ASource::kFragBf16, q8::Output::kResidual, 1, 1>(

@@ -266,6 +266,9 @@ template<bool kWide, bool kDown>
 struct ResidualPlan {
   static constexpr int kMt = kWide ? 1 : 2;
   static constexpr int kPw = kWide ? 4 : 1;
+  // The wide plan's four pairs per wave cover k in one pass (Supported
+  // asks for at most 64 pairs).
+  static constexpr bool kOnePass = kWide;
   __device__ static void Prefetch(const Args& a, int l, int wg, std::uint8_t* stage) {
     const q8::TileArgs t = ResidualArgs<kWide, kDown>(a, Opaque(l));
     const int grid = t.groups * t.row_blocks;
@@ -277,7 +280,7 @@ struct ResidualPlan {
     const int grid = t.groups * t.row_blocks;
     if (wg < grid)
       q8::EngineBody<kMt, 1, q8::ASource::kFragBf16, q8::Output::kResidual, kPw, 2 * kMt,
-                     q8::Weights::kQ8, 0, true, true>(t, wg, grid, Thread(), stage);
+                     q8::Weights::kQ8, 0, true, true, kOnePass>(t, wg, grid, Thread(), stage);
   }
 };
 
@@ -292,7 +295,7 @@ struct QkvPlan {
     const q8::TileArgs t = QkvArgs(a, Opaque(l));
     if (wg < t.groups)
       q8::EngineBody<2, 1, q8::ASource::kScaledBf16, q8::Output::kStore, PA, 4,
-                     q8::Weights::kQ8, 0, true, true>(t, wg, t.groups, Thread(), stage);
+                     q8::Weights::kQ8, 0, true, true, true>(t, wg, t.groups, Thread(), stage);
   }
 };
 
@@ -307,7 +310,7 @@ struct GateUpPlan {
     const q8::TileArgs t = GateUpArgs(a, Opaque(l));
     if (wg < t.group_stride)
       q8::EngineBody<2, 2, q8::ASource::kScaledBf16, q8::Output::kSwiGlu, PA, 4,
-                     q8::Weights::kQ8, 0, true, true>(t, wg, t.group_stride, Thread(), stage);
+                     q8::Weights::kQ8, 0, true, true, true>(t, wg, t.group_stride, Thread(), stage);
   }
 };
 
@@ -511,7 +514,11 @@ bool Supported(const fused::Shape& s, int layers, int grid) {
     return false;
   const int q_width = s.heads * s.head_dim;
   const int qkv_width = (s.heads + 2 * s.kv_heads) * s.head_dim;
-  if (qkv_width % 16 != 0 || fused::PairsOf(s.hidden) > 2 * kWaves)
+  // qkv and gate_up take k = hidden in one pass of at most two pairs per
+  // wave, the wide residual plan at most four.
+  if (qkv_width % 16 != 0 || fused::PairsOf(s.hidden) > 2 * kWaves ||
+      (Wide(q_width) && fused::PairsOf(q_width) > 4 * kWaves) ||
+      (Wide(s.ffn) && fused::PairsOf(s.ffn) > 4 * kWaves))
     return false;
   // Every phase's workgroups fit the grid.
   if (s.hidden / 16 > grid || qkv_width / 16 > grid || 2 * s.heads > grid ||

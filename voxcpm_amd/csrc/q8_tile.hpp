@@ -360,8 +360,12 @@ __device__ __forceinline__ void EnginePrefetch(const TileArgs& a, int block_id, 
 /// the engine's per-lane index arithmetic in registers across its phases). kCoherent: the epilogue's stores are
 /// device-scope (Put). kPre: fragment-order sources over Q8_0 panels whose
 /// first pass's weights EnginePrefetch staged in the LDS at `pre`.
+/// kOnePass: fragment-order sources whose pairs one pass covers
+/// (pairs <= waves PW, the launcher's promise): no registers are set aside
+/// for a next pass in flight.
 template<int MT, int RG, ASource SRC, Output OUT, int PW = 1, int JR = 2 * MT,
-         Weights WK = Weights::kQ8, int NW = 0, bool kCoherent = false, bool kPre = false>
+         Weights WK = Weights::kQ8, int NW = 0, bool kCoherent = false, bool kPre = false,
+         bool kOnePass = false>
 __device__ __forceinline__ void EngineBody(const TileArgs& a, int block_id, int grid, int thread,
                                            const std::uint8_t* pre = nullptr) {
   // One 16-row tile of a fragment-order source per workgroup.
@@ -908,7 +912,8 @@ __device__ __forceinline__ void EngineBody(const TileArgs& a, int block_id, int 
     // Passes of PW pairs per wave (slot p of the pass at base: pair
     // base + p waves + wave); the next pass is loaded before this one is
     // multiplied, so 2 PW pairs per wave are in flight.
-    PairStage<MT, RG> current[PW], next[PW];
+    PairStage<MT, RG> current[PW];
+    PairStage<MT, RG> next[kOnePass ? 1 : PW];
     const int step = waves * PW;
 #pragma unroll
     for (int p = 0; p < PW; ++p) {
@@ -931,12 +936,14 @@ __device__ __forceinline__ void EngineBody(const TileArgs& a, int block_id, int 
     if constexpr (kScaled)
       load_squares();
     for (int base = 0; base < a.pairs; base += step) {
-      const bool more = base + step < a.pairs;
-      if (more) {
+      const bool more = !kOnePass && base + step < a.pairs;
+      if constexpr (!kOnePass) {
+        if (more) {
 #pragma unroll
-        for (int p = 0; p < PW; ++p) {
-          load_activations(base + step + p * waves + wave, next[p]);
-          load_weights(base + step + p * waves + wave, next[p]);
+          for (int p = 0; p < PW; ++p) {
+            load_activations(base + step + p * waves + wave, next[p]);
+            load_weights(base + step + p * waves + wave, next[p]);
+          }
         }
       }
 #pragma unroll
@@ -945,9 +952,11 @@ __device__ __forceinline__ void EngineBody(const TileArgs& a, int block_id, int 
           multiply(current[p]);
       if (!more)
         break;
+      if constexpr (!kOnePass) {
 #pragma unroll
-      for (int p = 0; p < PW; ++p)
-        current[p] = next[p];
+        for (int p = 0; p < PW; ++p)
+          current[p] = next[p];
+      }
     }
   }
 
@@ -1074,10 +1083,10 @@ __device__ __forceinline__ void EngineBody(const TileArgs& a, int block_id, int 
 }
 
 template<int MT, int RG, ASource SRC, Output OUT, int PW = 1, int JR = 2 * MT,
-         Weights WK = Weights::kQ8, int NW = 0>
+         Weights WK = Weights::kQ8, int NW = 0, bool kOnePass = false>
 __global__ __launch_bounds__(NW > 0 ? NW * kWave : EngineThreads(MT, RG)) void EngineKernel(
     TileArgs a) {
-  EngineBody<MT, RG, SRC, OUT, PW, JR, WK, NW>(a, static_cast<int>(blockIdx.x),
+  EngineBody<MT, RG, SRC, OUT, PW, JR, WK, NW, false, false, kOnePass>(a, static_cast<int>(blockIdx.x),
                                               static_cast<int>(gridDim.x),
                                               static_cast<int>(threadIdx.x));
 }
