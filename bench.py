@@ -35,6 +35,8 @@ SWEEP_SHAPES = [(1024, 3072), (1024, 8192), (2048, 2048), (2048, 16384)]
 SINGLE_SHAPE = (1024, 4096)
 SWEEP_ROWS = [1, 2, 22, 44, 128]
 ROWS = 22
+# Runs of the CPU oracle's whole patch (the median is reported).
+CPU_PATCH_RUNS = 5
 ROTATION_BYTES = 1.1e9
 BF16_PEAK_TFLOPS = 2500.0
 # MFMA utilisation read from rocprofv3 counters for the prefill kernel
@@ -88,17 +90,26 @@ class Product:
         self.copies = max(8, int(np.ceil(ROTATION_BYTES / self.bytes)))
         self.pool = packed.repeat(self.copies).view(self.copies, -1)
         self.inputs = {}
+        self.outputs_bf16 = {}
         for m in rows:
             x = synth.activations(rng, m, k)
             self.inputs[m] = (
                 torch.from_numpy(x.view(np.int16)).to(device).view(torch.bfloat16),
                 torch.empty((m, n), dtype=torch.float32, device=device))
+            self.outputs_bf16[m] = torch.empty((m, n), dtype=torch.bfloat16, device=device)
         self.launches = 0
 
     def launch(self, ops, scratch, m: int) -> None:
         x, y = self.inputs[m]
         ops.q8_linear(x, self.pool[self.launches % self.copies], self.n, y=y,
                       scratch=scratch)
+        self.launches += 1
+
+    def launch_bf16(self, ops, scratch, m: int) -> None:
+        """The same product with its bf16 output (vx_q8_linear_bf16)."""
+        x, _ = self.inputs[m]
+        ops.q8_linear_bf16(x, self.pool[self.launches % self.copies], self.n,
+                           y=self.outputs_bf16[m], scratch=scratch)
         self.launches += 1
 
 
@@ -146,6 +157,36 @@ def read_probe(torch, device, stream) -> float:
     return data.numel() * 8 / seconds / 1e9
 
 
+def gpu_launch_floor(torch, ops, device, stream):
+    """The per-launch costs every kernel of a HIP graph pays, measured with
+    the kernels' own launch pattern (vx_handoff, replayed from a graph,
+    events on the launch stream): an empty launch of one workgroup and of
+    the products' grid (256 workgroups of 1024 threads), and a chain of
+    dependent launches in which every workgroup reads the whole block the
+    previous launch wrote (1, 45 and 64 KB: the DiT's activation blocks
+    are 45-64 KB of bf16 per workgroup)."""
+    sink = torch.zeros(4, dtype=torch.int32, device=device)
+    buffers = [torch.zeros(1 << 18, dtype=torch.int32, device=device) for _ in range(2)]
+    count = 400
+    result = {}
+    for name, workgroups, threads, nbytes in [
+            ("empty_1x64", 1, 64, 0), ("empty_256x1024", 256, 1024, 0),
+            ("dependent_1KB", 256, 1024, 1024), ("dependent_45KB", 256, 1024, 45056),
+            ("dependent_64KB", 256, 1024, 65536)]:
+        g = graph_of(torch, stream,
+                     lambda i, w=workgroups, t=threads, b=nbytes: ops.handoff(
+                         buffers[i % 2], buffers[(i + 1) % 2], b, w, t, sink), count)
+        g.replay()
+        result[name] = round(time_graph(torch, stream, g, repeats=5) / count * 1e6, 3)
+        del g
+    log(f"launch floor: {result}")
+    return {"launch_floor_us": result["empty_256x1024"],
+            "dependent_launch_us": result["dependent_64KB"],
+            "us": result,
+            "method": "vx_handoff launches replayed 400 at a time from one HIP graph, "
+                      "median of five replays"}
+
+
 def gpu_products(args, torch, ops, synth, device, stream):
     scratch = ops.Scratch(128, 16384)
     log("building weight pools")
@@ -186,16 +227,25 @@ def gpu_products(args, torch, ops, synth, device, stream):
     for row in sweep:
         if row["m"] == ROWS:
             log(f"  M=22 K={row['k']} N={row['n']}: {row['us']} us, {row['gbs']} GB/s")
+    # The CPU-runnable configuration's product: bf16 output [22][4096] as
+    # that configuration states it (vx_q8_linear_bf16), and beside it the
+    # float32 output of the sweep's launches.
     count = max(single.copies, 64)
-    g = graph_of(torch, stream, lambda _i: single.launch(ops, scratch, ROWS), count)
+    g = graph_of(torch, stream, lambda _i: single.launch_bf16(ops, scratch, ROWS), count)
     g.replay()
     us = time_graph(torch, stream, g) / count * 1e6
     del g
-    single_row = {"m": ROWS, "k": single.k, "n": single.n, "us": round(us, 3),
+    g = graph_of(torch, stream, lambda _i: single.launch(ops, scratch, ROWS), count)
+    g.replay()
+    us_f32 = time_graph(torch, stream, g) / count * 1e6
+    del g
+    single_row = {"m": ROWS, "k": single.k, "n": single.n, "output": "bf16",
+                  "us": round(us, 3),
                   "gbs": round(single.bytes / us / 1e3, 1),
-                  "hbm_frac": round(single.bytes / us / 1e3 / HBM_PEAK_GBS, 4)}
-    log(f"  single product M=22 K={single.k} N={single.n}: {us:.3f} us, "
-        f"{single.bytes / us / 1e3:.1f} GB/s")
+                  "hbm_frac": round(single.bytes / us / 1e3 / HBM_PEAK_GBS, 4),
+                  "us_f32_output": round(us_f32, 3)}
+    log(f"  single product M=22 K={single.k} N={single.n}, bf16 output: {us:.3f} us, "
+        f"{single.bytes / us / 1e3:.1f} GB/s (float32 output {us_f32:.3f} us)")
     del single
     # The per-launch read ceiling: each shape's bytes, rotated and replayed
     # from a HIP graph the same way, read once with no arithmetic
@@ -599,6 +649,7 @@ def gpu_patch(args, torch, ops, synth, device, stream):
     # The persistent evaluation (one launch per Euler step, grid barriers
     # between the layer's phases), selected explicitly.
     from voxcpm_amd import _lib
+    default_path = dit.path
     dit.set_path(_lib.DIT_PATH_PERSISTENT)
     for _ in range(2):
         dit.patch(mu, cond, x, t, dt, evaluate, config.cfg, config.zero_star)
@@ -674,7 +725,100 @@ def gpu_patch(args, torch, ops, synth, device, stream):
             "roofline_us": round(patch_bytes / HBM_PEAK_GBS / 1e3, 1),
             "hbm_frac_cold": round(patch_bytes / cold_us / 1e3 / HBM_PEAK_GBS, 4),
             "workload": "12 blocks hidden 1024, 16 heads x 64, SwiGLU 4096, "
-                        "22 rows (CFG pair x 11), 10 uniform Euler steps, CFG 2.0"}
+                        "22 rows (CFG pair x 11), 10 uniform Euler steps, CFG 2.0",
+            "path": "us_warm and us_cold: the default (AUTO) path, "
+                    f"{PATH_NAMES[default_path]}; us_warm_persistent, us_warm_per_kernel and "
+                    "us_warm_fused_reference_order the other paths, selected explicitly"}
+
+
+PATH_NAMES = {
+    1: "PERSISTENT (one launch per evaluation, grid barriers between the phases)",
+    2: "FUSED (five launches per layer: qkv from the producers' norm operand, "
+       "attention, o + residual, gate_up + SwiGLU, down + residual)",
+    3: "UNFUSED (the reference's launch sequence)",
+    4: "FUSED_REFERENCE_ORDER (the fused launches with the norms before the products' "
+       "bf16 rounding)",
+}
+
+
+def dit_workload(torch, ops, synth, device, stream) -> None:
+    """Eager launches for counter runs of the DiT's fused kernels: twenty
+    evaluations of the synthetic 12-block DiT on the default path (the
+    weights stay in the 256 MB MALL across evaluations, as within a
+    patch), after five untimed ones."""
+    config = synth.SYNTHETIC_DIT
+    rope = ops.rope_table(config.rope_theta, config.head_dim, config.rope_factors,
+                          config.rope_scaling, 3 + 2 * config.patch)
+    weights = synth.dit_weights(config, 3, rope)
+    dit = ops.Dit(weights, device, stream)
+    inputs = synth.patch_inputs(config, 4)
+    mu = torch.from_numpy(inputs.mu).to(device)
+    cond = torch.from_numpy(inputs.cond_latent).to(device)
+    x = torch.from_numpy(inputs.noise).to(device)
+    for _ in range(25):
+        dit.velocity(mu, cond, x, 0.63)
+    torch.cuda.synchronize()
+    log(f"DiT workload done: 25 evaluations on path {dit.path}")
+    dit.close()
+
+
+def dit_trace(torch, ops, synth, device, stream) -> None:
+    """The persistent evaluation's per-phase timeline (vx_dit_set_trace):
+    one traced evaluation of the synthetic 12-block DiT after warm-up; per
+    phase kind, the mean over layers of the workgroups' times from leaving
+    the previous barrier to their products done (mean and latest workgroup)
+    and to their stores done (latest), the phase's critical time (first
+    workgroup out of the previous barrier to the last one in at the next),
+    and the barrier's own time (last arrival to first and last exit).
+    Printed as a table to stderr."""
+    from voxcpm_amd import _lib
+    config = synth.SYNTHETIC_DIT
+    rope = ops.rope_table(config.rope_theta, config.head_dim, config.rope_factors,
+                          config.rope_scaling, 3 + 2 * config.patch)
+    weights = synth.dit_weights(config, 3, rope)
+    dit = ops.Dit(weights, device, stream)
+    inputs = synth.patch_inputs(config, 4)
+    mu = torch.from_numpy(inputs.mu).to(device)
+    cond = torch.from_numpy(inputs.cond_latent).to(device)
+    x = torch.from_numpy(inputs.noise).to(device)
+    dit.set_path(_lib.DIT_PATH_PERSISTENT)
+    for _ in range(5):
+        dit.velocity(mu, cond, x, 0.63)
+    torch.cuda.synchronize()
+    trace = dit.set_trace(True)
+    for _ in range(3):
+        dit.velocity(mu, cond, x, 0.63)
+        torch.cuda.synchronize()
+    dit.status()
+    layers = config.layers
+    barriers = 1 + 5 * layers
+    tr = trace.cpu().numpy().astype(np.float64)
+    grid = tr.size // (4 * (barriers + 1))
+    tr = tr.reshape(grid, barriers + 1, 4) / 100.0  # 100 MHz ticks -> us
+    start = tr[:, 0, 0].min()
+    span = tr[:, 0, 1].max() - start
+    kinds = ["qkv", "attention", "o", "gate_up", "down"]
+    rows = {name: [] for name in ["input assembly"] + kinds}
+    for b in range(1, barriers + 1):
+        arrive, leave, products, stores = (tr[:, b, i] for i in range(4))
+        previous = tr[:, b - 1, 1] if b > 1 else tr[:, 0, 0]
+        kind = "input assembly" if b == 1 else kinds[(b - 2) % 5]
+        rows[kind].append(((products - previous).mean(), (products - previous).max(),
+                           (stores - previous).max(), arrive.max() - previous.min(),
+                           leave.min() - arrive.max(), leave.max() - arrive.max()))
+    log(f"persistent evaluation: {grid} workgroups, {span:.2f} us per evaluation, "
+        f"{span / layers:.2f} us per layer")
+    log("| phase | products done, mean (us) | products done, latest | stores done, latest | "
+        "critical | barrier to first exit | barrier to last exit |")
+    log("|---|---|---|---|---|---|---|")
+    total = 0.0
+    for name, values in rows.items():
+        mean = np.mean(np.array(values), axis=0)
+        if name != "input assembly":
+            total += mean[3] + mean[4]
+        log(f"| {name} | " + " | ".join(f"{v:.2f}" for v in mean) + " |")
+    log(f"per layer, critical + barrier summed over the five phases: {total:.2f} us")
+    dit.close()
 
 
 def host_cores() -> int:
@@ -742,13 +886,19 @@ def cpu_patch(synth):
     dit = oracle_lib.OracleDit(weights, threads=threads)
     inputs = synth.patch_inputs(config, 4)
     t, dt, evaluate = oracle_lib.euler_schedule(config.steps, config.sway, config.skip)
-    start = time.perf_counter()
-    dit.patch(inputs.mu, inputs.cond_latent, inputs.noise, t, dt, evaluate, config.cfg,
-              config.zero_star)
-    seconds = time.perf_counter() - start
-    log(f"CPU oracle: one 10-step patch {seconds * 1e3:.0f} ms on {threads} threads")
+    times = []
+    for _ in range(CPU_PATCH_RUNS):
+        start = time.perf_counter()
+        dit.patch(inputs.mu, inputs.cond_latent, inputs.noise, t, dt, evaluate, config.cfg,
+                  config.zero_star)
+        times.append(time.perf_counter() - start)
+    seconds = float(np.median(times))
+    log(f"CPU oracle: one 10-step patch {seconds * 1e3:.0f} ms on {threads} threads "
+        f"(median of {len(times)})")
     return {"us_per_patch": round(seconds * 1e6, 1), "cores": threads,
-            "sample": f"one whole patch ({int(np.sum(evaluate))} evaluations), timed once"}
+            "runs_us": [round(x * 1e6, 1) for x in times],
+            "sample": f"one whole patch ({int(np.sum(evaluate))} evaluations), the median "
+                      f"of {len(times)} runs"}
 
 
 def main() -> int:
@@ -770,6 +920,10 @@ def main() -> int:
                         help="only run the eager launches that counter runs read")
     parser.add_argument("--prefill-workload", action="store_true",
                         help="only run eager prefill products (for counter runs)")
+    parser.add_argument("--dit-workload", action="store_true",
+                        help="only run eager DiT evaluations (for counter runs)")
+    parser.add_argument("--dit-trace", action="store_true",
+                        help="only print the persistent DiT evaluation's per-phase timeline")
     parser.add_argument("--lm-step-workload", action="store_true",
                         help="only run the stacks' decode steps and the AudioVAE "
                              "(for kernel traces)")
@@ -797,6 +951,12 @@ def main() -> int:
     if args.prefill_workload:
         prefill_workload(torch, ops, synth, device, stream)
         return 0
+    if args.dit_trace:
+        dit_trace(torch, ops, synth, device, stream)
+        return 0
+    if args.dit_workload:
+        dit_workload(torch, ops, synth, device, stream)
+        return 0
     if args.lm_step_workload:
         gpu_lm_step(args, torch, ops, synth, device, stream)
         gpu_vae(args, torch, ops, synth, device, stream)
@@ -804,6 +964,7 @@ def main() -> int:
 
     probe = read_probe(torch, device, stream)
     log(f"read probe {probe:.0f} GB/s")
+    floor = gpu_launch_floor(torch, ops, device, stream)
     products = gpu_products(args, torch, ops, synth, device, stream)
     lm = None if args.no_lm else gpu_lm(args, torch, ops, synth, device, stream)
     if lm is not None:
@@ -865,6 +1026,9 @@ def main() -> int:
         },
         "cpu_baseline": baseline,
         "read_probe_gbs": round(probe, 1),
+        "launch_floor_us": floor["launch_floor_us"],
+        "dependent_launch_us": floor["dependent_launch_us"],
+        "launch_costs": floor,
         "sweep": products["sweep"],
         "single_product": products["single"],
         "lm_decode": lm,

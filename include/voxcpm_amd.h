@@ -90,7 +90,14 @@ int vx_q8_unpack_bf16(const void* packed, size_t n, size_t k, uint16_t* out,
 /* Split-reduction scratch of the products: partial sums and counters that
  * are zero between products (the products leave them so), like
  * Bf16Gemm::State's partials/counters (gemm.cpp:95-98). One scratch serves
- * one stream at a time. */
+ * one stream at a time. vx_scratch_create(max_m, max_n) (max_m <= 128)
+ * holds 16 max_m max_n floats of partial sums: the splits of products up
+ * to max_m x max_n. Products of more than 128 rows split k only on grids
+ * of few tiles and use at most VX_PREFILL_SPLIT_FLOATS floats (the split
+ * is skipped when the scratch holds fewer than it needs): a scratch of
+ * 16 max_m max_n >= VX_PREFILL_SPLIT_FLOATS serves all of them, e.g.
+ * vx_scratch_create(128, 1536). */
+#define VX_PREFILL_SPLIT_FLOATS (3u << 20)
 typedef struct vx_scratch vx_scratch;
 int vx_scratch_create(vx_scratch** scratch, size_t max_m, size_t max_n);
 void vx_scratch_destroy(vx_scratch* scratch);
@@ -113,11 +120,16 @@ int vx_q8_linear_bf16(const uint16_t* x, const void* packed, uint16_t* y,
  * capture, tight serving loops, harnesses that forbid hipMalloc): no
  * counterpart in the reference. It allocates nothing and takes no
  * vx_scratch: the k-split partial sums of products of more than 128 rows
- * live in a static 12 MiB device array per GPU (held until the process
- * ends). Same arguments and results as vx_q8_linear with a scratch, bit for
- * bit; VX_BAD_ARG when a product's split would need more than the array
- * holds. Every call on one GPU shares that GPU's array, so calls that
- * overlap on one GPU (two streams at once) race. */
+ * live in a static device array of VX_PREFILL_SPLIT_FLOATS floats (12 MiB)
+ * per GPU, held until the process ends; the product plans never split
+ * into more than that. Same arguments as vx_q8_linear; its results are bit
+ * for bit vx_q8_linear's with a scratch of at least VX_PREFILL_SPLIT_FLOATS
+ * partial-sum floats (vx_scratch_create(128, 1536) or larger), with which
+ * both take the same split; a smaller scratch may split k less and round
+ * differently. Its first call on a GPU looks up the array's address there
+ * (hipGetSymbolAddress), which may happen under stream capture. Every call
+ * on one GPU shares that GPU's array, so calls that overlap on one GPU (two
+ * streams at once) race. */
 int vx_q8_linear_noalloc(const uint16_t* x, const void* packed, float* y,
                          size_t m, size_t k, size_t n, int accumulate,
                          void* stream);

@@ -53,6 +53,13 @@ int vx_q8_linear_gemm(const uint16_t* x, const void* packed, float* y,
 int vx_q8_plan(size_t m, size_t k, size_t n, vx_scratch* scratch,
                int32_t* out7);
 
+/* The plan of an m x k x n product of more than 128 rows (the expanded
+ * path) with this scratch: out4 = {kernel (0 the tiled kernel, 1 the
+ * 32 x 32 MFMA kernel), rows per tile, columns per tile, splits along k}.
+ * Counterpart of the plan gemm.cpp:259-313 picks between hipBLASLt and
+ * its chunked products. */
+int vx_q8_prefill_plan(size_t m, size_t k, size_t n, vx_scratch* scratch, int32_t* out4);
+
 /* float32 [n] -> bf16 bits [n] through the conversion the fused kernels use
  * for their bf16 activations (gfx950's v_cvt_pk_bf16_f32), so that tests can
  * check it bit for bit against the reference's rounding

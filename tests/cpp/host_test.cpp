@@ -19,6 +19,7 @@
 #include "../../oracle/oracle.h"
 #include "../../voxcpm_amd/host/dit_sampler.hpp"
 #include "voxcpm_amd.h"
+#include "voxcpm_amd_internal.h"
 
 namespace vc = gufo::models::voxcpm;
 
@@ -199,6 +200,47 @@ void TestLinear(std::size_t in, std::size_t out, Random& rng,
     threw = true;
   }
   Report(threw, "unsupported weight format throws GpuError");
+}
+
+/// Bf16Gemm::Linear of 129 x 2048 x 2048 takes the expanded path's plan
+/// that splits k (its grid has few tiles): the operator's scratch holds the
+/// split's partial sums, as the reference's State owns its partials
+/// (gemm.cpp:95-98). The result is bit for bit vx_q8_linear's with a
+/// scratch that size, whose plan splits (and without one would not), and
+/// within 1e-4 of the expanded arithmetic (products_test.cpp:301-309).
+void TestPrefillSplit(Random& rng, hipStream_t stream) {
+  const std::size_t rows = 129, in = 2048, out = 2048;
+  const auto blocks = Weights(out, in, rng);
+  const auto packed = Pack(blocks, out, in);
+  const auto x = Activations(rows, in, rng, 2.0);
+  const auto x_device = Upload(x);
+  vx_scratch* scratch = nullptr;
+  vc::CheckVx(vx_scratch_create(&scratch, 128, VX_PREFILL_SPLIT_FLOATS / (16 * 128)),
+              "scratch");
+  std::int32_t plan[4] = {0, 0, 0, 0};
+  std::int32_t bare[4] = {0, 0, 0, 0};
+  vc::CheckVx(vx_q8_prefill_plan(rows, in, out, scratch, plan), "plan");
+  vc::CheckVx(vx_q8_prefill_plan(rows, in, out, nullptr, bare), "plan");
+  Report(plan[3] > 1 && bare[3] == 1,
+         "prefill 129 x 2048 x 2048 plan: " + std::to_string(plan[3]) +
+             " splits with the scratch, " + std::to_string(bare[3]) + " without");
+  vc::DeviceBuffer<float> y(rows * out);
+  vc::DeviceBuffer<float> reference(rows * out);
+  vc::Bf16Gemm gemm(nullptr, stream);
+  gemm.Linear(x_device.get(), vc::Matrix{vc::WeightFormat::kQ8Panels, packed.get()}, y.get(),
+              rows, in, out, false);
+  vc::CheckVx(vx_q8_linear(x_device.get(), packed.get(), reference.get(), rows, in, out, 0,
+                           scratch, stream),
+              "vx_q8_linear");
+  vc::Check(hipStreamSynchronize(stream), "sync");
+  vx_scratch_destroy(scratch);
+  const auto result = Download(y.get(), y.size());
+  const auto expected = Download(reference.get(), reference.size());
+  Report(std::memcmp(result.data(), expected.data(), result.size() * sizeof(float)) == 0,
+         "Bf16Gemm::Linear 129 x 2048 x 2048 equals the split plan's product bit for bit");
+  const double worst = ExpandedError(result, x, blocks, nullptr, rows, in, out);
+  Report(worst <= 1e-4, "Bf16Gemm::Linear 129 x 2048 x 2048 (split k): worst " +
+                            Scientific(worst));
 }
 
 /// Bf16Gemm::Linear on bf16 weights, as panels and as rows, at rows 1, 22,
@@ -572,6 +614,7 @@ int main() {
     TestLinear(1024, 2560, rng, stream);
     TestLinear(4096, 1024, rng, stream);
     TestLinearBf16(1024, 2560, rng, stream);
+    TestPrefillSplit(rng, stream);
     TestDitSampler(rng);
     TestForwardStack(rng, stream);
     vc::Check(hipStreamDestroy(stream), "stream");

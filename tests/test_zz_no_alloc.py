@@ -4,6 +4,9 @@ with a caller's scratch: bit for bit on two calls in a row, the second
 smaller, each also within the reference's 1e-4 of the expanded arithmetic
 in double (products_test.cpp:279-310); a skinny call (m <= 128) delegates
 to the split-free plan."""
+import pathlib
+import sys
+
 import numpy as np
 import pytest
 import torch
@@ -50,3 +53,17 @@ def test_noalloc_product_matches_scratch_product(vx, oracle, cuda, stream):
             assert expanded_error(got.cpu().numpy(), x_host, blocks, oracle) <= 1e-4
         else:
             assert oracle.q8_check(got.cpu().numpy(), x_host, blocks) <= 1e-5
+
+
+def test_noalloc_first_call_under_graph_capture(cuda):
+    """The advertised use: the first call on a GPU (which looks up the
+    static array's address) happens under HIP graph capture, and every
+    replay equals vx_q8_linear bit for bit (tests/noalloc_capture.py, in a
+    process of its own so that no earlier call has looked the address up)."""
+    import subprocess
+    script = pathlib.Path(__file__).resolve().parent / "noalloc_capture.py"
+    result = subprocess.run([sys.executable, "-u", str(script)], capture_output=True, text=True,
+                            timeout=180)
+    print(result.stdout)
+    assert result.returncode == 0, result.stdout + result.stderr
+    assert "capture ok" in result.stdout

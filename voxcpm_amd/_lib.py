@@ -132,6 +132,7 @@ _SIGNATURES = {
     "vx_q8_linear_gemm": ([c_void_p, c_void_p, c_void_p, c_size, c_size, c_size,
                            c_int, c_int, c_void_p, c_void_p], c_int),
     "vx_q8_plan": ([c_size, c_size, c_size, c_void_p, c_void_p], c_int),
+    "vx_q8_prefill_plan": ([c_size, c_size, c_size, c_void_p, c_void_p], c_int),
     "vx_bf16_packed_bytes": ([c_size, c_size], c_size),
     "vx_bf16_pack": ([c_void_p, c_size, c_size, c_void_p, c_void_p], c_int),
     "vx_bf16_unpack": ([c_void_p, c_size, c_size, c_void_p, c_void_p], c_int),

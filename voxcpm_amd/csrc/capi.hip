@@ -309,4 +309,24 @@ int vx_q8_plan(size_t m, size_t k, size_t n, vx_scratch* scratch,
   return vx::Succeed();
 }
 
+int vx_q8_prefill_plan(size_t m, size_t k, size_t n, vx_scratch* scratch, int32_t* out4) {
+  if (out4 == nullptr || m <= vx::kExactRows || k % 32 != 0 || k == 0 || n == 0)
+    return vx::Fail(VX_BAD_ARG, "vx_q8_prefill_plan: bad arguments");
+  const std::size_t floats = scratch != nullptr ? scratch->partial_floats : 0;
+  if (vx::UseGemm(m, n)) {
+    const vx::GemmPlan plan = vx::PlanGemm(m, k, n, floats);
+    out4[0] = 1;
+    out4[1] = plan.bm;
+    out4[2] = plan.bn;
+    out4[3] = plan.splits;
+  } else {
+    const vx::TiledPlan plan = vx::PlanTiled(m, k, n, floats);
+    out4[0] = 0;
+    out4[1] = plan.bm;
+    out4[2] = 128;  // the tiled kernel's columns per tile
+    out4[3] = plan.splits;
+  }
+  return vx::Succeed();
+}
+
 }  // extern "C"

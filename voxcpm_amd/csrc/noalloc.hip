@@ -15,7 +15,6 @@
 #include <array>
 #include <cstdint>
 #include <mutex>
-#include <string>
 
 #include "common.hpp"
 #include "products.hpp"
@@ -25,6 +24,7 @@
 /// store splits x m x n partial sums here. 12 MiB per device: every default
 /// plan keeps its splits' partial sums within it.
 constexpr std::size_t kScratchFloats = vx::kMaxSplitFloats;
+static_assert(kScratchFloats >= VX_PREFILL_SPLIT_FLOATS, "the array holds every split");
 
 static __device__ __align__(256) float scratch[kScratchFloats];
 
@@ -69,20 +69,9 @@ int vx_q8_linear_noalloc(const uint16_t* x, const void* packed, float* y, size_t
   VX_TRY(vx::CheckProduct(x, packed, y, m, k, n, "vx_q8_linear_noalloc"));
   if (m <= vx::kExactRows)  // these plans split nothing over workgroups
     return vx_q8_linear(x, packed, y, m, k, n, accumulate, nullptr, stream);
-  // The partial sums of the split the planner picks with unlimited room
-  // must fit the array.
-  std::size_t need = 0;
-  if (vx::UseGemm(m, n)) {
-    const vx::GemmPlan plan = vx::PlanGemm(m, k, n, SIZE_MAX);
-    need = plan.splits > 1 ? static_cast<std::size_t>(plan.splits) * m * n : 0;
-  } else {
-    const vx::TiledPlan plan = vx::PlanTiled(m, k, n, SIZE_MAX);
-    need = plan.splits > 1 ? static_cast<std::size_t>(plan.splits) * m * n : 0;
-  }
-  if (need > kScratchFloats)
-    return vx::Fail(VX_BAD_ARG, "vx_q8_linear_noalloc: the product's split needs " +
-                                    std::to_string(need) + " floats of scratch, the static " +
-                                    "scratch holds " + std::to_string(kScratchFloats));
+  // The planners keep every split within kMaxSplitFloats floats whatever
+  // room they are given, which the array holds: they pick here the split
+  // they pick for a vx_scratch of at least that many floats.
   float* address = nullptr;
   VX_TRY(ScratchAddress(&address));
   if (vx::UseGemm(m, n))

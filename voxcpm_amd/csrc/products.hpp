@@ -9,6 +9,7 @@
 
 #include "common.hpp"
 #include "q8.hpp"
+#include "voxcpm_amd.h"
 
 namespace vx {
 
@@ -67,7 +68,7 @@ int RunEngineTuned(const Bf16* x, const void* w, float* y, std::size_t m, std::s
 /// Most floats of split partial sums any default plan uses (12 MiB): the
 /// products' k splits stay within it, so that a static scratch of this size
 /// serves every product (vx_q8_linear_noalloc).
-constexpr std::size_t kMaxSplitFloats = std::size_t{3} << 20;
+constexpr std::size_t kMaxSplitFloats = VX_PREFILL_SPLIT_FLOATS;
 
 /// Whether an m > 128 product takes the 32 x 32 MFMA kernel (q8_gemm.hip)
 /// rather than the tiled kernel (q8_tiled.hip), which measured faster on the

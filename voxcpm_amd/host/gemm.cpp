@@ -37,8 +37,13 @@ struct Bf16Gemm::State {
   }
 
   vx_scratch* Reserve(std::size_t want_rows, std::size_t want_out) {
-    if (want_rows > 128)
-      return scratch;  // the expanded path needs no split scratch
+    if (want_rows > 128) {
+      // The expanded path splits k on grids of few tiles into at most
+      // VX_PREFILL_SPLIT_FLOATS floats of partial sums: a scratch of
+      // 128 x (that / (16 x 128)) holds all of them.
+      want_rows = 128;
+      want_out = VX_PREFILL_SPLIT_FLOATS / (16 * 128);
+    }
     if (scratch != nullptr && want_rows <= rows && want_out <= out)
       return scratch;
     rows = std::max(rows, want_rows);
