@@ -210,9 +210,10 @@ def test_products_beyond_32_rows(vx, oracle, cuda, stream, rows):
 
 
 @pytest.mark.parametrize("rows,k,n", [(100, 1024, 16400), (128, 2048, 16384)])
-def test_tiled_exact_products(vx, oracle, cuda, stream, rows, k, n):
-    """More than 64 rows over wide outputs take the LDS-tiled kernel; it
-    keeps the exact per-block arithmetic (ragged rows and columns, and
+def test_wide_products_beyond_64_rows(vx, oracle, cuda, stream, rows, k, n):
+    """More than 64 rows over wide outputs take blocks of up to 64 rows,
+    each staged per wave, with the exact per-block arithmetic (ragged rows
+    and columns, a tile count that is not a multiple of 8, and
     accumulation)."""
     rng = synth.Rng(77, rows + n)
     blocks = reference_weights(rng, n, k)

@@ -25,7 +25,6 @@ constexpr std::size_t kExactRows = 128;
 /// also split k over workgroups.
 struct ProductPlan {
   bool engine = false;
-  bool tiled = false;  // default plans of more than 32 rows: RunTiled, exact
   int mt = 1;
   int rg = 1;
   int waves = 4;
@@ -52,7 +51,7 @@ ProductPlan PlanSkinny(std::size_t m, std::size_t k, std::size_t n,
 
 /// Launches the product (m <= 128) with `plan`: Q8_0 panels with the exact
 /// arithmetic, or bf16 weights (panels, or rows [n][k] for m <= 32) on the
-/// engine and tiled plans.
+/// engine plans.
 int RunSkinny(const Bf16* x, const void* w, float* y, Bf16* y_bf16,
               std::size_t m, std::size_t k, std::size_t n, bool accumulate,
               const ProductPlan& plan, float* partials, unsigned* counters,
@@ -100,10 +99,9 @@ int RunGemm(const Bf16* x, const void* w, float* y, Bf16* y_bf16, std::size_t m,
             std::size_t n, bool accumulate, bool bf16_weights, float* partials,
             std::size_t partial_floats, hipStream_t stream, int shape = -1, int splits = 1);
 
-/// What the tiled kernel multiplies: Q8_0 panels with the exact per-block
-/// arithmetic, Q8_0 panels expanded to bf16(scale * q) (the reference's
-/// arithmetic beyond 128 rows), or bf16 panels.
-enum class TiledMode : int { kQ8Exact = 0, kQ8Expanded = 1, kBf16 = 2 };
+/// What the tiled kernel multiplies: Q8_0 panels expanded to bf16(scale * q)
+/// (the reference's arithmetic beyond 128 rows) or bf16 panels.
+enum class TiledMode : int { kQ8Expanded = 1, kBf16 = 2 };
 
 /// VX_OK, or VX_BAD_ARG (with the message) for product arguments the
 /// kernels cannot take: null pointers, m, n or k zero, k not a multiple of
@@ -125,7 +123,7 @@ struct TiledPlan {
 /// `partial_floats` floats of partial sums.
 TiledPlan PlanTiled(std::size_t m, std::size_t k, std::size_t n, std::size_t partial_floats);
 
-/// Launches the LDS-tiled product (q8_tiled.hip; meant for m > 32). Small
+/// Launches the LDS-tiled product (q8_tiled.hip; m > 128). Small
 /// grids split k over workgroups when `partials` holds partial_floats >=
 /// 2 m n floats (a second launch adds the splits in order).
 int RunTiled(const Bf16* x, const void* w, float* y, Bf16* y_bf16, std::size_t m,

@@ -179,14 +179,13 @@ constexpr int EngineThreads(int mt, int rg) {
   return (mt <= 2 && rg <= 2) ? 1024 : 512;
 }
 
-/// Row-major activations of up to 32 rows are staged per wave through LDS
-/// (below); more rows are loaded straight into the MFMA operands.
+/// Row-major activations of up to 64 rows (a workgroup's row block) are
+/// staged per wave through LDS (below); more rows are loaded straight into
+/// the MFMA operands.
 __host__ __device__ constexpr bool StagesRows(ASource source, int mt) {
-  return source == ASource::kRowMajor && mt <= 2;
+  return source == ASource::kRowMajor && mt <= 4;
 }
 
-/// Floats of one wave's private row-staging region: PW pairs of 16 MT rows
-/// x 128 bytes.
 /// Floats of a wave's row-staging region: one pair's 16 MT rows x 64
 /// columns of bf16 (the pairs of a pass are staged one after another).
 __host__ __device__ constexpr int StageFloats(int mt) {
@@ -421,9 +420,9 @@ __device__ __forceinline__ void EngineBody(const TileArgs& a, int block_id, int 
   if constexpr (kPre)
     __builtin_amdgcn_s_waitcnt(0);
   // The workgroup's first activation row: its 16-row tile of a fragment
-  // source, or the first row of its block for one-tile row-major
-  // activations (the block's rows are then the tile's, at most 16).
-  constexpr bool kBlockTile = SRC == ASource::kRowMajor && MT == 1;
+  // source, or the first row of its block for row-major activations (the
+  // block's rows then lie in the MT tiles from there).
+  constexpr bool kBlockTile = SRC == ASource::kRowMajor;
   const int row_base = kBlockTile ? row_lo : 16 * tile_base;
   const int k_blocks = a.k / 32;
 

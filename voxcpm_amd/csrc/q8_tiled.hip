@@ -1,16 +1,12 @@
-// Q8_0 (or bf16) x bfloat16 products of more than 32 activation rows on
-// gfx950's matrix cores: LDS-tiled, BM activation rows x 128 weight rows per
-// workgroup, 64 columns (one panel pair, two Q8_0 blocks) per step.
+// Q8_0 (or bf16) x bfloat16 products of more than 128 activation rows on
+// gfx950's matrix cores (the smaller, latency-bound prefill shapes):
+// LDS-tiled, BM activation rows x 128 weight rows per workgroup, 64
+// columns (one panel pair, two Q8_0 blocks) per step.
 //
-// Two arithmetics, as the reference dispatches them (gemm.cpp:259-313):
-//  - exact (up to 128 rows, kernels/wmma_products.hip:192-215): the int8
-//    values become bf16 exactly, each 32-column block is one
-//    v_mfma_f32_16x16x32_bf16 from zero, and acc = fmaf(f16 scale, block
-//    sum, acc) walks the blocks in k order;
-//  - expanded (more rows, gemm.cpp:305-312 with
-//    kernels/wmma_products.hip:94-112): every weight becomes
-//    bf16_rne(f32(f16 scale) * q) once per workgroup and step, and the MFMAs
-//    accumulate over all of k in float32.
+// The arithmetic is the reference's expansion beyond 128 rows (gemm.cpp:
+// 305-312 with kernels/wmma_products.hip:94-112): every weight becomes
+// bf16_rne(f32(f16 scale) * q) once per workgroup and step, and the MFMAs
+// accumulate over all of k in float32.
 // bf16 panels (kernels/wmma_products.hip:210-213, the WmmaBf16 products)
 // take the expanded path's MFMA accumulation with the weights copied as
 // they are.
@@ -38,7 +34,6 @@ namespace {
 using q8::AsBf16x8;
 using q8::Bf16x8;
 using q8::F32x4;
-using q8::Int8x8ToBf16;
 using q8::kUnitBytes;
 using q8::kValueBytes;
 using q8::Mfma16x16x32;
@@ -102,11 +97,11 @@ struct TileShape {
   static constexpr int kMinBlocks = MINB;
 };
 
-/// MODE: TiledMode (products.hpp) as an int: 0 Q8_0 exact, 1 Q8_0
-/// expanded, 2 bf16 panels.
+/// MODE: TiledMode (products.hpp) as an int: 1 Q8_0 expanded, 2 bf16
+/// panels.
 template<class T, int MODE>
 __global__ __launch_bounds__(T::kThreads, T::kMinBlocks) void TiledKernel(TiledArgs a) {
-  constexpr bool EXACT = MODE == 0;
+  static_assert(MODE == 1 || MODE == 2, "expanded Q8_0 or bf16 panels");
   constexpr bool BF16 = MODE == 2;
   constexpr int kUnit = BF16 ? q8::kBf16UnitBytes : kUnitBytes;
   constexpr int BM = T::kBm;
@@ -117,7 +112,6 @@ __global__ __launch_bounds__(T::kThreads, T::kMinBlocks) void TiledKernel(TiledA
   constexpr int D = T::kD;
   __shared__ uint4 lds_a[2][BM * kRowChunks];
   __shared__ uint4 lds_b[2][kTileN * kRowChunks];
-  __shared__ float lds_s[EXACT ? 2 : 1][EXACT ? kTileN * 2 : 1];
   const int tid = static_cast<int>(threadIdx.x);
   const int lane = tid % kWave;
   const int wave = tid / kWave;
@@ -189,13 +183,6 @@ __global__ __launch_bounds__(T::kThreads, T::kMinBlocks) void TiledKernel(TiledA
       if constexpr (BF16) {
         first = s.w[u];
         second = s.w2[u];
-      } else if constexpr (EXACT) {
-        first = __builtin_bit_cast(uint4, Int8x8ToBf16(s.w[u].x, s.w[u].y));
-        second = __builtin_bit_cast(uint4, Int8x8ToBf16(s.w[u].z, s.w[u].w));
-        if (octet == 0) {
-          lds_s[buffer][2 * row] = s0;
-          lds_s[buffer][2 * row + 1] = s1;
-        }
       } else {
         first = Expand(s.w[u].x, s.w[u].y, s0);
         second = Expand(s.w[u].z, s.w[u].w, s1);
@@ -215,11 +202,9 @@ __global__ __launch_bounds__(T::kThreads, T::kMinBlocks) void TiledKernel(TiledA
       acc[i][j] = F32x4{0.0F, 0.0F, 0.0F, 0.0F};
 
   const auto compute = [&](int buffer) {
-    const F32x4 zero{0.0F, 0.0F, 0.0F, 0.0F};
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
       Bf16x8 af[kMi], bf[4];
-      float scale[4];
 #pragma unroll
       for (int i = 0; i < kMi; ++i)
         af[i] = AsBf16x8(
@@ -229,22 +214,12 @@ __global__ __launch_bounds__(T::kThreads, T::kMinBlocks) void TiledKernel(TiledA
       for (int j = 0; j < 4; ++j) {
         const int row = 64 * wn + 16 * j + r16;
         bf[j] = AsBf16x8(lds_b[buffer][row * kRowChunks + 4 * h + octet]);
-        if constexpr (EXACT)
-          scale[j] = lds_s[buffer][2 * row + h];
       }
 #pragma unroll
       for (int i = 0; i < kMi; ++i)
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          if constexpr (EXACT) {
-            const F32x4 sum = Mfma16x16x32(af[i], bf[j], zero);
-#pragma unroll
-            for (int e = 0; e < 4; ++e)
-              acc[i][j][e] = fmaf(scale[j], sum[e], acc[i][j][e]);
-          } else {
-            acc[i][j] = Mfma16x16x32(af[i], bf[j], acc[i][j]);
-          }
-        }
+        for (int j = 0; j < 4; ++j)
+          acc[i][j] = Mfma16x16x32(af[i], bf[j], acc[i][j]);
     }
   };
 
@@ -458,9 +433,6 @@ int RunTiled(const Bf16* x, const void* w, float* y, Bf16* y_bf16, std::size_t m
   args.pairs_per_split = (args.pairs + args.splits - 1) / args.splits;
   args.partials = partials;
   switch (mode) {
-    case TiledMode::kQ8Exact:
-      bm == 64 ? Launch<Small, 0>(args, stream) : Launch<Large, 0>(args, stream);
-      return LaunchStatus("q8 tiled product");
     case TiledMode::kQ8Expanded:
       bm == 64 ? Launch<Small, 1>(args, stream) : Launch<Large, 1>(args, stream);
       return LaunchStatus("q8 expanded product");
