@@ -40,11 +40,17 @@ int vx_q8_linear_engine(const uint16_t* x, const void* packed, float* y,
  * forced plan: tile `shape` 0 (256 x 256, one step prefetched), 1
  * (128 x 256), 2 (128 x 128), 3 (256 x 128), 4 (256 x 256, two steps),
  * 5 (128 x 64), k split over `splits` workgroups (the scratch must hold
- * splits m n floats when splits > 1). VX_UNSUPPORTED for other shapes. The
- * plan search behind vx_q8_linear's prefill plans. */
+ * splits m n floats when splits > 1); shape 6 is the skinny engine in
+ * blocks of 64 rows (no split). VX_UNSUPPORTED for other shapes. The plan
+ * search behind vx_q8_linear's prefill plans. */
 int vx_q8_linear_gemm(const uint16_t* x, const void* packed, float* y,
                       size_t m, size_t k, size_t n, int shape, int splits,
                       vx_scratch* scratch, void* stream);
+
+/* vx_q8_linear_gemm for bf16 panels (vx_bf16_pack's layout). */
+int vx_bf16_linear_gemm(const uint16_t* x, const void* packed, float* y,
+                        size_t m, size_t k, size_t n, int shape, int splits,
+                        vx_scratch* scratch, void* stream);
 
 /* The default plan of an m x k x n product (m <= 128):
  * out7 = {activation tiles, row groups per workgroup, waves per workgroup,
@@ -55,7 +61,8 @@ int vx_q8_plan(size_t m, size_t k, size_t n, vx_scratch* scratch,
 
 /* The plan of an m x k x n product of more than 128 rows (the expanded
  * path) with this scratch: out4 = {kernel (0 the tiled kernel, 1 the
- * 32 x 32 MFMA kernel), rows per tile, columns per tile, splits along k}.
+ * 32 x 32 MFMA kernel, 2 the skinny engine in blocks of 64 rows), rows per
+ * tile, columns per tile, splits along k}.
  * Counterpart of the plan gemm.cpp:259-313 picks between hipBLASLt and
  * its chunked products. */
 int vx_q8_prefill_plan(size_t m, size_t k, size_t n, vx_scratch* scratch, int32_t* out4);

@@ -19,13 +19,13 @@ from voxcpm_amd import _lib, ops, synth  # noqa: E402
 
 def main() -> int:
     device = torch.device("cuda:0")
-    m, k, n = 256, 2048, 2048  # the tiled plan splits k four ways here
+    m, k, n = 256, 2048, 4096  # the tiled plan splits k two ways here
     rng = synth.Rng(202, m + n)
     blocks = synth.q8_blocks(rng, n, k)
     packed = ops.q8_pack(torch.from_numpy(blocks).to(device), n, k)
     x = torch.from_numpy(synth.activations(rng, m, k).view(np.int16)).to(device).view(
         torch.bfloat16)
-    scratch = ops.Scratch(128, 1536)
+    scratch = ops.Scratch(128, 1536)  # VX_PREFILL_SPLIT_FLOATS partial sums
     plan = (ctypes.c_int32 * 4)()
     _lib.check(_lib.lib().vx_q8_prefill_plan(m, k, n, scratch.handle, plan))
     assert plan[3] > 1, f"expected a split plan, got {list(plan)}"

@@ -4,6 +4,7 @@ with a caller's scratch: bit for bit on two calls in a row, the second
 smaller, each also within the reference's 1e-4 of the expanded arithmetic
 in double (products_test.cpp:279-310); a skinny call (m <= 128) delegates
 to the split-free plan."""
+import ctypes
 import pathlib
 import sys
 
@@ -35,9 +36,13 @@ def test_noalloc_product_matches_scratch_product(vx, oracle, cuda, stream):
     function = noalloc()
     scratch = vx.Scratch(128, 16384)
     stream_handle = torch.cuda.current_stream().cuda_stream
-    # Both tiled calls split k (4 splits of 64 row tiles, then 4 of 24).
-    for m, k, n in [(256, 2048, 2048), (129, 1024, 1024), (22, 1024, 4096)]:
+    # Both tiled calls split k (2 splits of 128 row tiles, then 4 of 96).
+    for m, k, n in [(256, 2048, 4096), (160, 2048, 4096), (22, 1024, 4096)]:
         print(f"noalloc product m={m} k={k} n={n}", flush=True)
+        if m > 128:
+            plan = (ctypes.c_int32 * 4)()
+            _lib.check(_lib.lib().vx_q8_prefill_plan(m, k, n, scratch.handle, plan))
+            assert plan[0] == 0 and plan[3] > 1, f"expected a split tiled plan: {list(plan)}"
         rng = synth.Rng(101, m + n)
         blocks = synth.q8_blocks(rng, n, k)
         packed = vx.q8_pack(torch.from_numpy(blocks).to(cuda), n, k)

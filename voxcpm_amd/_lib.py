@@ -131,6 +131,8 @@ _SIGNATURES = {
                              c_int, c_int, c_int, c_int, c_void_p], c_int),
     "vx_q8_linear_gemm": ([c_void_p, c_void_p, c_void_p, c_size, c_size, c_size,
                            c_int, c_int, c_void_p, c_void_p], c_int),
+    "vx_bf16_linear_gemm": ([c_void_p, c_void_p, c_void_p, c_size, c_size, c_size,
+                             c_int, c_int, c_void_p, c_void_p], c_int),
     "vx_q8_plan": ([c_size, c_size, c_size, c_void_p, c_void_p], c_int),
     "vx_q8_prefill_plan": ([c_size, c_size, c_size, c_void_p, c_void_p], c_int),
     "vx_bf16_packed_bytes": ([c_size, c_size], c_size),

@@ -113,6 +113,9 @@ int Product(const uint16_t* x, const void* packed, float* y, uint16_t* y_bf16,
             size_t m, size_t k, size_t n, int accumulate, vx_scratch* scratch,
             int rg, int waves, int splits, void* stream,
             vx::q8::Weights kind = vx::q8::Weights::kQ8) {
+  if (vx::UseRowBlocks(m, k, n))
+    return vx::RunRowBlocks(x, packed, y, y_bf16, m, k, n, accumulate != 0,
+                            kind != vx::q8::Weights::kQ8, vx::Stream(stream));
   if (m > vx::kExactRows && vx::UseGemm(m, n))
     return vx::RunGemm(x, packed, y, y_bf16, m, k, n, accumulate != 0,
                        kind != vx::q8::Weights::kQ8,
@@ -256,7 +259,23 @@ int vx_q8_linear_gemm(const uint16_t* x, const void* packed, float* y, size_t m,
   VX_TRY(CheckProduct(x, packed, y, m, k, n, "vx_q8_linear_gemm"));
   if (m <= vx::kExactRows || shape < 0)
     return vx::Fail(VX_BAD_ARG, "vx_q8_linear_gemm: more than 128 rows and a shape");
+  if (shape == 6)  // the skinny engine in blocks of 64 rows
+    return vx::RunRowBlocks(x, packed, y, nullptr, m, k, n, false, false, vx::Stream(stream));
   return vx::RunGemm(x, packed, y, nullptr, m, k, n, false, false,
+                     scratch != nullptr ? scratch->partials : nullptr,
+                     scratch != nullptr ? scratch->partial_floats : 0, vx::Stream(stream),
+                     shape, splits);
+}
+
+/* Testing and tuning entry: vx_q8_linear_gemm for bf16 panels. */
+int vx_bf16_linear_gemm(const uint16_t* x, const void* packed, float* y, size_t m, size_t k,
+                        size_t n, int shape, int splits, vx_scratch* scratch, void* stream) {
+  VX_TRY(CheckProduct(x, packed, y, m, k, n, "vx_bf16_linear_gemm"));
+  if (m <= vx::kExactRows || shape < 0)
+    return vx::Fail(VX_BAD_ARG, "vx_bf16_linear_gemm: more than 128 rows and a shape");
+  if (shape == 6)
+    return vx::RunRowBlocks(x, packed, y, nullptr, m, k, n, false, true, vx::Stream(stream));
+  return vx::RunGemm(x, packed, y, nullptr, m, k, n, false, true,
                      scratch != nullptr ? scratch->partials : nullptr,
                      scratch != nullptr ? scratch->partial_floats : 0, vx::Stream(stream),
                      shape, splits);
@@ -313,7 +332,12 @@ int vx_q8_prefill_plan(size_t m, size_t k, size_t n, vx_scratch* scratch, int32_
   if (out4 == nullptr || m <= vx::kExactRows || k % 32 != 0 || k == 0 || n == 0)
     return vx::Fail(VX_BAD_ARG, "vx_q8_prefill_plan: bad arguments");
   const std::size_t floats = scratch != nullptr ? scratch->partial_floats : 0;
-  if (vx::UseGemm(m, n)) {
+  if (vx::UseRowBlocks(m, k, n)) {
+    out4[0] = 2;
+    out4[1] = 64;
+    out4[2] = static_cast<int32_t>(16 * (n > 4096 ? 2 : 1));  // columns per workgroup
+    out4[3] = 1;
+  } else if (vx::UseGemm(m, n)) {
     const vx::GemmPlan plan = vx::PlanGemm(m, k, n, floats);
     out4[0] = 1;
     out4[1] = plan.bm;

@@ -57,6 +57,18 @@ int RunSkinny(const Bf16* x, const void* w, float* y, Bf16* y_bf16,
               const ProductPlan& plan, float* partials, unsigned* counters,
               hipStream_t stream, q8::Weights kind = q8::Weights::kQ8);
 
+/// Whether an m > 128 product runs on the skinny engine in blocks of 64
+/// rows (RunRowBlocks) rather than the tiled or the 32 x 32 MFMA kernel:
+/// the smaller prefill products, where those kernels' grids are few tiles.
+bool UseRowBlocks(std::size_t m, std::size_t k, std::size_t n);
+
+/// More than 128 rows on the skinny engine in blocks of 64 rows, each
+/// staged per wave: Q8_0 panels with the reference's expanded arithmetic
+/// (bf16(scale * q) per weight, one float32 sum over k; gemm.cpp:305-312),
+/// or bf16 panels. No scratch.
+int RunRowBlocks(const Bf16* x, const void* w, float* y, Bf16* y_bf16, std::size_t m,
+                 std::size_t k, std::size_t n, bool accumulate, bool bf16, hipStream_t stream);
+
 /// The engine on 17..32 row-major rows with a forced plan (tuning and
 /// tests): `rg` row groups per workgroup (1, 2, 4), `waves` waves (4, 8,
 /// 16), `pw` pairs per wave per pass (1, 2), `row_blocks` (1..4).

@@ -54,9 +54,17 @@ inline std::size_t Bf16PackedBytes(std::size_t n, std::size_t k) {
   return Groups(n) * Pairs(k) * kBf16UnitBytes;
 }
 
-/// Weight formats the product kernels read: Q8_0 panels, bf16 panels, or
-/// bf16 rows [n][k] as they come (row-major, k a multiple of 8).
-enum class Weights : int { kQ8 = 0, kBf16 = 1, kBf16Rows = 2 };
+/// Weight formats the product kernels read: Q8_0 panels (the exact per-block
+/// arithmetic), bf16 panels, bf16 rows [n][k] as they come (row-major, k a
+/// multiple of 8), or Q8_0 panels expanded on the fly to bf16(scale * q)
+/// with one float32 sum over k (the reference's arithmetic beyond 128
+/// rows, gemm.cpp:305-312).
+enum class Weights : int { kQ8 = 0, kBf16 = 1, kBf16Rows = 2, kQ8Expanded = 3 };
+
+/// Whether the weights are Q8_0 panels (either arithmetic).
+__host__ __device__ constexpr bool IsQ8(Weights w) {
+  return w == Weights::kQ8 || w == Weights::kQ8Expanded;
+}
 
 typedef __bf16 Bf16x8 __attribute__((ext_vector_type(8)));
 typedef float F32x4 __attribute__((ext_vector_type(4)));

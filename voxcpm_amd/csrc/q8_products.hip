@@ -440,9 +440,16 @@ TunedLauncher PickTuned(int rg, int pw, int waves, int m) {
   }
 }
 
-/// bf16 rows [n][k] are read by the staged engine only (m <= 32).
+/// bf16 rows [n][k] are read by the staged engine only (m <= 32); the
+/// expanded Q8_0 arithmetic runs in blocks of 64 rows only (mt = 4).
 EngineLauncher PickEngine(int mt, int rg, int pw, int m, int waves, q8::Weights kind) {
   switch (kind) {
+    case q8::Weights::kQ8Expanded:
+      if (mt != 4 || pw != 1 || waves * kWave != q8::EngineThreads(4, rg))
+        return nullptr;
+      return rg == 1   ? EngineJr<4, 1, 1, q8::Weights::kQ8Expanded>(m)
+             : rg == 2 ? EngineJr<4, 2, 1, q8::Weights::kQ8Expanded>(m)
+                       : nullptr;
     case q8::Weights::kQ8: return PickEngineFor<q8::Weights::kQ8>(mt, rg, pw, m, waves);
     case q8::Weights::kBf16: return PickEngineFor<q8::Weights::kBf16>(mt, rg, pw, m, waves);
     case q8::Weights::kBf16Rows:
@@ -458,6 +465,24 @@ EngineLauncher PickEngine(int mt, int rg, int pw, int m, int waves, q8::Weights 
 }
 
 constexpr int kMaxPairsInFlight = 4;
+
+/// Engine plan in blocks of at most 64 rows (four 16-row tiles), one or two
+/// row groups per workgroup of 8 waves.
+ProductPlan PlanRowBlocks(std::size_t m, std::size_t k, std::size_t n) {
+  ProductPlan plan;
+  plan.engine = true;
+  plan.mt = 4;
+  plan.row_blocks = static_cast<int>((m + 63) / 64);
+  const int groups = static_cast<int>(q8::Groups(n));
+  const int pairs = static_cast<int>(q8::Pairs(k));
+  plan.rg = groups <= 256 ? 1 : 2;
+  plan.tiles = (groups + plan.rg - 1) / plan.rg;
+  plan.waves = q8::EngineThreads(plan.mt, plan.rg) / kWave;
+  plan.splits = 1;
+  plan.pairs_per_split = pairs;
+  plan.pairs_per_wave = (pairs + plan.waves - 1) / plan.waves;
+  return plan;
+}
 
 /// Engine plan: up to 256 row groups take one per workgroup; wider products
 /// share each activation fragment over 2 or 4 row groups (fewer workgroups
@@ -475,18 +500,7 @@ ProductPlan PlanEngine(std::size_t m, std::size_t k, std::size_t n, q8::Weights 
     // (1024, 8192) 21.1 -> 10.6 us, (2048, 2048) 14.0 -> 7.6 us against the
     // engine on all 128 rows; (2048, 16384) 29.2 -> 28.8 us against the
     // LDS-tiled kernel.
-    plan.engine = true;
-    plan.mt = 4;
-    plan.row_blocks = static_cast<int>((m + 63) / 64);
-    const int groups = static_cast<int>(q8::Groups(n));
-    const int pairs = static_cast<int>(q8::Pairs(k));
-    plan.rg = groups <= 256 ? 1 : 2;
-    plan.tiles = (groups + plan.rg - 1) / plan.rg;
-    plan.waves = q8::EngineThreads(plan.mt, plan.rg) / kWave;
-    plan.splits = 1;
-    plan.pairs_per_split = pairs;
-    plan.pairs_per_wave = (pairs + plan.waves - 1) / plan.waves;
-    return plan;
+    return PlanRowBlocks(m, k, n);
   }
   plan.engine = true;
   const int groups = static_cast<int>(q8::Groups(n));
@@ -626,7 +640,7 @@ int RunSkinny(const Bf16* x, const void* w, float* y, Bf16* y_bf16,
     args.y_bf16 = y_bf16;
     args.accumulate = accumulate ? 1 : 0;
     launch(args, plan.tiles * plan.row_blocks, plan.waves, stream);
-    return LaunchStatus(kind == q8::Weights::kQ8 ? "q8 product" : "bf16 product");
+    return LaunchStatus(q8::IsQ8(kind) ? "q8 product" : "bf16 product");
   }
   if (kind != q8::Weights::kQ8)
     return Fail(VX_UNSUPPORTED, "split plans take Q8_0 panels only");
@@ -650,6 +664,27 @@ int RunSkinny(const Bf16* x, const void* w, float* y, Bf16* y_bf16,
   args.accumulate = accumulate ? 1 : 0;
   launch(args, plan, stream);
   return LaunchStatus("q8 product");
+}
+
+bool UseRowBlocks(std::size_t m, std::size_t k, std::size_t n) {
+  // Measured on MI355X against the tiled kernel (with its k split) and the
+  // 32 x 32 MFMA kernel, Q8_0 and bf16 panels alike: faster up to about
+  // 1.2 G multiply-adds (129 x 2048 x 2048 15.6 -> 9.2 us, 256 x 1024 x 4096
+  // 14.3 -> 10.9 us), and on 2048 x 2048 weights up to 512 rows (512 rows
+  // 21.0 -> 17.3 us); slower beyond (256 x 2048 x 8192 on a par, 1024 x 2048
+  // x 2048 24.7 -> 32.9 us), where each 64-row block re-reads the weights.
+  if (m <= kExactRows)
+    return false;
+  const double work = static_cast<double>(m) * static_cast<double>(k) * static_cast<double>(n);
+  return work <= 1.2e9 || (m <= 512 && k >= 2048 && k * n <= 2048 * 2048);
+}
+
+int RunRowBlocks(const Bf16* x, const void* w, float* y, Bf16* y_bf16, std::size_t m,
+                 std::size_t k, std::size_t n, bool accumulate, bool bf16, hipStream_t stream) {
+  if (m <= kExactRows)
+    return Fail(VX_UNSUPPORTED, "row-block product: more than 128 rows");
+  return RunSkinny(x, w, y, y_bf16, m, k, n, accumulate, PlanRowBlocks(m, k, n), nullptr,
+                   nullptr, stream, bf16 ? q8::Weights::kBf16 : q8::Weights::kQ8Expanded);
 }
 
 int RunEngineTuned(const Bf16* x, const void* w, float* y, std::size_t m, std::size_t k,

@@ -242,6 +242,18 @@ __device__ inline uint4 PackBf16x8(const float (&v)[8]) {
                PackBf16x2(v[4], v[5]), PackBf16x2(v[6], v[7])};
 }
 
+/// Eight int8 values (two little-endian dwords) times `scale`, each rounded
+/// to bf16 (nearest even, quiet NaNs) by v_cvt_pk_bf16_f32: the
+/// reference's expansion of a Q8_0 block beyond 128 rows
+/// (kernels/wmma_products.hip:94-112, gemm.cpp:305-312).
+__device__ inline uint4 Expand(std::uint32_t w0, std::uint32_t w1, float scale) {
+  const auto v = [&](std::uint32_t word, int byte) {
+    return scale * static_cast<float>(static_cast<std::int8_t>(word >> (8 * byte)));
+  };
+  return uint4{PackBf16x2(v(w0, 0), v(w0, 1)), PackBf16x2(v(w0, 2), v(w0, 3)),
+               PackBf16x2(v(w1, 0), v(w1, 1)), PackBf16x2(v(w1, 2), v(w1, 3))};
+}
+
 /// One float32 -> bf16 bits through the same instruction.
 __device__ inline Bf16 Bf16Fast(float value) {
   return static_cast<Bf16>(PackBf16x2(value, 0.0F) & 0xFFFFU);
@@ -426,7 +438,7 @@ __device__ __forceinline__ void EngineBody(const TileArgs& a, int block_id, int 
   const int row_base = kBlockTile ? row_lo : 16 * tile_base;
   const int k_blocks = a.k / 32;
 
-  constexpr int kUnit = WK == Weights::kQ8 ? kUnitBytes : kBf16UnitBytes;
+  constexpr int kUnit = IsQ8(WK) ? kUnitBytes : kBf16UnitBytes;
   // kHalfPairs: workgroup tile is half tile % 2 (rows 8 half .. + 7) of
   // the group pair tile / 2; the lane reads its row of its group's panel
   // (panel lane 16 octet + row holds the row's k chunk octet).
@@ -540,7 +552,7 @@ __device__ __forceinline__ void EngineBody(const TileArgs& a, int block_id, int 
       } else {
         const std::uint8_t* u = unit[r] + static_cast<std::size_t>(ok ? pair : 0) * kUnit;
         s.w[r] = *reinterpret_cast<const uint4*>(u + 16 * panel_lane);
-        if constexpr (WK == Weights::kQ8)
+        if constexpr (IsQ8(WK))
           s.scales[r] = *reinterpret_cast<const std::uint32_t*>(u + kValueBytes + 4 * panel_row);
         else
           s.w2[r] = *reinterpret_cast<const uint4*>(u + kBf16HalfBytes + 16 * panel_lane);
@@ -645,6 +657,22 @@ __device__ __forceinline__ void EngineBody(const TileArgs& a, int block_id, int 
 
   const auto multiply = [&](const PairStage<MT, RG>& s) {
     const F32x4 zero{0.0F, 0.0F, 0.0F, 0.0F};
+    if constexpr (WK == Weights::kQ8Expanded) {
+      // Each block's weights as bf16(scale * q), one float32 sum over k.
+#pragma unroll
+      for (int r = 0; r < RG; ++r) {
+        const float s0 = HalfValue(static_cast<std::uint16_t>(s.scales[r] & 0xFFFFU));
+        const float s1 = HalfValue(static_cast<std::uint16_t>(s.scales[r] >> 16));
+        const Bf16x8 b0 = AsBf16x8(Expand(s.w[r].x, s.w[r].y, s0));
+        const Bf16x8 b1 = AsBf16x8(Expand(s.w[r].z, s.w[r].w, s1));
+#pragma unroll
+        for (int t = 0; t < MT; ++t) {
+          acc[r][t] = Mfma16x16x32(AsBf16x8(s.a[t][0]), b0, acc[r][t]);
+          acc[r][t] = Mfma16x16x32(AsBf16x8(s.a[t][1]), b1, acc[r][t]);
+        }
+      }
+      return;
+    }
     if constexpr (WK != Weights::kQ8) {
 #pragma unroll
       for (int r = 0; r < RG; ++r)

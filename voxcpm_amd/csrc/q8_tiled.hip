@@ -32,6 +32,7 @@ namespace vx {
 namespace {
 
 using q8::AsBf16x8;
+using q8::Expand;
 using q8::Bf16x8;
 using q8::F32x4;
 using q8::kUnitBytes;
@@ -60,16 +61,6 @@ struct TiledArgs {
   int splits, pairs_per_split;
   float* partials;
 };
-
-/// 8 int8 values (two little-endian dwords) times `scale`, each rounded to
-/// bf16 (nearest even) by v_cvt_pk_bf16_f32.
-__device__ inline uint4 Expand(std::uint32_t w0, std::uint32_t w1, float scale) {
-  const auto v = [&](std::uint32_t word, int byte) {
-    return scale * static_cast<float>(static_cast<std::int8_t>(word >> (8 * byte)));
-  };
-  return uint4{PackBf16x2(v(w0, 0), v(w0, 1)), PackBf16x2(v(w0, 2), v(w0, 3)),
-               PackBf16x2(v(w1, 0), v(w1, 1)), PackBf16x2(v(w1, 2), v(w1, 3))};
-}
 
 /// Logical tile of workgroup `b` of `blocks`: workgroup b runs on die b % 8;
 /// die d takes a contiguous range of logical tiles (the first blocks % 8
