@@ -44,16 +44,16 @@ BF16_PEAK_TFLOPS = 2500.0
 # wall-clock mfma_frac of each prefill row; profiles/q8_gemm_prefill.md.
 PREFILL_MFMA_BUSY = {"source": "profiles/q8_gemm_prefill.md (rocprofv3 --pmc "
                                "SQ_VALU_MFMA_BUSY_CYCLES, GRBM_GUI_ACTIVE)",
-                     "m512_n16384": 0.311, "m1024_n16384": 0.412}
+                     "m512_n16384": 0.309, "m1024_n16384": 0.413}
 # HBM bytes per launch of the M=22 sweep kernels from two rocprofv3 PMC runs
 # (profiles/q8_skinny_m22_traffic.md): FETCH_SIZE KiB (scaled by 2.0, its
 # reading of a 256 MiB copy of known size) + WRITE_SIZE KiB (scale 1.0).
 # Measured, not computed: re-measure when the product kernel changes. Last
 # measured on the build of commit TRAFFIC_BUILD (the summary names it).
 FETCH_SCALE = 262144 / 131083.5
-TRAFFIC_BUILD = "584d730"
-TRAFFIC_KIB = {(1024, 3072): (1834.0, 264.0), (1024, 8192): (4545.5, 704.0),
-               (2048, 2048): (2559.5, 176.0), (2048, 16384): (17802.0, 1408.0)}
+TRAFFIC_BUILD = "5769466"
+TRAFFIC_KIB = {(1024, 3072): (1834.0, 264.0), (1024, 8192): (4553.5, 704.0),
+               (2048, 2048): (2560.0, 176.0), (2048, 16384): (17795.5, 1408.0)}
 # The decode steps' products (tools/bench/gemm_bench.cpp:34-38): the base and
 # residual LMs (hidden 2048, 16 + 2 x 2 heads of 128, MLP 6144) and the
 # local encoder/DiT shapes, at one row (an LM step) and five (the encoder's
@@ -533,6 +533,19 @@ def gpu_prefill(args, torch, ops, synth, device, stream):
     """Prefill-sized Q8_0 products (m > 128, matrix-core bound): TFLOP/s of
     2 m n k per launch, launches replayed from a HIP graph over a few
     rotating weight copies."""
+    import ctypes
+
+    from voxcpm_amd import _lib
+
+    def prefill_kernel(m: int, k: int, n: int, scratch) -> str:
+        """The kernel vx_q8_linear's dispatch picks (vx_q8_prefill_plan)."""
+        plan = (ctypes.c_int32 * 4)()
+        _lib.check(_lib.lib().vx_q8_prefill_plan(m, k, n, scratch.handle, plan))
+        names = {0: "TiledKernel (q8_tiled.hip)", 1: "GemmKernel (q8_gemm.hip)",
+                 2: "EngineKernel in blocks of 64 rows (q8_tile.hpp)"}
+        split = f", k split {plan[3]} ways" if plan[3] > 1 else ""
+        return names[plan[0]] + split
+
     rows = []
     k = PREFILL_K
     # The product scratch (as the reference's Bf16Gemm owns its workspace):
@@ -563,9 +576,7 @@ def gpu_prefill(args, torch, ops, synth, device, stream):
             rows.append({"m": m, "k": k, "n": n, "us": round(seconds * 1e6, 2),
                          "tflops": round(tflops, 1),
                          "mfma_frac": round(tflops / BF16_PEAK_TFLOPS, 4),
-                         # vx_q8_linear's dispatch (products.hpp UseGemm)
-                         "kernel": "GemmKernel (q8_gemm.hip)" if m >= 512 and n >= 6144
-                                   else "TiledKernel (q8_tiled.hip)"})
+                         "kernel": prefill_kernel(m, k, n, scratch)})
             log(f"  prefill M={m} K={k} N={n}: {seconds * 1e6:.1f} us, {tflops:.1f} TFLOP/s")
             del g
         del pool, packed
