@@ -491,6 +491,17 @@ ProductPlan PlanRowBlocks(std::size_t m, std::size_t k, std::size_t n) {
 ProductPlan PlanEngine(std::size_t m, std::size_t k, std::size_t n, q8::Weights kind) {
   ProductPlan plan;
   plan.mt = static_cast<int>((m + 15) / 16);
+  if ((plan.mt == 3 || plan.mt == 4) && kind == q8::Weights::kQ8 && q8::Groups(n) <= 256) {
+    // 33-64 rows over at most 256 row groups: two blocks of at most 32
+    // rows, each the plan of its rows (the blocks of a tile `tiles`
+    // workgroups apart, on one compute die where tiles is a multiple of 8,
+    // so that its L2 serves the weights to both). Measured on MI355X:
+    // (1024, 3072) 5.12 -> 4.84 us at 44 rows, 5.54 -> 5.21 us at 64; wider
+    // products measured slower so ((2048, 16384) 16.5 -> 18.2 us at 44).
+    ProductPlan half = PlanEngine((m + 1) / 2, k, n, kind);
+    half.row_blocks *= 2;
+    return half;
+  }
   if (plan.mt > 4 && kind != q8::Weights::kBf16Rows) {
     // More than 64 rows: blocks of at most 64 rows, four 16-row tiles each,
     // staged per wave from whole-line loads; the blocks of a tile lie
@@ -521,6 +532,16 @@ ProductPlan PlanEngine(std::size_t m, std::size_t k, std::size_t n, q8::Weights 
   while (plan.tiles % 8 == 0 && plan.row_blocks < 4 && plan.tiles * 2 * plan.row_blocks <= 256 &&
          static_cast<int>(m) >= 10 * plan.row_blocks)
     plan.row_blocks *= 2;
+  // Each workgroup stages and multiplies its block's rows only: the tiles
+  // (and RunSkinny's load groups) follow the block's rows, not m's.
+  // Measured on MI355X at (2048, 2048): 22 rows 4.80 -> 4.36 us, 44 rows
+  // 6.67 -> 5.16 us, 64 rows 7.31 -> 5.49 us.
+  const int block_tiles =
+      static_cast<int>((m + plan.row_blocks - 1) / plan.row_blocks + 15) / 16;
+  if (block_tiles < plan.mt) {
+    plan.mt = block_tiles;
+    plan.waves = q8::EngineThreads(plan.mt, plan.rg) / kWave;
+  }
   if (plan.mt == 2 && groups >= 512 && kind == q8::Weights::kQ8) {
     // Wide Q8_0 products of 17-32 rows: about 512 workgroups of 8 waves
     // (two per compute unit), the fewest row groups that keep them at most
@@ -621,8 +642,10 @@ int RunSkinny(const Bf16* x, const void* w, float* y, Bf16* y_bf16,
               const ProductPlan& plan, float* partials, unsigned* counters,
               hipStream_t stream, q8::Weights kind) {
   if (plan.engine) {
+    // The rows one workgroup loads (its block's), which set the load groups.
+    const int block_rows = static_cast<int>((m + plan.row_blocks - 1) / plan.row_blocks);
     const EngineLauncher launch =
-        PickEngine(plan.mt, plan.rg, plan.pw, static_cast<int>(m), plan.waves, kind);
+        PickEngine(plan.mt, plan.rg, plan.pw, block_rows, plan.waves, kind);
     if (launch == nullptr)
       return Fail(VX_UNSUPPORTED, "no product engine for this plan");
     q8::TileArgs args{};
@@ -634,7 +657,7 @@ int RunSkinny(const Bf16* x, const void* w, float* y, Bf16* y_bf16,
     args.groups = static_cast<int>(q8::Groups(n));
     args.group_stride = 1;
     args.row_blocks = plan.row_blocks;
-    args.rows_per_block = static_cast<int>((m + plan.row_blocks - 1) / plan.row_blocks);
+    args.rows_per_block = block_rows;
     args.x = x;
     args.y = y_bf16 != nullptr ? nullptr : y;
     args.y_bf16 = y_bf16;

@@ -1,5 +1,6 @@
-// The skinny Q8_0 product engine (m <= 128 activation rows), shared by the
-// standalone products and the DiT's fused layer kernels.
+// The skinny Q8_0 product engine, shared by the standalone products (up to
+// 128 rows with the exact arithmetic, more in blocks of 64 rows with the
+// expanded one) and the DiT's fused layer kernels.
 //
 // A workgroup owns RG row groups (16 weight rows each) of the output and the
 // whole reduction length; its waves split the column pairs (two Q8_0
@@ -13,7 +14,8 @@
 //
 // Activations come from one of three sources:
 //  - kRowMajor: bf16 [m][k] row-major (the drop-in product's x); up to
-//    32 rows are staged per wave through LDS from whole-line loads;
+//    64 rows (a block of them) are staged per wave through LDS from
+//    whole-line loads;
 //  - kFragBf16: bf16 in fragment order (below), written by the DiT kernels
 //    so that each wave's operand load is 1 KB of contiguous bytes;
 //  - kNormF32: the float32 residual stream in fragment order, RMS-normalised
