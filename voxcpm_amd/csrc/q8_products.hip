@@ -350,7 +350,7 @@ EngineLauncher EnginePw(int pw, int m) {
 
 template<int MT, q8::Weights WK>
 EngineLauncher EngineRg(int rg, int pw, int m) {
-  if constexpr (MT * 4 <= 8) {
+  if constexpr (MT * 4 <= 16) {
     if (rg == 4)
       return EnginePw<MT, 4, WK>(pw, m);
   }
@@ -519,8 +519,11 @@ ProductPlan PlanEngine(std::size_t m, std::size_t k, std::size_t n, q8::Weights 
   // Up to 8 rows (one staged load group) the activations cost little to
   // re-read: one row group per workgroup spreads wide products over more
   // compute units (measured on MI355X at 1 and 5 rows, n 12288 and 16384).
+  // 33-64 rows over more than 512 row groups keep four (150-178 VGPRs in
+  // 8-wave workgroups, no spill): (2048, 16384) 15.4 -> 14.4 us at 44
+  // rows, 17.9 -> 16.6 us at 64, measured on MI355X against two.
   int rg = (m <= 8 || groups <= 256) ? 1 : groups <= 512 ? 2 : 4;
-  while (rg > 1 && rg * plan.mt > 8)
+  while (rg > 1 && rg * plan.mt > 16)
     rg /= 2;
   plan.rg = rg;
   plan.tiles = (groups + rg - 1) / rg;
