@@ -86,7 +86,7 @@ def test_bf16_products_against_double(vx, oracle, cuda, stream, k, n, rows_list)
     (1024, 2560, [40, 64, 100, 128]),   # the engine, one and two row blocks
     (2048, 2048, [129, 256]),           # past 128 rows (hipBLASLt's in the reference)
     (96, 40, [65, 130]),                # odd pair count, rows not a multiple of 16
-    (2048, 16384, [128]),               # a wide product in two row blocks
+    (2048, 16384, [44, 128]),           # four row groups per workgroup; two row blocks
 ])
 def test_bf16_products_many_rows(vx, oracle, cuda, stream, k, n, rows_list):
     rng = synth.Rng(77, k + n)
