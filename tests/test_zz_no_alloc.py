@@ -36,8 +36,8 @@ def test_noalloc_product_matches_scratch_product(vx, oracle, cuda, stream):
     function = noalloc()
     scratch = vx.Scratch(128, 16384)
     stream_handle = torch.cuda.current_stream().cuda_stream
-    # Both tiled calls split k (2 splits of 128 row tiles, then 4 of 96).
-    for m, k, n in [(256, 2048, 4096), (160, 2048, 4096), (22, 1024, 4096)]:
+    # Both tiled calls split k (4 splits of 80 tiles of 64 x 128).
+    for m, k, n in [(320, 4096, 2048), (300, 4096, 2048), (22, 1024, 4096)]:
         print(f"noalloc product m={m} k={k} n={n}", flush=True)
         if m > 128:
             plan = (ctypes.c_int32 * 4)()

@@ -113,7 +113,7 @@ int Product(const uint16_t* x, const void* packed, float* y, uint16_t* y_bf16,
             size_t m, size_t k, size_t n, int accumulate, vx_scratch* scratch,
             int rg, int waves, int splits, void* stream,
             vx::q8::Weights kind = vx::q8::Weights::kQ8) {
-  if (vx::UseRowBlocks(m, k, n))
+  if (vx::UseRowBlocks(m, k, n, kind == vx::q8::Weights::kQ8))
     return vx::RunRowBlocks(x, packed, y, y_bf16, m, k, n, accumulate != 0,
                             kind != vx::q8::Weights::kQ8, vx::Stream(stream));
   if (m > vx::kExactRows && vx::UseGemm(m, n))
@@ -332,7 +332,7 @@ int vx_q8_prefill_plan(size_t m, size_t k, size_t n, vx_scratch* scratch, int32_
   if (out4 == nullptr || m <= vx::kExactRows || k % 32 != 0 || k == 0 || n == 0)
     return vx::Fail(VX_BAD_ARG, "vx_q8_prefill_plan: bad arguments");
   const std::size_t floats = scratch != nullptr ? scratch->partial_floats : 0;
-  if (vx::UseRowBlocks(m, k, n)) {
+  if (vx::UseRowBlocks(m, k, n, true)) {
     out4[0] = 2;
     out4[1] = 64;
     out4[2] = static_cast<int32_t>(16 * (n > 4096 ? 2 : 1));  // columns per workgroup

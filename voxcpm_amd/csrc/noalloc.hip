@@ -74,7 +74,7 @@ int vx_q8_linear_noalloc(const uint16_t* x, const void* packed, float* y, size_t
   // they pick for a vx_scratch of at least that many floats.
   float* address = nullptr;
   VX_TRY(ScratchAddress(&address));
-  if (vx::UseRowBlocks(m, k, n))  // no split either
+  if (vx::UseRowBlocks(m, k, n, true))  // no split either
     return vx_q8_linear(x, packed, y, m, k, n, accumulate, nullptr, stream);
   if (vx::UseGemm(m, n))
     return vx::RunGemm(x, packed, y, nullptr, m, k, n, accumulate != 0, false, address,

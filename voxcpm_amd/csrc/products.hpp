@@ -59,8 +59,9 @@ int RunSkinny(const Bf16* x, const void* w, float* y, Bf16* y_bf16,
 
 /// Whether an m > 128 product runs on the skinny engine in blocks of 64
 /// rows (RunRowBlocks) rather than the tiled or the 32 x 32 MFMA kernel:
-/// the smaller prefill products, where those kernels' grids are few tiles.
-bool UseRowBlocks(std::size_t m, std::size_t k, std::size_t n);
+/// the smaller prefill products, where those kernels' grids are few tiles
+/// (`q8`: Q8_0 panels, else bf16 panels).
+bool UseRowBlocks(std::size_t m, std::size_t k, std::size_t n, bool q8);
 
 /// More than 128 rows on the skinny engine in blocks of 64 rows, each
 /// staged per wave: Q8_0 panels with the reference's expanded arithmetic

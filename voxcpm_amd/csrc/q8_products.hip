@@ -692,17 +692,21 @@ int RunSkinny(const Bf16* x, const void* w, float* y, Bf16* y_bf16,
   return LaunchStatus("q8 product");
 }
 
-bool UseRowBlocks(std::size_t m, std::size_t k, std::size_t n) {
+bool UseRowBlocks(std::size_t m, std::size_t k, std::size_t n, bool q8) {
   // Measured on MI355X against the tiled kernel (with its k split) and the
   // 32 x 32 MFMA kernel, Q8_0 and bf16 panels alike: faster up to about
   // 1.2 G multiply-adds (129 x 2048 x 2048 15.6 -> 9.2 us, 256 x 1024 x 4096
   // 14.3 -> 10.9 us), and on 2048 x 2048 weights up to 512 rows (512 rows
-  // 21.0 -> 17.3 us); slower beyond (256 x 2048 x 8192 on a par, 1024 x 2048
-  // x 2048 24.7 -> 32.9 us), where each 64-row block re-reads the weights.
+  // 21.0 -> 17.3 us); slower beyond (1024 x 2048 x 2048 24.7 -> 32.9 us),
+  // where each 64-row block re-reads the weights. Q8_0 panels of up to
+  // 2048 x 6144 values also up to 256 rows (129 x 2048 x 6144 24.2 -> 16.1
+  // us, 256 x 6144 x 2048 25.8 -> 23.6 us; 256 x 2048 x 4096 and
+  // 256 x 1024 x 8192 on a par); bf16 panels lost there.
   if (m <= kExactRows)
     return false;
   const double work = static_cast<double>(m) * static_cast<double>(k) * static_cast<double>(n);
-  return work <= 1.2e9 || (m <= 512 && k >= 2048 && k * n <= 2048 * 2048);
+  return work <= 1.2e9 || (m <= 512 && k >= 2048 && k * n <= 2048 * 2048) ||
+         (q8 && m <= 256 && k * n <= 2048 * 6144);
 }
 
 int RunRowBlocks(const Bf16* x, const void* w, float* y, Bf16* y_bf16, std::size_t m,
