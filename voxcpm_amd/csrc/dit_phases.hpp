@@ -63,6 +63,48 @@ __device__ __forceinline__ void InAssembleBody(const InArgs& a, int group, int l
   const int r16 = lane % 16;
   const int octet = lane / 16;
   const int pairs = PairsOf(a.feat);
+  const int column = 16 * group + r16;
+  const int groups = a.hidden / 16;
+  // Every value the wave stores after its product is loaded first, so that
+  // all its loads are in flight together instead of one round trip per
+  // store: the bias, the norm weight of its column (lane % 16 is the column
+  // of every row the lane writes) and its mu / time / condition values,
+  // pass p holding element 64 p + lane of the 2 (3 + patch) rows x 16
+  // columns (branch-major).
+  // Buffer loads: a value a lane does not need (a null bias, a source row
+  // it does not take) is read as zero with no access and no branch, so the
+  // compiler issues every load before it waits for the first.
+  const std::uint32_t hidden_bytes = 4U * static_cast<std::uint32_t>(a.hidden);
+  const auto bf16_at = [&](const Bf16* base) {
+    const std::uint32_t word = q8::BufferLoad4(
+        q8::BufferOf(base, base != nullptr ? hidden_bytes / 2 : 0U),
+        4U * static_cast<std::uint32_t>(column / 2), base != nullptr);
+    return Bf16Value(static_cast<Bf16>(column % 2 != 0 ? word >> 16 : word & 0xFFFFU));
+  };
+  const float bias = bf16_at(a.bias);
+  const float gamma = bf16_at(a.norm_out != nullptr ? a.norm_gamma : nullptr);
+  const int fixed = 3 + a.patch;  // mu, mu, time, condition rows
+  constexpr int kFixedPasses = 6;  // 2 (3 + patch) 16 <= 384 for patch <= 8
+  const __amdgpu_buffer_rsrc_t mu_buffer = q8::BufferOf(a.mu, 2U * hidden_bytes);
+  const __amdgpu_buffer_rsrc_t time_buffer = q8::BufferOf(a.time, hidden_bytes);
+  const __amdgpu_buffer_rsrc_t cond_buffer =
+      q8::BufferOf(a.cond, static_cast<std::uint32_t>(a.patch) * hidden_bytes);
+  float fixed_value[kFixedPasses];
+#pragma unroll
+  for (int pass = 0; pass < kFixedPasses; ++pass) {
+    const int e = kWave * pass + lane;
+    const bool live = e < 2 * fixed * 16;
+    const int branch = e / (fixed * 16);
+    const int row = (e / 16) % fixed;
+    const std::uint32_t at = 4U * static_cast<std::uint32_t>(column);
+    const std::uint32_t mu = q8::BufferLoad4(
+        mu_buffer, at + static_cast<std::uint32_t>(row) * hidden_bytes,
+        live && row < 2 && branch == 0);
+    const std::uint32_t time = q8::BufferLoad4(time_buffer, at, live && row == 2);
+    const std::uint32_t cond = q8::BufferLoad4(
+        cond_buffer, at + static_cast<std::uint32_t>(row - 3) * hidden_bytes, live && row > 2);
+    fixed_value[pass] = __uint_as_float(row < 2 ? mu : row == 2 ? time : cond);
+  }
   const std::uint8_t* unit =
       a.w + static_cast<std::size_t>(group) * pairs * kUnit;
   F32x4 acc{0.0F, 0.0F, 0.0F, 0.0F};
@@ -77,11 +119,11 @@ __device__ __forceinline__ void InAssembleBody(const InArgs& a, int group, int l
     uint4 xa[2];
 #pragma unroll
     for (int hf = 0; hf < 2; ++hf) {
-      const int column = 64 * pair + 32 * hf + 8 * octet;
+      const int x_column = 64 * pair + 32 * hf + 8 * octet;
       float v[8] = {0, 0, 0, 0, 0, 0, 0, 0};
-      if (r16 < a.patch && column < a.feat) {
+      if (r16 < a.patch && x_column < a.feat) {
         const float4* source = reinterpret_cast<const float4*>(
-            a.x + static_cast<std::size_t>(r16) * a.feat + column);
+            a.x + static_cast<std::size_t>(r16) * a.feat + x_column);
         const float4 lo = source[0];
         const float4 hi = source[1];
         v[0] = lo.x; v[1] = lo.y; v[2] = lo.z; v[3] = lo.w;
@@ -107,21 +149,17 @@ __device__ __forceinline__ void InAssembleBody(const InArgs& a, int group, int l
     for (int i = 0; i < 4; ++i)
       acc[i] = fmaf(s1, sum1[i], acc[i]);
   }
-  const int column = 16 * group + r16;
-  const float bias = a.bias != nullptr ? Bf16Value(a.bias[column]) : 0.0F;
-  const int groups = a.hidden / 16;
   // The norm operand and the row's sum over the wave's 16 columns: the 16
   // lanes of a DPP row hold one row's 16 columns (uniform control flow;
   // dead lanes add zeros and write nothing).
-  const auto emit_norm = [&](bool live, int row, int c, float value) {
+  const auto emit_norm = [&](bool live, int row, float value) {
     if (a.norm_out == nullptr)
       return;
     const float square = RowSum16(live ? value * value : 0.0F);
     if (live) {
-      q8::Put<kCoherent>(a.norm_out + BfFragIndex(row, c),
-                         q8::Bf16Fast(value * Bf16Value(a.norm_gamma[c])));
-      if (c % 16 == 0)
-        q8::Put<kCoherent>(a.norm_squares + row * groups + c / 16, square);
+      q8::Put<kCoherent>(a.norm_out + BfFragIndex(row, column), q8::Bf16Fast(value * gamma));
+      if (column % 16 == 0)
+        q8::Put<kCoherent>(a.norm_squares + row * groups + column / 16, square);
     }
   };
 #pragma unroll
@@ -133,27 +171,20 @@ __device__ __forceinline__ void InAssembleBody(const InArgs& a, int group, int l
       q8::Put<kCoherent>(a.h + F32FragIndex(3 + a.patch + row, column), value);
       q8::Put<kCoherent>(a.h + F32FragIndex(a.length + 3 + a.patch + row, column), value);
     }
-    emit_norm(live, 3 + a.patch + row, column, value);
-    emit_norm(live, a.length + 3 + a.patch + row, column, value);
+    emit_norm(live, 3 + a.patch + row, value);
+    emit_norm(live, a.length + 3 + a.patch + row, value);
   }
-  const int fixed = 3 + a.patch;  // mu, mu, time, condition rows
-  for (int first = 0; first < 2 * fixed * 16; first += kWave) {
-    const int e = first + lane;
+#pragma unroll
+  for (int pass = 0; pass < kFixedPasses; ++pass) {
+    if (kWave * pass >= 2 * fixed * 16)  // uniform
+      break;
+    const int e = kWave * pass + lane;
     const bool live = e < 2 * fixed * 16;
     const int branch = e / (fixed * 16);
     const int row = (e / 16) % fixed;
-    const int c = 16 * group + e % 16;
-    float value = 0.0F;
-    if (live) {
-      if (row < 2)
-        value = branch == 0 ? a.mu[static_cast<std::size_t>(row) * a.hidden + c] : 0.0F;
-      else if (row == 2)
-        value = a.time[c];
-      else
-        value = a.cond[static_cast<std::size_t>(row - 3) * a.hidden + c];
-      q8::Put<kCoherent>(a.h + F32FragIndex(branch * a.length + row, c), value);
-    }
-    emit_norm(live, branch * a.length + row, c, value);
+    if (live)
+      q8::Put<kCoherent>(a.h + F32FragIndex(branch * a.length + row, column), fixed_value[pass]);
+    emit_norm(live, branch * a.length + row, fixed_value[pass]);
   }
 }
 
@@ -366,10 +397,21 @@ __device__ __forceinline__ void OutEulerBody(const OutArgs& a, float* lds) {
   const bool row_ok = r16 < out_rows;
   const int h_row = row_ok ? (r16 / a.patch) * a.length + 3 + a.patch + r16 % a.patch : 0;
   constexpr int kPw = 2;  // pairs per wave: hidden <= 2048
+  // Every operand is a buffer load issued here, before the first wait: the
+  // weights, the rows, the norm weights, the bias and x (a lane's value it
+  // does not need reads zero with no access and no branch), so that they
+  // arrive in one round trip instead of one per use.
+  const __amdgpu_buffer_rsrc_t w_buffer = q8::BufferOf(
+      a.w, static_cast<std::uint32_t>(groups) * static_cast<std::uint32_t>(pairs) * kUnit);
+  const __amdgpu_buffer_rsrc_t h_buffer = q8::BufferOf(
+      a.h, 4U * static_cast<std::uint32_t>(q8::kFragRows * 64 * pairs));
+  const __amdgpu_buffer_rsrc_t norm_buffer =
+      q8::BufferOf(a.norm, 2U * static_cast<std::uint32_t>(a.hidden));
   uint4 wv[kPw][kOutGroups];
   uint4 wv2[kPw][kOutGroups];  // bf16: the pair's second block
   std::uint32_t sc[kPw][kOutGroups];
   float4 hv[kPw][2][2];
+  uint4 gw[kPw][2];
 #pragma unroll
   for (int p = 0; p < kPw; ++p) {
     const int pair = wave + p * waves;
@@ -377,29 +419,45 @@ __device__ __forceinline__ void OutEulerBody(const OutArgs& a, float* lds) {
 #pragma unroll
     for (int g = 0; g < kOutGroups; ++g) {
       const bool use = ok && g < groups;
-      const std::uint8_t* u =
-          a.w + (static_cast<std::size_t>(use ? g : 0) * pairs + (use ? pair : 0)) * kUnit;
-      wv[p][g] = use ? *reinterpret_cast<const uint4*>(u + 16 * lane) : uint4{0U, 0U, 0U, 0U};
+      const std::uint32_t unit =
+          (static_cast<std::uint32_t>(g) * static_cast<std::uint32_t>(pairs) +
+           static_cast<std::uint32_t>(pair)) * kUnit;
+      wv[p][g] = q8::BufferLoad16(w_buffer, unit + 16U * lane, use);
       if constexpr (kBf16) {
-        wv2[p][g] = use ? *reinterpret_cast<const uint4*>(u + q8::kBf16HalfBytes + 16 * lane)
-                        : uint4{0U, 0U, 0U, 0U};
+        wv2[p][g] = q8::BufferLoad16(w_buffer, unit + q8::kBf16HalfBytes + 16U * lane, use);
         sc[p][g] = 0U;
       } else {
-        sc[p][g] =
-            use ? *reinterpret_cast<const std::uint32_t*>(u + kValueBytes + 4 * r16) : 0U;
+        sc[p][g] = q8::BufferLoad4(w_buffer, unit + kValueBytes + 4U * r16, use);
       }
     }
 #pragma unroll
-    for (int hf = 0; hf < 2; ++hf)
+    for (int hf = 0; hf < 2; ++hf) {
 #pragma unroll
-      for (int q = 0; q < 2; ++q) {
-        float4 v{0.0F, 0.0F, 0.0F, 0.0F};
-        if (ok && row_ok)
-          v = *reinterpret_cast<const float4*>(
-              a.h + F32FragIndex(h_row, 64 * pair + 32 * hf + 8 * octet + 4 * q));
-        hv[p][hf][q] = v;
-      }
+      for (int q = 0; q < 2; ++q)
+        hv[p][hf][q] = __builtin_bit_cast(
+            float4, q8::BufferLoad16(
+                        h_buffer,
+                        4U * static_cast<std::uint32_t>(F32FragIndex(
+                                 h_row, 64 * pair + 32 * hf + 8 * octet + 4 * q)),
+                        ok && row_ok));
+      gw[p][hf] = q8::BufferLoad16(
+          norm_buffer, 2U * static_cast<std::uint32_t>(64 * pair + 32 * hf + 8 * octet), ok);
+    }
   }
+  // The epilogue's first element of this thread (e = threadIdx.x; the
+  // product's 4 x 256 outputs fit one pass of 1024 threads) and its x value.
+  const int first_g = static_cast<int>(threadIdx.x) / 256;
+  const int first_column = 16 * first_g + static_cast<int>(threadIdx.x) % 16;
+  const std::uint32_t bias_word = q8::BufferLoad4(
+      q8::BufferOf(a.bias, a.bias != nullptr ? 2U * static_cast<std::uint32_t>(a.feat) : 0U),
+      4U * static_cast<std::uint32_t>(first_column / 2),
+      a.bias != nullptr && first_g < kOutGroups && first_column < a.feat);
+  const float first_bias = Bf16Value(static_cast<Bf16>(
+      first_column % 2 != 0 ? bias_word >> 16 : bias_word & 0xFFFFU));
+  const int values = a.patch * a.feat;  // per branch
+  const float first_x = __uint_as_float(q8::BufferLoad4(
+      q8::BufferOf(a.x, a.x != nullptr ? 4U * static_cast<std::uint32_t>(values) : 0U),
+      4U * threadIdx.x, a.x != nullptr && static_cast<int>(threadIdx.x) < values));
   float partial = 0.0F;
 #pragma unroll
   for (int p = 0; p < kPw; ++p)
@@ -431,10 +489,10 @@ __device__ __forceinline__ void OutEulerBody(const OutArgs& a, float* lds) {
     uint4 xa[2];
 #pragma unroll
     for (int hf = 0; hf < 2; ++hf) {
-      const uint4 gw = *reinterpret_cast<const uint4*>(a.norm + 64 * pair + 32 * hf + 8 * octet);
-      const float gamma[8] = {q8::Bf16Lo(gw.x), q8::Bf16Hi(gw.x), q8::Bf16Lo(gw.y),
-                              q8::Bf16Hi(gw.y), q8::Bf16Lo(gw.z), q8::Bf16Hi(gw.z),
-                              q8::Bf16Lo(gw.w), q8::Bf16Hi(gw.w)};
+      const uint4 g8 = gw[p][hf];
+      const float gamma[8] = {q8::Bf16Lo(g8.x), q8::Bf16Hi(g8.x), q8::Bf16Lo(g8.y),
+                              q8::Bf16Hi(g8.y), q8::Bf16Lo(g8.z), q8::Bf16Hi(g8.z),
+                              q8::Bf16Lo(g8.w), q8::Bf16Hi(g8.w)};
       const float4 lo = hv[p][hf][0];
       const float4 hi = hv[p][hf][1];
       const float x8[8] = {lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
@@ -473,7 +531,6 @@ __device__ __forceinline__ void OutEulerBody(const OutArgs& a, float* lds) {
     for (int i = 0; i < 4; ++i)
       reduce[wave][g][i][lane] = acc[g][i];
   __syncthreads();
-  const int values = a.patch * a.feat;  // per branch
   for (int e = threadIdx.x; e < kOutGroups * 256; e += blockDim.x) {
     const int g = e / 256;
     const int i = (e / 64) % 4;
@@ -486,7 +543,7 @@ __device__ __forceinline__ void OutEulerBody(const OutArgs& a, float* lds) {
     for (int w = 1; w < waves; ++w)
       v += reduce[w][g][i][l];
     if (a.bias != nullptr)
-      v += Bf16Value(a.bias[column]);
+      v += e == static_cast<int>(threadIdx.x) ? first_bias : Bf16Value(a.bias[column]);
     const int at = row * a.feat + column;  // [branch][patch][feat]
     a.velocity[at] = v;
     velocity[at] = v;
@@ -510,7 +567,8 @@ __device__ __forceinline__ void OutEulerBody(const OutArgs& a, float* lds) {
   }
   for (int i = threadIdx.x; i < values; i += blockDim.x) {
     const float guided = u[i] * s + a.cfg * (c[i] - u[i] * s);
-    a.x[i] -= a.dt * guided;
+    const float before = i == static_cast<int>(threadIdx.x) ? first_x : a.x[i];
+    a.x[i] = before - a.dt * guided;
   }
 }
 
