@@ -397,21 +397,10 @@ __device__ __forceinline__ void OutEulerBody(const OutArgs& a, float* lds) {
   const bool row_ok = r16 < out_rows;
   const int h_row = row_ok ? (r16 / a.patch) * a.length + 3 + a.patch + r16 % a.patch : 0;
   constexpr int kPw = 2;  // pairs per wave: hidden <= 2048
-  // Every operand is a buffer load issued here, before the first wait: the
-  // weights, the rows, the norm weights, the bias and x (a lane's value it
-  // does not need reads zero with no access and no branch), so that they
-  // arrive in one round trip instead of one per use.
-  const __amdgpu_buffer_rsrc_t w_buffer = q8::BufferOf(
-      a.w, static_cast<std::uint32_t>(groups) * static_cast<std::uint32_t>(pairs) * kUnit);
-  const __amdgpu_buffer_rsrc_t h_buffer = q8::BufferOf(
-      a.h, 4U * static_cast<std::uint32_t>(q8::kFragRows * 64 * pairs));
-  const __amdgpu_buffer_rsrc_t norm_buffer =
-      q8::BufferOf(a.norm, 2U * static_cast<std::uint32_t>(a.hidden));
   uint4 wv[kPw][kOutGroups];
   uint4 wv2[kPw][kOutGroups];  // bf16: the pair's second block
   std::uint32_t sc[kPw][kOutGroups];
   float4 hv[kPw][2][2];
-  uint4 gw[kPw][2];
 #pragma unroll
   for (int p = 0; p < kPw; ++p) {
     const int pair = wave + p * waves;
@@ -419,45 +408,29 @@ __device__ __forceinline__ void OutEulerBody(const OutArgs& a, float* lds) {
 #pragma unroll
     for (int g = 0; g < kOutGroups; ++g) {
       const bool use = ok && g < groups;
-      const std::uint32_t unit =
-          (static_cast<std::uint32_t>(g) * static_cast<std::uint32_t>(pairs) +
-           static_cast<std::uint32_t>(pair)) * kUnit;
-      wv[p][g] = q8::BufferLoad16(w_buffer, unit + 16U * lane, use);
+      const std::uint8_t* u =
+          a.w + (static_cast<std::size_t>(use ? g : 0) * pairs + (use ? pair : 0)) * kUnit;
+      wv[p][g] = use ? *reinterpret_cast<const uint4*>(u + 16 * lane) : uint4{0U, 0U, 0U, 0U};
       if constexpr (kBf16) {
-        wv2[p][g] = q8::BufferLoad16(w_buffer, unit + q8::kBf16HalfBytes + 16U * lane, use);
+        wv2[p][g] = use ? *reinterpret_cast<const uint4*>(u + q8::kBf16HalfBytes + 16 * lane)
+                        : uint4{0U, 0U, 0U, 0U};
         sc[p][g] = 0U;
       } else {
-        sc[p][g] = q8::BufferLoad4(w_buffer, unit + kValueBytes + 4U * r16, use);
+        sc[p][g] =
+            use ? *reinterpret_cast<const std::uint32_t*>(u + kValueBytes + 4 * r16) : 0U;
       }
     }
 #pragma unroll
-    for (int hf = 0; hf < 2; ++hf) {
+    for (int hf = 0; hf < 2; ++hf)
 #pragma unroll
-      for (int q = 0; q < 2; ++q)
-        hv[p][hf][q] = __builtin_bit_cast(
-            float4, q8::BufferLoad16(
-                        h_buffer,
-                        4U * static_cast<std::uint32_t>(F32FragIndex(
-                                 h_row, 64 * pair + 32 * hf + 8 * octet + 4 * q)),
-                        ok && row_ok));
-      gw[p][hf] = q8::BufferLoad16(
-          norm_buffer, 2U * static_cast<std::uint32_t>(64 * pair + 32 * hf + 8 * octet), ok);
-    }
+      for (int q = 0; q < 2; ++q) {
+        float4 v{0.0F, 0.0F, 0.0F, 0.0F};
+        if (ok && row_ok)
+          v = *reinterpret_cast<const float4*>(
+              a.h + F32FragIndex(h_row, 64 * pair + 32 * hf + 8 * octet + 4 * q));
+        hv[p][hf][q] = v;
+      }
   }
-  // The epilogue's first element of this thread (e = threadIdx.x; the
-  // product's 4 x 256 outputs fit one pass of 1024 threads) and its x value.
-  const int first_g = static_cast<int>(threadIdx.x) / 256;
-  const int first_column = 16 * first_g + static_cast<int>(threadIdx.x) % 16;
-  const std::uint32_t bias_word = q8::BufferLoad4(
-      q8::BufferOf(a.bias, a.bias != nullptr ? 2U * static_cast<std::uint32_t>(a.feat) : 0U),
-      4U * static_cast<std::uint32_t>(first_column / 2),
-      a.bias != nullptr && first_g < kOutGroups && first_column < a.feat);
-  const float first_bias = Bf16Value(static_cast<Bf16>(
-      first_column % 2 != 0 ? bias_word >> 16 : bias_word & 0xFFFFU));
-  const int values = a.patch * a.feat;  // per branch
-  const float first_x = __uint_as_float(q8::BufferLoad4(
-      q8::BufferOf(a.x, a.x != nullptr ? 4U * static_cast<std::uint32_t>(values) : 0U),
-      4U * threadIdx.x, a.x != nullptr && static_cast<int>(threadIdx.x) < values));
   float partial = 0.0F;
 #pragma unroll
   for (int p = 0; p < kPw; ++p)
@@ -489,10 +462,10 @@ __device__ __forceinline__ void OutEulerBody(const OutArgs& a, float* lds) {
     uint4 xa[2];
 #pragma unroll
     for (int hf = 0; hf < 2; ++hf) {
-      const uint4 g8 = gw[p][hf];
-      const float gamma[8] = {q8::Bf16Lo(g8.x), q8::Bf16Hi(g8.x), q8::Bf16Lo(g8.y),
-                              q8::Bf16Hi(g8.y), q8::Bf16Lo(g8.z), q8::Bf16Hi(g8.z),
-                              q8::Bf16Lo(g8.w), q8::Bf16Hi(g8.w)};
+      const uint4 gw = *reinterpret_cast<const uint4*>(a.norm + 64 * pair + 32 * hf + 8 * octet);
+      const float gamma[8] = {q8::Bf16Lo(gw.x), q8::Bf16Hi(gw.x), q8::Bf16Lo(gw.y),
+                              q8::Bf16Hi(gw.y), q8::Bf16Lo(gw.z), q8::Bf16Hi(gw.z),
+                              q8::Bf16Lo(gw.w), q8::Bf16Hi(gw.w)};
       const float4 lo = hv[p][hf][0];
       const float4 hi = hv[p][hf][1];
       const float x8[8] = {lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
@@ -531,6 +504,7 @@ __device__ __forceinline__ void OutEulerBody(const OutArgs& a, float* lds) {
     for (int i = 0; i < 4; ++i)
       reduce[wave][g][i][lane] = acc[g][i];
   __syncthreads();
+  const int values = a.patch * a.feat;  // per branch
   for (int e = threadIdx.x; e < kOutGroups * 256; e += blockDim.x) {
     const int g = e / 256;
     const int i = (e / 64) % 4;
@@ -543,7 +517,7 @@ __device__ __forceinline__ void OutEulerBody(const OutArgs& a, float* lds) {
     for (int w = 1; w < waves; ++w)
       v += reduce[w][g][i][l];
     if (a.bias != nullptr)
-      v += e == static_cast<int>(threadIdx.x) ? first_bias : Bf16Value(a.bias[column]);
+      v += Bf16Value(a.bias[column]);
     const int at = row * a.feat + column;  // [branch][patch][feat]
     a.velocity[at] = v;
     velocity[at] = v;
@@ -567,8 +541,7 @@ __device__ __forceinline__ void OutEulerBody(const OutArgs& a, float* lds) {
   }
   for (int i = threadIdx.x; i < values; i += blockDim.x) {
     const float guided = u[i] * s + a.cfg * (c[i] - u[i] * s);
-    const float before = i == static_cast<int>(threadIdx.x) ? first_x : a.x[i];
-    a.x[i] = before - a.dt * guided;
+    a.x[i] -= a.dt * guided;
   }
 }
 
