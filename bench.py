@@ -51,9 +51,9 @@ PREFILL_MFMA_BUSY = {"source": "profiles/q8_gemm_prefill.md (rocprofv3 --pmc "
 # Measured, not computed: re-measure when the product kernel changes. Last
 # measured on the build of commit TRAFFIC_BUILD (the summary names it).
 FETCH_SCALE = 262144 / 131083.5
-TRAFFIC_BUILD = "5769466"
-TRAFFIC_KIB = {(1024, 3072): (1834.0, 264.0), (1024, 8192): (4553.5, 704.0),
-               (2048, 2048): (2560.0, 176.0), (2048, 16384): (17795.5, 1408.0)}
+TRAFFIC_BUILD = "6605d9d"
+TRAFFIC_KIB = {(1024, 3072): (1831.5, 264.0), (1024, 8192): (4545.5, 704.0),
+               (2048, 2048): (2547.5, 176.0), (2048, 16384): (17802.0, 1408.0)}
 # The decode steps' products (tools/bench/gemm_bench.cpp:34-38): the base and
 # residual LMs (hidden 2048, 16 + 2 x 2 heads of 128, MLP 6144) and the
 # local encoder/DiT shapes, at one row (an LM step) and five (the encoder's
