@@ -315,8 +315,9 @@ void LaunchEngine(const q8::TileArgs& args, int tiles, int waves,
 
 using EngineLauncher = void (*)(const q8::TileArgs&, int, int, hipStream_t);
 
-/// Up to 32 rows the engine stages the rows through LDS in JR load groups
-/// of 8 rows; more rows load straight into the operands.
+/// Up to 64 rows (a workgroup's block; `m` here is the block's rows) the
+/// engine stages the rows through LDS in JR load groups of 8 rows, JR the
+/// fewest that cover them.
 template<int MT, int RG, int PW, q8::Weights WK, int NW = 0>
 EngineLauncher EngineJr(int m) {
   if constexpr (q8::StagesRows(q8::ASource::kRowMajor, MT)) {

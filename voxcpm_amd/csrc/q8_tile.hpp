@@ -583,7 +583,7 @@ __device__ __forceinline__ void EngineBody(const TileArgs& a, int block_id, int 
       }
   };
 
-  // Row staging (row-major x of up to 32 rows): a pair's rows come in as
+  // Row staging (row-major x, a block of up to 64 rows): a pair's rows come in as
   // whole 128-byte row segments, eight rows per load instruction (lane L:
   // row 8 j + L / 8, bytes 16 (L % 8) .. + 15 of the segment), go to the
   // wave's private LDS region with each 16-byte chunk index XORed with
