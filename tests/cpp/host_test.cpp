@@ -461,6 +461,19 @@ void TestDitSampler(Random& rng) {
   vc::Check(hipEventSynchronize(sampler->latent_event()), "latent event");
   const auto on_device = Download(sampler->latent(), latent.size());
   Report(on_device == latent, "latent() holds the returned latent");
+  // set_trace (generator.hpp:93-94): each traced Sample records the mu it
+  // ran with; none after the trace is cleared.
+  vc::SamplerTrace trace;
+  sampler->set_trace(&trace);
+  std::vector<float> mu2 = mu;
+  for (auto& v : mu2)
+    v = -v;
+  sampler->Sample(mu.data(), cond.data(), x.data(), 10, 2.0F, nullptr);
+  sampler->Sample(mu2.data(), cond.data(), x.data(), 10, 2.0F, nullptr);
+  sampler->set_trace(nullptr);
+  sampler->Sample(mu.data(), cond.data(), x.data(), 10, 2.0F, nullptr);
+  Report(trace.mu.size() == 2 && trace.mu[0] == mu && trace.mu[1] == mu2,
+         "set_trace records the mu of each traced Sample");
 }
 
 /// ForwardStack (transformer.cpp:55-100) on a small GQA stack with a key/

@@ -2,6 +2,7 @@
 
 #include <cstdint>
 #include <exception>
+#include <utility>
 
 #include "voxcpm_amd.h"
 
@@ -160,6 +161,13 @@ void DitSampler::Sample(const float* mu, const float* prefix_cond,
     Check(hipMemcpyAsync(latent, x_.get(), values * sizeof(float),
                          hipMemcpyDeviceToHost, stream_),
           "hipMemcpy latent");
+  if (trace_ != nullptr) {
+    std::vector<float> used(2 * config_.dit.hidden);
+    Check(hipMemcpyAsync(used.data(), mu_.get(), used.size() * sizeof(float),
+                         hipMemcpyDeviceToHost, stream_),
+          "hipMemcpy trace");
+    trace_->mu.push_back(std::move(used));
+  }
   Check(hipStreamSynchronize(stream_), "hipStreamSynchronize");
   ++steps_taken_;
 }

@@ -70,6 +70,14 @@ struct SamplerOptions {
   bool cfg_zero_star = true;
 };
 
+/// Intermediate tensors for tests, copied to the host while tracing: the
+/// DiT's part of the reference's Trace (generator.hpp:47-53), the condition
+/// mu [2 hidden] of every Sample call as the device held it when the patch
+/// ran (the reference records it per Step).
+struct SamplerTrace {
+  std::vector<std::vector<float>> mu;
+};
+
 /// The local DiT with its CFM sampler on one non-blocking stream. One
 /// sequence at a time; not thread-safe (the reference's Generator,
 /// generator.hpp:55-58, has the same rule).
@@ -106,6 +114,10 @@ public:
   [[nodiscard]] const float* latent() const { return latent_slot_; }
   [[nodiscard]] hipEvent_t latent_event() const { return latent_event_; }
 
+  /// Copies intermediate tensors into `trace` while set, null to stop
+  /// (tests; generator.hpp:93-94).
+  void set_trace(SamplerTrace* trace) { trace_ = trace; }
+
 private:
   DitSampler() = default;
 
@@ -121,6 +133,7 @@ private:
   const float* latent_slot_ = nullptr;
   std::size_t steps_taken_ = 0;
   hipEvent_t latent_event_ = nullptr;
+  SamplerTrace* trace_ = nullptr;
 };
 
 }  // namespace gufo::models::voxcpm
