@@ -9,6 +9,10 @@
 // side by side, K = 2 in), and three residual units (Snake, dilated
 // depthwise conv fused with the second Snake, pointwise product added into
 // the stream), then Snake and the 7-tap convolution to mono with tanh.
+// Over at most 128 channels (and for the latents' input convolutions) the
+// depthwise convolution and its Snake are made in the pointwise product's
+// operand loads, staged through LDS, and the units' windows alternate
+// between two buffers; wider units keep a depthwise launch.
 // Each product's epilogue applies its bias and makes its consumer's input
 // (a residual unit's window: bias, Snake, history; a block's input; the
 // output window); each state is filled by the kernel that first reads it
@@ -50,6 +54,46 @@ __device__ inline float Snake(float y, float a) {
   return y + (1.0F / (a + 1e-9F)) * (s * s);
 }
 
+/// Up to N copies (to[e] = from[e], e < count) spread over every thread of
+/// a grid: each thread's first element is loaded by Load() beside the
+/// kernel's first loads and stored by Store() at its end, so that no load
+/// of the kernel waits behind a copy's round trip; elements past the
+/// grid's threads go in a loop after them.
+template<int N>
+struct SideCopies {
+  float* to[N] = {};
+  const float* from[N] = {};
+  int count[N] = {};
+  float first[N] = {};
+  int flat = 0;
+  int threads = 0;
+  __device__ SideCopies()
+      : flat(static_cast<int>((blockIdx.y * gridDim.x + blockIdx.x) * blockDim.x + threadIdx.x)),
+        threads(static_cast<int>(gridDim.x * gridDim.y * blockDim.x)) {}
+  __device__ void Add(int i, float* into, const float* source, int n) {
+    to[i] = into;
+    from[i] = source;
+    count[i] = n;
+  }
+  __device__ void Load() {
+#pragma unroll
+    for (int i = 0; i < N; ++i)
+      first[i] = __builtin_bit_cast(
+          float, vx::q8::BufferLoad4(
+                     vx::q8::BufferOf(from[i], 4U * static_cast<std::uint32_t>(count[i])),
+                     4U * static_cast<std::uint32_t>(flat), flat < count[i]));
+  }
+  __device__ void Store() const {
+#pragma unroll
+    for (int i = 0; i < N; ++i) {
+      if (flat < count[i])
+        to[i][flat] = first[i];
+      for (int e = flat + threads; e < count[i]; e += threads)
+        to[i][e] = from[i][e];
+    }
+  }
+};
+
 /// p[0 .. count) = 0.
 __global__ void ZeroKernel(float* p, std::size_t count) {
   const std::size_t i = static_cast<std::size_t>(blockIdx.x) * blockDim.x + threadIdx.x;
@@ -69,41 +113,44 @@ __global__ void StageKernel(const float* state, const float* latents, float* wor
 }
 
 /// out[f][c] = b[c] + sum_j w[c][j] work[f + j d][c] (work holds 6 d rows
-/// of history first), optionally through Snake(alpha); afterwards
-/// state = work's last 6 d rows (this kernel never reads the state).
+/// of history first), optionally through Snake(alpha); also state =
+/// work's last 6 d rows (this kernel never reads the state).
 __global__ void DepthwiseKernel(const float* work, const float* w, const float* b,
                                 const float* alpha, float* out, float* state, std::size_t t,
                                 std::size_t c, int d, const float* copy_from = nullptr,
                                 float* copy_to = nullptr, std::size_t copy_count = 0) {
   const std::size_t i = static_cast<std::size_t>(blockIdx.x) * blockDim.x + threadIdx.x;
   const std::size_t rows = static_cast<std::size_t>(kTaps - 1) * d;
-  if (i < rows * c)
-    state[i] = work[t * c + i];
-  if (i < copy_count)  // a refresh for a kernel before this one (the block input's state)
-    copy_to[i] = copy_from[i];
-  if (i >= t * c)
-    return;
-  const std::size_t f = i / c;
-  const std::size_t ch = i % c;
-  float sum = b[ch];
+  // The state refresh and a refresh for a kernel before this one (the
+  // block input's state), loaded beside the taps.
+  SideCopies<2> copies;
+  copies.Add(0, state, work + t * c, static_cast<int>(rows * c));
+  copies.Add(1, copy_to, copy_from, static_cast<int>(copy_count));
+  copies.Load();
+  if (i < t * c) {
+    const std::size_t f = i / c;
+    const std::size_t ch = i % c;
+    float sum = b[ch];
 #pragma unroll
-  for (int j = 0; j < kTaps; ++j)
-    sum += w[ch * kTaps + j] * work[(f + static_cast<std::size_t>(j) * d) * c + ch];
-  out[i] = alpha != nullptr ? Snake(sum, alpha[ch]) : sum;
+    for (int j = 0; j < kTaps; ++j)
+      sum += w[ch * kTaps + j] * work[(f + static_cast<std::size_t>(j) * d) * c + ch];
+    out[i] = alpha != nullptr ? Snake(sum, alpha[ch]) : sum;
+  }
+  copies.Store();
 }
 
 /// samples[f] = tanh(b + sum_c sum_j w[c][j] work[f + j][c]), one
-/// workgroup per 4 frames, lanes over channels; afterwards state = work's
-/// last 6 rows (this kernel never reads the state).
+/// workgroup per 4 frames, lanes over channels; also state = work's last
+/// 6 rows (this kernel never reads the state).
 __global__ void ToMonoKernel(const float* work, const float* w, float b, float* samples,
                              float* state, std::size_t t, std::size_t c) {
   __shared__ float partial[kThreads / kWave];
   const std::size_t first = static_cast<std::size_t>(blockIdx.x) * 4;
   const int lane = static_cast<int>(threadIdx.x) % kWave;
   const int wave = static_cast<int>(threadIdx.x) / kWave;  // frame first + wave
-  if (blockIdx.x == 0)
-    for (std::size_t i = threadIdx.x; i < (kTaps - 1) * c; i += blockDim.x)
-      state[i] = work[t * c + i];
+  SideCopies<1> copies;  // the state refresh, loaded beside the window
+  copies.Add(0, state, work + t * c, static_cast<int>((kTaps - 1) * c));
+  copies.Load();
   const std::size_t f = first + wave;
   float sum = 0.0F;
   if (f < t)
@@ -117,6 +164,7 @@ __global__ void ToMonoKernel(const float* work, const float* w, float b, float* 
   __syncthreads();
   if (threadIdx.x < 4 && first + threadIdx.x < t)
     samples[first + threadIdx.x] = tanhf(partial[threadIdx.x] + b);
+  copies.Store();
 }
 
 // ---- float32 products of few rows ------------------------------------------
@@ -157,11 +205,41 @@ struct UnitWindow {
   int frames = 0;
 };
 
-template<int MT, int W>
+/// A residual unit's pointwise operand made from the unit's window as the
+/// product reads it, in place of a depthwise launch and its output buffer
+/// (vae.cpp:489-500, vae_kernels.hip:36-51): x[f][c] = Snake(b[c] +
+/// sum_j w[c][j] win[f + j d][c], alpha[c]) over the window [6 d history
+/// rows | t rows], with no Snake when alpha is null. The product's
+/// workgroups also refresh the unit's state from the window's last 6 d
+/// rows and copy `copy_count` floats (a block input's state refresh),
+/// memory that no workgroup of the launch reads.
+struct DwOperand {
+  const float* weights = nullptr;  // [c][7]
+  const float* bias = nullptr;     // [c]
+  const float* alpha = nullptr;    // [c], or null
+  int dilation = 1;
+  float* state = nullptr;          // [6 d][c]
+  const float* copy_from = nullptr;
+  float* copy_to = nullptr;
+  int copy_count = 0;
+};
+
+/// Floats of dynamic LDS a fused unit operand takes: the tap table [9][k]
+/// (seven taps, bias, alpha) and the operand rows [16 MT][k + 4].
+constexpr std::size_t DwLdsFloats(std::size_t k, int mt) {
+  return 9 * k + static_cast<std::size_t>(16 * mt) * (k + 4);
+}
+constexpr std::size_t kDwLdsBytes = 60 * 1024;  // under the default 64 KiB
+
+/// With kDw the operand is made from a window (DwOperand) into LDS before
+/// the products; k then takes one pass of KA groups per wave.
+template<int MT, int W, int KA, bool kDw>
 __global__ __launch_bounds__(W * kWave) void F32SkinnyKernel(
     const float* x, const float* w, float* y, int t, int k, int n, int accumulate,
-    UnitWindow unit) {
-  __shared__ float reduce[W][MT][4][kWave];
+    UnitWindow unit, DwOperand dw) {
+  // The waves' partial sums; with kDw they meet in the operand rows' LDS.
+  __shared__ float reduce_static[kDw ? 1 : W][MT][4][kWave];
+  extern __shared__ float staged[];  // kDw: tap table [9][k], operand rows [16 MT][k + 4]
   const int lane = static_cast<int>(threadIdx.x) % kWave;
   const int wave = static_cast<int>(threadIdx.x) / kWave;
   const int r = lane % 16;
@@ -171,11 +249,27 @@ __global__ __launch_bounds__(W * kWave) void F32SkinnyKernel(
   // This workgroup's rows: x and y from row0 on, t rows of them.
   const int row0 = 16 * MT * static_cast<int>(blockIdx.y);
   const bool block_input = unit.scale != nullptr;
-  if (unit.window != nullptr && blockIdx.y == 0) {
+  const int d = dw.dilation;
+  const int halo = kDw ? (kTaps - 1) * d : 0;  // window rows before the first frame
+  // Copies beside the product, spread over every workgroup of the grid:
+  // the next window's history and, with kDw, the unit's state (the
+  // window's last 6 d rows) and a block input's state.
+  // (Issuing these copies' loads beside the operands' and storing them at
+  // the end, as the depthwise kernel does, measured slower here.)
+  const int grid_threads = static_cast<int>(gridDim.x * gridDim.y * blockDim.x);
+  const int flat = static_cast<int>((blockIdx.y * gridDim.x + blockIdx.x) * blockDim.x +
+                                    threadIdx.x);
+  if (unit.window != nullptr) {
     float* head = unit.window + (block_input ? unit.channels : 0);
-    for (int e = static_cast<int>(blockIdx.x * blockDim.x + threadIdx.x); e < unit.head;
-         e += static_cast<int>(gridDim.x * blockDim.x))
+    for (int e = flat; e < unit.head; e += grid_threads)
       head[e] = unit.state[e];
+  }
+  if constexpr (kDw) {
+    const float* last = x + static_cast<std::size_t>(t) * k;  // the window's last 6 d rows
+    for (int e = flat; e < halo * k; e += grid_threads)
+      dw.state[e] = last[e];
+    for (int e = flat; e < dw.copy_count; e += grid_threads)
+      dw.copy_to[e] = dw.copy_from[e];
   }
   float* window = unit.window != nullptr && !block_input
                       ? unit.window + unit.head + static_cast<std::size_t>(row0) * n
@@ -187,8 +281,8 @@ __global__ __launch_bounds__(W * kWave) void F32SkinnyKernel(
   // loads stay in flight together.
   const __amdgpu_buffer_rsrc_t w_buffer =
       vx::q8::BufferOf(w, 4U * static_cast<std::uint32_t>(n) * static_cast<std::uint32_t>(k));
-  const __amdgpu_buffer_rsrc_t x_buffer =
-      vx::q8::BufferOf(x, 4U * static_cast<std::uint32_t>(t) * static_cast<std::uint32_t>(k));
+  const __amdgpu_buffer_rsrc_t x_buffer = vx::q8::BufferOf(
+      x, 4U * static_cast<std::uint32_t>(t + halo) * static_cast<std::uint32_t>(k));
   const std::uint32_t w_at = 4U * static_cast<std::uint32_t>((n0 + r) * k + 4 * g);
   std::uint32_t x_at[MT];
   bool row_ok[MT];
@@ -221,63 +315,197 @@ __global__ __launch_bounds__(W * kWave) void F32SkinnyKernel(
   float alpha[kOut];
   float scale[kOut];
   float shift[kOut];
+  const auto load_epilogue = [&]() {  // beside the operands' loads
 #pragma unroll
-  for (int j = 0; j < kOut; ++j) {
-    const int e = static_cast<int>(threadIdx.x) + j * W * kWave;
-    const int l = e % kWave;
-    out_row[j] = e < MT * 4 * kWave ? 16 * (e / (4 * kWave)) + 4 * (l / 16) + (e / kWave) % 4 : t;
-    out_column[j] = n0 + l % 16;
-    const bool live = out_row[j] < t && out_column[j] < n;
-    prior[j] = __builtin_bit_cast(
-        float, vx::q8::BufferLoad4(
-                   y_buffer, 4U * static_cast<std::uint32_t>(out_row[j] * n + out_column[j]),
-                   live && accumulate != 0));
-    const std::uint32_t at = 4U * static_cast<std::uint32_t>(out_column[j] % unit.channels);
-    bias[j] = __builtin_bit_cast(
-        float, vx::q8::BufferLoad4(bias_buffer, at, live && windowed && unit.bias != nullptr));
-    alpha[j] = __builtin_bit_cast(float, vx::q8::BufferLoad4(alpha_buffer, at, live && windowed));
-    const bool block_live = live && windowed && block_input;
-    scale[j] = __builtin_bit_cast(float, vx::q8::BufferLoad4(scale_buffer, at, block_live));
-    shift[j] = __builtin_bit_cast(float, vx::q8::BufferLoad4(shift_buffer, at, block_live));
-  }
+    for (int j = 0; j < kOut; ++j) {
+      const int e = static_cast<int>(threadIdx.x) + j * W * kWave;
+      const int l = e % kWave;
+      out_row[j] =
+          e < MT * 4 * kWave ? 16 * (e / (4 * kWave)) + 4 * (l / 16) + (e / kWave) % 4 : t;
+      out_column[j] = n0 + l % 16;
+      const bool live = out_row[j] < t && out_column[j] < n;
+      prior[j] = __builtin_bit_cast(
+          float, vx::q8::BufferLoad4(
+                     y_buffer, 4U * static_cast<std::uint32_t>(out_row[j] * n + out_column[j]),
+                     live && accumulate != 0));
+      const std::uint32_t at = 4U * static_cast<std::uint32_t>(out_column[j] % unit.channels);
+      bias[j] = __builtin_bit_cast(
+          float, vx::q8::BufferLoad4(bias_buffer, at, live && windowed && unit.bias != nullptr));
+      alpha[j] =
+          __builtin_bit_cast(float, vx::q8::BufferLoad4(alpha_buffer, at, live && windowed));
+      const bool block_live = live && windowed && block_input;
+      scale[j] = __builtin_bit_cast(float, vx::q8::BufferLoad4(scale_buffer, at, block_live));
+      shift[j] = __builtin_bit_cast(float, vx::q8::BufferLoad4(shift_buffer, at, block_live));
+    }
+  };
+  load_epilogue();
   F32x4 acc[MT];
 #pragma unroll
   for (int m = 0; m < MT; ++m)
     acc[m] = F32x4{0.0F, 0.0F, 0.0F, 0.0F};
   const int groups = k / 16;
-  constexpr int kAhead = 4;
-  for (int base = wave; base < groups; base += W * kAhead) {
-    float4 wv[kAhead];
-    float4 xv[kAhead][MT];
+  const auto multiply = [&](const float4& wv, const float4 (&xv)[MT]) {
 #pragma unroll
-    for (int a = 0; a < kAhead; ++a) {
-      const int group = base + a * W;
-      const bool ok = group < groups;
+    for (int m = 0; m < MT; ++m) {
+      acc[m] = __builtin_amdgcn_mfma_f32_16x16x4f32(xv[m].x, wv.x, acc[m], 0, 0, 0);
+      acc[m] = __builtin_amdgcn_mfma_f32_16x16x4f32(xv[m].y, wv.y, acc[m], 0, 0, 0);
+      acc[m] = __builtin_amdgcn_mfma_f32_16x16x4f32(xv[m].z, wv.z, acc[m], 0, 0, 0);
+      acc[m] = __builtin_amdgcn_mfma_f32_16x16x4f32(xv[m].w, wv.w, acc[m], 0, 0, 0);
+    }
+  };
+  if constexpr (kDw) {
+    // One pass: the launch gives every wave at most KA groups of k. The
+    // weights' loads go out first, then the window's, then the operand is
+    // made into LDS while they arrive.
+    float4 wv[KA];
+#pragma unroll
+    for (int a = 0; a < KA; ++a) {
+      const int group = wave + a * W;
       wv[a] = __builtin_bit_cast(
           float4, vx::q8::BufferLoad16(w_buffer, w_at + 64U * static_cast<std::uint32_t>(group),
-                                       ok && column_ok));
-#pragma unroll
-      for (int m = 0; m < MT; ++m)
-        xv[a][m] = __builtin_bit_cast(
-            float4, vx::q8::BufferLoad16(x_buffer,
-                                         x_at[m] + 64U * static_cast<std::uint32_t>(group),
-                                         ok && row_ok[m]));
+                                       group < groups && column_ok));
     }
+    float* taps = staged;               // [9][k]: w_j for j < 7, then bias, then alpha
+    float* rows = staged + 9 * k;       // [16 MT][k + 4]
+    const int stride = k + 4;
+    const int tid = static_cast<int>(threadIdx.x);
+    constexpr int kThreadsW = W * kWave;
+    // Items: a quad of channels and up to four operand rows d apart
+    // (residue class rho of the rows mod d, run it), which read ten window
+    // rows d apart: (4 + 6) loads for four rows instead of 28. One item per
+    // thread in flight; the window's loads of the first go out before the
+    // tap table's barrier.
+    const int quads = k / 4;
+    const int runs = (16 * MT + 4 * d - 1) / (4 * d);
+    const int items = quads * d * runs;
+    float4 win[10];
+    int item_q = 0;
+    int item_row = 0;  // rho + 4 it d
+    const auto load_item = [&](int item) {
+      const bool live = item < items;
+      item_q = live ? item % quads : 0;
+      const int task = live ? item / quads : 0;
+      item_row = live ? task % d + 4 * (task / d) * d : 16 * MT;
 #pragma unroll
-    for (int a = 0; a < kAhead; ++a)
+      for (int l = 0; l < 10; ++l) {
+        const int row = item_row + l * d;
+        win[l] = __builtin_bit_cast(
+            float4, vx::q8::BufferLoad16(
+                        x_buffer, 4U * static_cast<std::uint32_t>(row * k + 4 * item_q),
+                        live && row < t + halo));
+      }
+    };
+    const auto make_item = [&]() {
+      if (item_row >= 16 * MT)
+        return;
+      const int c = 4 * item_q;
+      float4 sum[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        sum[i] = *reinterpret_cast<const float4*>(&taps[7 * k + c]);
+      // Tap by tap (each row's sum in tap order), one tap's weights live.
+#pragma unroll
+      for (int j = 0; j < kTaps; ++j) {
+        const float4 wj = *reinterpret_cast<const float4*>(&taps[j * k + c]);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          sum[i].x += wj.x * win[i + j].x;
+          sum[i].y += wj.y * win[i + j].y;
+          sum[i].z += wj.z * win[i + j].z;
+          sum[i].w += wj.w * win[i + j].w;
+        }
+      }
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int row = item_row + i * d;
+        if (row >= 16 * MT)
+          break;
+        *reinterpret_cast<float4*>(&rows[row * stride + c]) =
+            row < t ? sum[i] : float4{0.0F, 0.0F, 0.0F, 0.0F};
+      }
+    };
+    load_item(tid);
+    // The tap table: [c][7] in memory, tap-major in LDS.
+    const __amdgpu_buffer_rsrc_t taps_buffer =
+        vx::q8::BufferOf(dw.weights, 4U * kTaps * static_cast<std::uint32_t>(k));
+    const __amdgpu_buffer_rsrc_t dw_bias_buffer =
+        vx::q8::BufferOf(dw.bias, 4U * static_cast<std::uint32_t>(k));
+    const __amdgpu_buffer_rsrc_t dw_alpha_buffer =
+        vx::q8::BufferOf(dw.alpha, dw.alpha != nullptr ? 4U * static_cast<std::uint32_t>(k) : 0U);
+    for (int e = tid; e < kTaps * quads; e += kThreadsW) {
+      const float4 v = __builtin_bit_cast(
+          float4, vx::q8::BufferLoad16(taps_buffer, 16U * static_cast<std::uint32_t>(e), true));
+      const float parts[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+      for (int s = 0; s < 4; ++s) {
+        const int flat_tap = 4 * e + s;  // channel flat_tap / 7, tap flat_tap % 7
+        taps[(flat_tap % kTaps) * k + flat_tap / kTaps] = parts[s];
+      }
+    }
+    for (int e = tid; e < quads; e += kThreadsW) {
+      const std::uint32_t at = 16U * static_cast<std::uint32_t>(e);
+      *reinterpret_cast<uint4*>(&taps[7 * k + 4 * e]) =
+          vx::q8::BufferLoad16(dw_bias_buffer, at, true);
+      *reinterpret_cast<uint4*>(&taps[8 * k + 4 * e]) =
+          vx::q8::BufferLoad16(dw_alpha_buffer, at, dw.alpha != nullptr);
+    }
+    __syncthreads();
+    make_item();
+    for (int item = tid + kThreadsW; item < items; item += kThreadsW) {
+      load_item(item);
+      make_item();
+    }
+    __syncthreads();
+#pragma unroll
+    for (int a = 0; a < KA; ++a) {
+      const int group = wave + a * W;
+      if (group >= groups)
+        break;
+      // The second Snake as the operand is read: each element of the rows
+      // is read by one lane of one wave. Rows past t hold zero, and
+      // Snake(0) = 0.
+      const int c = 16 * group + 4 * g;
+      const float4 alpha4 = *reinterpret_cast<const float4*>(&taps[8 * k + c]);
+      float4 xv[MT];
 #pragma unroll
       for (int m = 0; m < MT; ++m) {
-        acc[m] = __builtin_amdgcn_mfma_f32_16x16x4f32(xv[a][m].x, wv[a].x, acc[m], 0, 0, 0);
-        acc[m] = __builtin_amdgcn_mfma_f32_16x16x4f32(xv[a][m].y, wv[a].y, acc[m], 0, 0, 0);
-        acc[m] = __builtin_amdgcn_mfma_f32_16x16x4f32(xv[a][m].z, wv[a].z, acc[m], 0, 0, 0);
-        acc[m] = __builtin_amdgcn_mfma_f32_16x16x4f32(xv[a][m].w, wv[a].w, acc[m], 0, 0, 0);
+        xv[m] = *reinterpret_cast<const float4*>(&rows[(16 * m + r) * stride + c]);
+        if (dw.alpha != nullptr)
+          xv[m] = float4{Snake(xv[m].x, alpha4.x), Snake(xv[m].y, alpha4.y),
+                         Snake(xv[m].z, alpha4.z), Snake(xv[m].w, alpha4.w)};
       }
+      multiply(wv[a], xv);
+    }
+    __syncthreads();  // the operand rows become the partial sums' LDS
+  } else {
+    for (int base = wave; base < groups; base += W * KA) {
+      float4 wv[KA];
+      float4 xv[KA][MT];
+#pragma unroll
+      for (int a = 0; a < KA; ++a) {
+        const int group = base + a * W;
+        const bool ok = group < groups;
+        wv[a] = __builtin_bit_cast(
+            float4, vx::q8::BufferLoad16(w_buffer, w_at + 64U * static_cast<std::uint32_t>(group),
+                                         ok && column_ok));
+#pragma unroll
+        for (int m = 0; m < MT; ++m)
+          xv[a][m] = __builtin_bit_cast(
+              float4, vx::q8::BufferLoad16(x_buffer,
+                                           x_at[m] + 64U * static_cast<std::uint32_t>(group),
+                                           ok && row_ok[m]));
+      }
+#pragma unroll
+      for (int a = 0; a < KA; ++a)
+        multiply(wv[a], xv[a]);
+    }
   }
+  float* reduce = kDw ? staged : &reduce_static[0][0][0][0];  // [W][MT][4][64]
 #pragma unroll
   for (int m = 0; m < MT; ++m)
 #pragma unroll
     for (int i = 0; i < 4; ++i)
-      reduce[wave][m][i][lane] = acc[m][i];
+      reduce[((wave * MT + m) * 4 + i) * kWave + lane] = acc[m][i];
   __syncthreads();
 #pragma unroll
   for (int j = 0; j < kOut; ++j) {
@@ -287,10 +515,10 @@ __global__ __launch_bounds__(W * kWave) void F32SkinnyKernel(
     const int m = e / (4 * kWave);
     const int i = (e / kWave) % 4;
     const int l = e % kWave;
-    float total = reduce[0][m][i][l];
+    float total = reduce[((0 * MT + m) * 4 + i) * kWave + l];
 #pragma unroll
     for (int v = 1; v < W; ++v)
-      total += reduce[v][m][i][l];
+      total += reduce[((v * MT + m) * 4 + i) * kWave + l];
     float v = accumulate != 0 ? prior[j] + total : total;
     const std::size_t at = static_cast<std::size_t>(out_row[j]) * n + out_column[j];
     if (windowed) {
@@ -351,10 +579,10 @@ __global__ __launch_bounds__(kTileThreads) void F32TileKernel(const float* x, co
   const int n0 = kTileRows * static_cast<int>(blockIdx.x);
   const int row0 = kTileRows * static_cast<int>(blockIdx.y);
   const bool block_input = unit.scale != nullptr;
-  if (unit.window != nullptr && blockIdx.y == 0) {
+  if (unit.window != nullptr) {  // spread over every workgroup of the grid
     float* head = unit.window + (block_input ? unit.channels : 0);
-    for (int e = static_cast<int>(blockIdx.x * blockDim.x) + tid; e < unit.head;
-         e += static_cast<int>(gridDim.x * blockDim.x))
+    for (int e = static_cast<int>((blockIdx.y * gridDim.x + blockIdx.x) * blockDim.x) + tid;
+         e < unit.head; e += static_cast<int>(gridDim.x * gridDim.y * blockDim.x))
       head[e] = unit.state[e];
   }
   const __amdgpu_buffer_rsrc_t w_buffer =
@@ -524,6 +752,42 @@ __global__ void RepackUpKernel(const float* up, float* w2, std::size_t in, std::
   w2[i] = up[(channel * out + o) * 2 * s + tap];
 }
 
+/// One F32SkinnyKernel launch's grid and arguments.
+struct SkinnyLaunch {
+  dim3 grid;
+  std::size_t lds = 0;  // dynamic LDS bytes: the fused operand's
+  hipStream_t stream = nullptr;
+  const float* x = nullptr;
+  const float* w = nullptr;
+  float* y = nullptr;
+  int t = 0;
+  int k = 0;
+  int n = 0;
+  int accumulate = 0;
+  UnitWindow unit;
+  DwOperand dw;
+};
+
+/// F32SkinnyKernel<MT, W, KA, fused> for `ka` groups per wave pass, fused
+/// when the launch carries a depthwise operand.
+template<int MT, int W>
+void LaunchSkinny(const SkinnyLaunch& l, int ka) {
+  const auto launch = [&](auto kernel) {
+    kernel<<<l.grid, W * kWave, l.lds, l.stream>>>(l.x, l.w, l.y, l.t, l.k, l.n, l.accumulate,
+                                                   l.unit, l.dw);
+  };
+  if (l.dw.weights != nullptr) {
+    if (ka == 2)
+      launch(F32SkinnyKernel<MT, W, 2, true>);
+    else
+      launch(F32SkinnyKernel<MT, W, 4, true>);
+  } else if (ka == 2) {
+    launch(F32SkinnyKernel<MT, W, 2, false>);
+  } else {
+    launch(F32SkinnyKernel<MT, W, 4, false>);
+  }
+}
+
 template<typename T>
 int Allocate(T** pointer, std::size_t count, const char* what) {
   if (hipMalloc(reinterpret_cast<void**>(pointer), std::max<std::size_t>(count, 1) * sizeof(T)) !=
@@ -567,6 +831,7 @@ struct vx_vae {
   float* next = nullptr;
   float* work = nullptr;
   float* scratch = nullptr;
+  float* scratch2 = nullptr;
   std::size_t capacity_frames = 0;
   GraphKey graph_key;
   hipGraphExec_t graph = nullptr;
@@ -583,7 +848,8 @@ struct vx_vae {
     }
     for (void* p : {static_cast<void*>(in_state), static_cast<void*>(out_state),
                     static_cast<void*>(hidden), static_cast<void*>(next),
-                    static_cast<void*>(work), static_cast<void*>(scratch)})
+                    static_cast<void*>(work), static_cast<void*>(scratch),
+                    static_cast<void*>(scratch2)})
       (void)hipFree(p);
   }
 
@@ -598,34 +864,70 @@ struct vx_vae {
            (t <= 32 || x_reads <= (std::size_t{32} << 20));
   }
 
+  /// A residual unit's depthwise convolution is made in its pointwise
+  /// product's operand loads (DwOperand) when the product takes
+  /// F32SkinnyKernel over at most 128 channels. Every 16-column workgroup
+  /// makes its row block's operand: at 256 and 512 channels (16 and 32
+  /// workgroups per row block) that measured slower than the separate
+  /// depthwise launch, at 32-128 channels faster (one patch of VoxCPM2's
+  /// decoder 284 -> 268 us).
+  static bool Fusable(std::size_t t, std::size_t k, std::size_t n) {
+    return k <= 128 && Skinny(t, k, n) && DwLdsFloats(k, 1) * sizeof(float) <= kDwLdsBytes &&
+           (t + (kTaps - 1) * kDilations[2]) * k * sizeof(float) < (std::size_t{1} << 32);
+  }
+
   /// With `unit.window` set, the product's epilogue also makes its
-  /// consumer's input. k a multiple of 4 (checked at create).
+  /// consumer's input. With `dw` (Fusable shapes only), x is a window
+  /// [6 d rows | t rows] and the operand is made from it. k a multiple of
+  /// 4 (checked at create).
   int Gemm(const float* x, const float* w, float* y, std::size_t t, std::size_t k, std::size_t n,
-           bool accumulate, hipStream_t stream, const UnitWindow& unit = UnitWindow{}) {
+           bool accumulate, hipStream_t stream, const UnitWindow& unit = UnitWindow{},
+           const DwOperand* dw = nullptr) {
+    if (dw != nullptr && !Fusable(t, k, n))
+      return vx::Fail(VX_UNSUPPORTED, "vx_vae_decode: fused operand shape");
     if (Skinny(t, k, n)) {
-      const int mt = t <= 16 ? 1 : 2;
+      int mt = t <= 16 ? 1 : 2;
+      if (dw != nullptr && DwLdsFloats(k, mt) * sizeof(float) > kDwLdsBytes)
+        mt = 1;
       const std::size_t groups = k / 16;
-      int waves = kF32Waves;  // at least two groups of k per wave
-      while (waves > 1 && groups < 2 * static_cast<std::size_t>(waves))
+      // At least two groups of k per wave; with a fused operand one group
+      // per wave up to 8 waves, whose threads then make it in about one
+      // round and whose workgroups fit two to a compute unit.
+      const std::size_t per_wave = dw != nullptr ? 1 : 2;
+      int waves = dw != nullptr ? kF32Waves / 2 : kF32Waves;
+      while (waves > 1 && groups < per_wave * static_cast<std::size_t>(waves))
         waves /= 2;
+      // Groups per wave pass: two where that covers k in one pass.
+      const int ka = groups <= 2 * static_cast<std::size_t>(waves) ? 2 : 4;
+      if (dw != nullptr && groups > static_cast<std::size_t>(waves) * ka)
+        return vx::Fail(VX_UNSUPPORTED, "vx_vae_decode: fused operand over one pass of k");
+      const std::size_t lds = dw != nullptr ? DwLdsFloats(k, mt) * sizeof(float) : 0;
       const dim3 grid(static_cast<unsigned>((n + 15) / 16),
                       static_cast<unsigned>((t + 16 * mt - 1) / (16 * mt)));
-      const auto launch = [&](auto kernel) {
-        kernel<<<grid, waves * kWave, 0, stream>>>(x, w, y, static_cast<int>(t),
-                                                   static_cast<int>(k), static_cast<int>(n),
-                                                   accumulate ? 1 : 0, unit);
-      };
+      const DwOperand none;
+      const SkinnyLaunch launch{grid,
+                                lds,
+                                stream,
+                                x,
+                                w,
+                                y,
+                                static_cast<int>(t),
+                                static_cast<int>(k),
+                                static_cast<int>(n),
+                                accumulate ? 1 : 0,
+                                unit,
+                                dw != nullptr ? *dw : none};
       switch (mt * 100 + waves) {
-        case 101: launch(F32SkinnyKernel<1, 1>); break;
-        case 102: launch(F32SkinnyKernel<1, 2>); break;
-        case 104: launch(F32SkinnyKernel<1, 4>); break;
-        case 108: launch(F32SkinnyKernel<1, 8>); break;
-        case 116: launch(F32SkinnyKernel<1, 16>); break;
-        case 201: launch(F32SkinnyKernel<2, 1>); break;
-        case 202: launch(F32SkinnyKernel<2, 2>); break;
-        case 204: launch(F32SkinnyKernel<2, 4>); break;
-        case 208: launch(F32SkinnyKernel<2, 8>); break;
-        default: launch(F32SkinnyKernel<2, 16>); break;
+        case 101: LaunchSkinny<1, 1>(launch, ka); break;
+        case 102: LaunchSkinny<1, 2>(launch, ka); break;
+        case 104: LaunchSkinny<1, 4>(launch, ka); break;
+        case 108: LaunchSkinny<1, 8>(launch, ka); break;
+        case 116: LaunchSkinny<1, 16>(launch, ka); break;
+        case 201: LaunchSkinny<2, 1>(launch, ka); break;
+        case 202: LaunchSkinny<2, 2>(launch, ka); break;
+        case 204: LaunchSkinny<2, 4>(launch, ka); break;
+        case 208: LaunchSkinny<2, 8>(launch, ka); break;
+        default: LaunchSkinny<2, 16>(launch, ka); break;
       }
       return VX_OK;
     }
@@ -652,7 +954,7 @@ struct vx_vae {
       widest = std::max(widest, t * b.out + 54 * b.out);
     }
     widest = std::max(widest, (t + kTaps) * out_channels);
-    for (float** p : {&hidden, &next, &work, &scratch}) {
+    for (float** p : {&hidden, &next, &work, &scratch, &scratch2}) {
       if (*p != nullptr)
         (void)hipFree(*p);
       *p = nullptr;
@@ -673,17 +975,20 @@ struct vx_vae {
     // buffers block by block (locals: every call starts from the same two).
     float* stream_rows = hidden;
     float* next_rows = next;
+    // The windows alternate between two buffers: a product whose operand
+    // is made from one window writes the next window into the other.
+    float* windows[2] = {scratch, scratch2};
     std::size_t t = frames;
-    StageKernel<<<Blocks((kTaps - 1 + t) * latent), kThreads, 0, stream>>>(in_state, latents,
-                                                                          work, t, latent);
-    DepthwiseKernel<<<Blocks(std::max(t, std::size_t{kTaps - 1}) * latent), kThreads, 0,
-                      stream>>>(work, weights.in_depthwise, weights.in_depthwise_bias, nullptr,
-                                scratch, in_state, t, latent, 1);
+    // The latents after their history, in the second window buffer: the
+    // input product writes the first block's input into work.
+    StageKernel<<<Blocks((kTaps - 1 + t) * latent), kThreads, 0, stream>>>(
+        in_state, latents, windows[1], t, latent);
     // Each product's epilogue makes its consumer's input: a block's input
-    // x2 (in work; unit 0's depthwise kernel then refreshes the block's
-    // state from x2's last frame), a unit's window (in scratch) or the
-    // output window (in scratch). The depthwise outputs go to the stream
-    // buffer the block's transposed convolution left behind.
+    // x2 (in work; unit 0 then refreshes the block's state from x2's last
+    // frame), a unit's window or the output window. Where a unit's
+    // depthwise convolution is not made in its product's operand loads, it
+    // writes into the stream buffer the block's transposed convolution
+    // left behind.
     const auto block_input_of = [&](const Block& b, const float* bias) {
       UnitWindow unit;
       unit.bias = bias;
@@ -697,52 +1002,82 @@ struct vx_vae {
       unit.frames = static_cast<int>(t);
       return unit;
     };
-    const auto window_of = [&](const float* alpha, float* state, int head_rows, std::size_t c,
-                               const float* bias) {
+    const auto window_of = [&](float* into, const float* alpha, float* state, int head_rows,
+                               std::size_t c, const float* bias) {
       UnitWindow unit;
       unit.bias = bias;
       unit.alpha = alpha;
-      unit.window = scratch;
+      unit.window = into;
       unit.state = state;
       unit.head = head_rows * static_cast<int>(c);
       unit.channels = static_cast<int>(c);
       return unit;
     };
-    VX_TRY(Gemm(scratch, weights.in_pointwise, stream_rows, t, latent, shape.decoder_dim, false,
-                stream, block_input_of(blocks.front(), weights.in_pointwise_bias)));
+    // A depthwise convolution (with Snake when alpha is set) of `window`
+    // feeding a product: in its operand loads where Fusable, else its own
+    // launch into next_rows.
+    const auto depthwise_product = [&](const float* window, const float* dw_w, const float* dw_b,
+                                       const float* dw_alpha, float* state, int d,
+                                       const float* copy_from, float* copy_to,
+                                       std::size_t copy_count, const float* w, float* y,
+                                       std::size_t k, std::size_t n, bool accumulate,
+                                       const UnitWindow& next) {
+      if (Fusable(t, k, n)) {
+        DwOperand op;
+        op.weights = dw_w;
+        op.bias = dw_b;
+        op.alpha = dw_alpha;
+        op.dilation = d;
+        op.state = state;
+        op.copy_from = copy_from;
+        op.copy_to = copy_to;
+        op.copy_count = static_cast<int>(copy_count);
+        return Gemm(window, w, y, t, k, n, accumulate, stream, next, &op);
+      }
+      const std::size_t rows = static_cast<std::size_t>(kTaps - 1) * d;
+      DepthwiseKernel<<<Blocks(std::max({t, rows, copy_count}) * k), kThreads, 0, stream>>>(
+          window, dw_w, dw_b, dw_alpha, next_rows, state, t, k, d, copy_from, copy_to,
+          copy_count);
+      return Gemm(next_rows, w, y, t, k, n, accumulate, stream, next);
+    };
+    VX_TRY(depthwise_product(windows[1], weights.in_depthwise, weights.in_depthwise_bias, nullptr,
+                             in_state, 1, nullptr, nullptr, 0, weights.in_pointwise, stream_rows,
+                             latent, shape.decoder_dim, false,
+                             block_input_of(blocks.front(), weights.in_pointwise_bias)));
     for (std::size_t bi = 0; bi < blocks.size(); ++bi) {
       Block& b = blocks[bi];
       const std::size_t t_in = t;
       const std::size_t c = b.out;
       VX_TRY(Gemm(work, b.up2, next_rows, t, 2 * b.in, b.stride * c, false, stream,
-                  window_of(b.w.units[0].alpha_in, b.unit_state[0], kTaps - 1, c, b.w.up_bias)));
+                  window_of(windows[0], b.w.units[0].alpha_in, b.unit_state[0], kTaps - 1, c,
+                            b.w.up_bias)));
       std::swap(stream_rows, next_rows);
       t *= b.stride;
       for (int u = 0; u < 3; ++u) {
         const vx_vae_unit& unit = b.w.units[u];
-        const int d = kDilations[u];
-        const std::size_t rows = static_cast<std::size_t>(kTaps - 1) * d;
         const bool refresh = u == 0;
-        DepthwiseKernel<<<Blocks(std::max(t, rows) * c), kThreads, 0, stream>>>(
-            scratch, unit.depthwise, unit.depthwise_bias, unit.alpha_out, next_rows,
-            b.unit_state[u], t, c, d, refresh ? work + (t_in - 1) * 2 * b.in : nullptr,
-            refresh ? b.state : nullptr, refresh ? b.in : 0);
         // The next consumer: unit u + 1, the next block's input or the output.
+        float* into = windows[(u + 1) % 2];
         UnitWindow next;
         if (u < 2) {
           const int dn = kDilations[u + 1];
-          next = window_of(b.w.units[u + 1].alpha_in, b.unit_state[u + 1], (kTaps - 1) * dn, c,
-                           unit.pointwise_bias);
+          next = window_of(into, b.w.units[u + 1].alpha_in, b.unit_state[u + 1],
+                           (kTaps - 1) * dn, c, unit.pointwise_bias);
         } else if (bi + 1 < blocks.size()) {
           next = block_input_of(blocks[bi + 1], unit.pointwise_bias);
         } else {
-          next = window_of(weights.out_alpha, out_state, kTaps - 1, c, unit.pointwise_bias);
+          next = window_of(into, weights.out_alpha, out_state, kTaps - 1, c,
+                           unit.pointwise_bias);
         }
-        VX_TRY(Gemm(next_rows, unit.pointwise, stream_rows, t, c, c, true, stream, next));
+        VX_TRY(depthwise_product(windows[u % 2], unit.depthwise, unit.depthwise_bias,
+                                 unit.alpha_out, b.unit_state[u], kDilations[u],
+                                 refresh ? work + (t_in - 1) * 2 * b.in : nullptr,
+                                 refresh ? b.state : nullptr, refresh ? b.in : 0, unit.pointwise,
+                                 stream_rows, c, c, true, next));
       }
     }
     const std::size_t c = out_channels;
-    float* out_window = scratch;
+    float* out_window = windows[1];  // the last unit's (u = 2) next window
     ToMonoKernel<<<static_cast<unsigned>((t + 3) / 4), kThreads, 0, stream>>>(
         out_window, weights.out_conv, weights.out_bias, samples, out_state, t, c);
     return vx::LaunchStatus("vx_vae_decode");
