@@ -4,8 +4,9 @@ vae_test compares streamed and at-once decoding, vae_test.cpp:114-138):
 chunks of latents decoded in turn equal the whole sequence decoded at
 once; a reset starts a new stream; graph replays with the same buffers
 match. Tolerance: float32 products in another summation order through
-the decoder's 25 layers, max |gpu - oracle| <= 2e-3 on samples in
-[-1, 1] (measured far below)."""
+the decoder's 25 layers and Snake on the hardware sine, max |gpu -
+oracle| <= 2e-3 on samples in [-1, 1] (measured 5.1e-6 small, 7.7e-4 at
+the VoxCPM2 shape)."""
 import numpy as np
 import pytest
 import torch

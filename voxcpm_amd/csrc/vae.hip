@@ -9,7 +9,7 @@
 // side by side, K = 2 in), and three residual units (Snake, dilated
 // depthwise conv fused with the second Snake, pointwise product added into
 // the stream), then Snake and the 7-tap convolution to mono with tanh.
-// Over at most 128 channels (and for the latents' input convolutions) the
+// Over at most 256 channels (and for the latents' input convolutions) the
 // depthwise convolution and its Snake are made in the pointwise product's
 // operand loads, staged through LDS, and the units' windows alternate
 // between two buffers; wider units keep a depthwise launch.
@@ -49,8 +49,14 @@ dim3 Blocks(std::size_t count) {
   return dim3(static_cast<unsigned>((count + kThreads - 1) / kThreads));
 }
 
+/// Snake(y) = y + sin^2(a y) / (a + 1e-9). The sine is the hardware's
+/// (v_sin_f32 takes turns: sin(2 pi r)) of a y in turns reduced to
+/// [-1/2, 1/2]: the decoder evaluates Snake on every element of every unit
+/// and block input, and the library sine's range reduction and polynomial
+/// made the units' products bound by their vector instructions.
 __device__ inline float Snake(float y, float a) {
-  const float s = sinf(a * y);
+  const float turns = a * y * 0.159154943091895336F;  // 1 / (2 pi)
+  const float s = __builtin_amdgcn_sinf(turns - rintf(turns));
   return y + (1.0F / (a + 1e-9F)) * (s * s);
 }
 
@@ -866,13 +872,14 @@ struct vx_vae {
 
   /// A residual unit's depthwise convolution is made in its pointwise
   /// product's operand loads (DwOperand) when the product takes
-  /// F32SkinnyKernel over at most 128 channels. Every 16-column workgroup
-  /// makes its row block's operand: at 256 and 512 channels (16 and 32
-  /// workgroups per row block) that measured slower than the separate
-  /// depthwise launch, at 32-128 channels faster (one patch of VoxCPM2's
-  /// decoder 284 -> 268 us).
+  /// F32SkinnyKernel over at most 256 channels. Every 16-column workgroup
+  /// makes its row block's operand: at 512 channels (32 workgroups per row
+  /// block) that measured slower than the separate depthwise launch, at
+  /// 32-256 channels faster (one patch of VoxCPM2's decoder 284 -> 268 us
+  /// up to 128 channels with the library sine in Snake, 251 -> 249 us
+  /// adding 256 with the hardware sine).
   static bool Fusable(std::size_t t, std::size_t k, std::size_t n) {
-    return k <= 128 && Skinny(t, k, n) && DwLdsFloats(k, 1) * sizeof(float) <= kDwLdsBytes &&
+    return k <= 256 && Skinny(t, k, n) && DwLdsFloats(k, 1) * sizeof(float) <= kDwLdsBytes &&
            (t + (kTaps - 1) * kDilations[2]) * k * sizeof(float) < (std::size_t{1} << 32);
   }
 
