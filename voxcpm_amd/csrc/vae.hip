@@ -893,10 +893,15 @@ struct vx_vae {
     if (dw != nullptr && !Fusable(t, k, n))
       return vx::Fail(VX_UNSUPPORTED, "vx_vae_decode: fused operand shape");
     if (Skinny(t, k, n)) {
-      // One 16-row tile per workgroup up to 32 rows (twice the workgroups
-      // of a 32-row tile, each with half the operand loads: one patch of
-      // VoxCPM2's decoder 247.7 -> 245.9 us); 32-row tiles beyond.
-      int mt = t <= 32 ? 1 : 2;
+      // One 16-row tile per workgroup up to 16 rows, and up to 32 while
+      // the tiles still take one workgroup per compute unit (twice the
+      // workgroups of 32-row tiles, each with half the operand loads:
+      // block 0's units 8.2 -> 6.2-7.2 us; where the second round of
+      // workgroups would load more per compute unit than 32-row tiles, as
+      // block 1's transposed convolution, 14.0 -> 17.7 us); 32-row tiles
+      // beyond.
+      const std::size_t column_tiles = (n + 15) / 16;
+      int mt = t <= 16 || (t <= 32 && 2 * column_tiles <= 256) ? 1 : 2;
       if (dw != nullptr && DwLdsFloats(k, mt) * sizeof(float) > kDwLdsBytes)
         mt = 1;
       const std::size_t groups = k / 16;
