@@ -147,15 +147,19 @@ __global__ void DepthwiseKernel(const float* work, const float* w, const float* 
 
 /// samples[f] = tanh(b + sum_c sum_j w[c][j] work[f + j][c]), one
 /// workgroup per 4 frames, lanes over channels; also state = work's last
-/// 6 rows (this kernel never reads the state).
+/// 6 rows (this kernel never reads the state) and copy_to = copy_from
+/// (copy_count floats: the latents' history, which the first product of
+/// the chunk read).
 __global__ void ToMonoKernel(const float* work, const float* w, float b, float* samples,
-                             float* state, std::size_t t, std::size_t c) {
+                             float* state, std::size_t t, std::size_t c,
+                             const float* copy_from, float* copy_to, int copy_count) {
   __shared__ float partial[kThreads / kWave];
   const std::size_t first = static_cast<std::size_t>(blockIdx.x) * 4;
   const int lane = static_cast<int>(threadIdx.x) % kWave;
   const int wave = static_cast<int>(threadIdx.x) / kWave;  // frame first + wave
-  SideCopies<1> copies;  // the state refresh, loaded beside the window
+  SideCopies<2> copies;  // the state refreshes, loaded beside the window
   copies.Add(0, state, work + t * c, static_cast<int>((kTaps - 1) * c));
+  copies.Add(1, copy_to, copy_from, copy_count);
   copies.Load();
   const std::size_t f = first + wave;
   float sum = 0.0F;
@@ -225,6 +229,10 @@ struct DwOperand {
   const float* alpha = nullptr;    // [c], or null
   int dilation = 1;
   float* state = nullptr;          // [6 d][c]
+  // When set, the window's first 6 d rows come from here and the rest from
+  // x ([t][c]); `state` is then a buffer of its own, which a later kernel
+  // copies into head.
+  const float* head = nullptr;
   const float* copy_from = nullptr;
   float* copy_to = nullptr;
   int copy_count = 0;
@@ -270,10 +278,15 @@ __global__ __launch_bounds__(W * kWave) void F32SkinnyKernel(
     for (int e = flat; e < unit.head; e += grid_threads)
       head[e] = unit.state[e];
   }
+  const float* x_all = x;  // before this workgroup's row offset
+  const int t_all_rows_outer = t;
   if constexpr (kDw) {
-    const float* last = x + static_cast<std::size_t>(t) * k;  // the window's last 6 d rows
+    // The window's last 6 d rows: window element t k + e.
+    const int last = t * k;
     for (int e = flat; e < halo * k; e += grid_threads)
-      dw.state[e] = last[e];
+      dw.state[e] = dw.head == nullptr ? x[last + e]
+                    : last + e < halo * k ? dw.head[last + e]
+                                          : x[last + e - halo * k];
     for (int e = flat; e < dw.copy_count; e += grid_threads)
       dw.copy_to[e] = dw.copy_from[e];
   }
@@ -384,6 +397,11 @@ __global__ __launch_bounds__(W * kWave) void F32SkinnyKernel(
     const int quads = k / 4;
     const int runs = (16 * MT + 4 * d - 1) / (4 * d);
     const int items = quads * d * runs;
+    const int t_all_rows = t_all_rows_outer;
+    const __amdgpu_buffer_rsrc_t head_buffer = vx::q8::BufferOf(
+        dw.head, dw.head != nullptr ? 4U * static_cast<std::uint32_t>(halo * k) : 0U);
+    const __amdgpu_buffer_rsrc_t x_all_buffer = vx::q8::BufferOf(
+        x_all, dw.head != nullptr ? 4U * static_cast<std::uint32_t>(t_all_rows * k) : 0U);
     float4 win[10];
     int item_q = 0;
     int item_row = 0;  // rho + 4 it d
@@ -392,13 +410,34 @@ __global__ __launch_bounds__(W * kWave) void F32SkinnyKernel(
       item_q = live ? item % quads : 0;
       const int task = live ? item / quads : 0;
       item_row = live ? task % d + 4 * (task / d) * d : 16 * MT;
+      if (dw.head == nullptr) {
 #pragma unroll
-      for (int l = 0; l < 10; ++l) {
-        const int row = item_row + l * d;
-        win[l] = __builtin_bit_cast(
-            float4, vx::q8::BufferLoad16(
-                        x_buffer, 4U * static_cast<std::uint32_t>(row * k + 4 * item_q),
-                        live && row < t + halo));
+        for (int l = 0; l < 10; ++l) {
+          const int row = item_row + l * d;
+          win[l] = __builtin_bit_cast(
+              float4, vx::q8::BufferLoad16(
+                          x_buffer, 4U * static_cast<std::uint32_t>(row * k + 4 * item_q),
+                          live && row < t + halo));
+        }
+      } else {
+        // Window row w (of the whole window) from the head below 6 d, else
+        // row w - 6 d of x: one of the two loads is masked to zero and the
+        // row is their sum (a select kept the pair in scratch memory).
+#pragma unroll
+        for (int l = 0; l < 10; ++l) {
+          const int w = row0 + item_row + l * d;
+          const float4 from_head = __builtin_bit_cast(
+              float4, vx::q8::BufferLoad16(
+                          head_buffer, 4U * static_cast<std::uint32_t>(w * k + 4 * item_q),
+                          live && w < halo));
+          const float4 from_x = __builtin_bit_cast(
+              float4,
+              vx::q8::BufferLoad16(
+                  x_all_buffer, 4U * static_cast<std::uint32_t>((w - halo) * k + 4 * item_q),
+                  live && w >= halo && w - halo < t_all_rows));
+          win[l] = float4{from_head.x + from_x.x, from_head.y + from_x.y,
+                          from_head.z + from_x.z, from_head.w + from_x.w};
+        }
       }
     };
     const auto make_item = [&]() {
@@ -832,6 +871,7 @@ struct vx_vae {
   std::size_t out_channels = 0;
   std::size_t hop = 1;
   float* in_state = nullptr;   // [6][latent]
+  float* in_state_next = nullptr;  // [6][latent]: the next chunk's, copied in at the end
   float* out_state = nullptr;  // [6][out_channels]
   float* hidden = nullptr;
   float* next = nullptr;
@@ -852,7 +892,8 @@ struct vx_vae {
       for (float* s : b.unit_state)
         (void)hipFree(s);
     }
-    for (void* p : {static_cast<void*>(in_state), static_cast<void*>(out_state),
+    for (void* p : {static_cast<void*>(in_state), static_cast<void*>(in_state_next),
+                    static_cast<void*>(out_state),
                     static_cast<void*>(hidden), static_cast<void*>(next),
                     static_cast<void*>(work), static_cast<void*>(scratch),
                     static_cast<void*>(scratch2)})
@@ -994,10 +1035,6 @@ struct vx_vae {
     // is made from one window writes the next window into the other.
     float* windows[2] = {scratch, scratch2};
     std::size_t t = frames;
-    // The latents after their history, in the second window buffer: the
-    // input product writes the first block's input into work.
-    StageKernel<<<Blocks((kTaps - 1 + t) * latent), kThreads, 0, stream>>>(
-        in_state, latents, windows[1], t, latent);
     // Each product's epilogue makes its consumer's input: a block's input
     // x2 (in work; unit 0 then refreshes the block's state from x2's last
     // frame), a unit's window or the output window. Where a unit's
@@ -1055,10 +1092,29 @@ struct vx_vae {
           copy_count);
       return Gemm(next_rows, w, y, t, k, n, accumulate, stream, next);
     };
-    VX_TRY(depthwise_product(windows[1], weights.in_depthwise, weights.in_depthwise_bias, nullptr,
-                             in_state, 1, nullptr, nullptr, 0, weights.in_pointwise, stream_rows,
-                             latent, shape.decoder_dim, false,
-                             block_input_of(blocks.front(), weights.in_pointwise_bias)));
+    // The latents' depthwise (no Snake) and pointwise convolutions. Where
+    // Fusable the product reads its window from the latents' history and
+    // the latents themselves, and leaves the next chunk's history in
+    // in_state_next, which the last launch copies into in_state; else the
+    // latents are staged after their history in the second window buffer.
+    const bool input_fused = Fusable(t, latent, shape.decoder_dim);
+    if (input_fused) {
+      DwOperand op;
+      op.weights = weights.in_depthwise;
+      op.bias = weights.in_depthwise_bias;
+      op.dilation = 1;
+      op.state = in_state_next;
+      op.head = in_state;
+      VX_TRY(Gemm(latents, weights.in_pointwise, stream_rows, t, latent, shape.decoder_dim, false,
+                  stream, block_input_of(blocks.front(), weights.in_pointwise_bias), &op));
+    } else {
+      StageKernel<<<Blocks((kTaps - 1 + t) * latent), kThreads, 0, stream>>>(
+          in_state, latents, windows[1], t, latent);
+      VX_TRY(depthwise_product(windows[1], weights.in_depthwise, weights.in_depthwise_bias,
+                               nullptr, in_state, 1, nullptr, nullptr, 0, weights.in_pointwise,
+                               stream_rows, latent, shape.decoder_dim, false,
+                               block_input_of(blocks.front(), weights.in_pointwise_bias)));
+    }
     for (std::size_t bi = 0; bi < blocks.size(); ++bi) {
       Block& b = blocks[bi];
       const std::size_t t_in = t;
@@ -1094,7 +1150,9 @@ struct vx_vae {
     const std::size_t c = out_channels;
     float* out_window = windows[1];  // the last unit's (u = 2) next window
     ToMonoKernel<<<static_cast<unsigned>((t + 3) / 4), kThreads, 0, stream>>>(
-        out_window, weights.out_conv, weights.out_bias, samples, out_state, t, c);
+        out_window, weights.out_conv, weights.out_bias, samples, out_state, t, c,
+        input_fused ? in_state_next : nullptr, input_fused ? in_state : nullptr,
+        input_fused ? static_cast<int>((kTaps - 1) * latent) : 0);
     return vx::LaunchStatus("vx_vae_decode");
   }
 };
@@ -1173,6 +1231,9 @@ int vx_vae_create(vx_vae** vae, const vx_vae_shape* shape, const vx_vae_weights*
   created->out_channels = c;
   if (status == VX_OK)
     status = Allocate(&created->in_state, (kTaps - 1) * shape->latent_dim, "vx_vae: hipMalloc");
+  if (status == VX_OK)
+    status = Allocate(&created->in_state_next, (kTaps - 1) * shape->latent_dim,
+                      "vx_vae: hipMalloc");
   if (status == VX_OK)
     status = Allocate(&created->out_state, (kTaps - 1) * c, "vx_vae: hipMalloc");
   if (status == VX_OK && hipDeviceSynchronize() != hipSuccess)
