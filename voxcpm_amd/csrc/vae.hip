@@ -54,11 +54,14 @@ dim3 Blocks(std::size_t count) {
 /// [-1/2, 1/2]: the decoder evaluates Snake on every element of every unit
 /// and block input, and the library sine's range reduction and polynomial
 /// made the units' products bound by their vector instructions.
-__device__ inline float Snake(float y, float a) {
+__device__ inline float SnakeScale(float a) { return 1.0F / (a + 1e-9F); }
+/// Snake with the channel's 1 / (a + 1e-9) given (the same value).
+__device__ inline float Snake(float y, float a, float inverse) {
   const float turns = a * y * 0.159154943091895336F;  // 1 / (2 pi)
   const float s = __builtin_amdgcn_sinf(turns - rintf(turns));
-  return y + (1.0F / (a + 1e-9F)) * (s * s);
+  return y + inverse * (s * s);
 }
+__device__ inline float Snake(float y, float a) { return Snake(y, a, SnakeScale(a)); }
 
 /// Up to N copies (to[e] = from[e], e < count) spread over every thread of
 /// a grid: each thread's first element is loaded by Load() beside the
@@ -238,10 +241,11 @@ struct DwOperand {
   int copy_count = 0;
 };
 
-/// Floats of dynamic LDS a fused unit operand takes: the tap table [9][k]
-/// (seven taps, bias, alpha) and the operand rows [16 MT][k + 4].
+/// Floats of dynamic LDS a fused unit operand takes: the tap table [10][k]
+/// (seven taps, bias, alpha, Snake's 1 / (alpha + 1e-9)) and the operand
+/// rows [16 MT][k + 4].
 constexpr std::size_t DwLdsFloats(std::size_t k, int mt) {
-  return 9 * k + static_cast<std::size_t>(16 * mt) * (k + 4);
+  return 10 * k + static_cast<std::size_t>(16 * mt) * (k + 4);
 }
 constexpr std::size_t kDwLdsBytes = 60 * 1024;  // under the default 64 KiB
 
@@ -384,8 +388,9 @@ __global__ __launch_bounds__(W * kWave) void F32SkinnyKernel(
           float4, vx::q8::BufferLoad16(w_buffer, w_at + 64U * static_cast<std::uint32_t>(group),
                                        group < groups && column_ok));
     }
-    float* taps = staged;               // [9][k]: w_j for j < 7, then bias, then alpha
-    float* rows = staged + 9 * k;       // [16 MT][k + 4]
+    // [10][k]: w_j for j < 7, then bias, alpha and Snake's 1 / (alpha + 1e-9)
+    float* taps = staged;
+    float* rows = staged + 10 * k;      // [16 MT][k + 4]
     const int stride = k + 4;
     const int tid = static_cast<int>(threadIdx.x);
     constexpr int kThreadsW = W * kWave;
@@ -491,8 +496,11 @@ __global__ __launch_bounds__(W * kWave) void F32SkinnyKernel(
       const std::uint32_t at = 16U * static_cast<std::uint32_t>(e);
       *reinterpret_cast<uint4*>(&taps[7 * k + 4 * e]) =
           vx::q8::BufferLoad16(dw_bias_buffer, at, true);
-      *reinterpret_cast<uint4*>(&taps[8 * k + 4 * e]) =
-          vx::q8::BufferLoad16(dw_alpha_buffer, at, dw.alpha != nullptr);
+      const float4 a = __builtin_bit_cast(
+          float4, vx::q8::BufferLoad16(dw_alpha_buffer, at, dw.alpha != nullptr));
+      *reinterpret_cast<float4*>(&taps[8 * k + 4 * e]) = a;
+      *reinterpret_cast<float4*>(&taps[9 * k + 4 * e]) =
+          float4{SnakeScale(a.x), SnakeScale(a.y), SnakeScale(a.z), SnakeScale(a.w)};
     }
     __syncthreads();
     make_item();
@@ -511,13 +519,16 @@ __global__ __launch_bounds__(W * kWave) void F32SkinnyKernel(
       // Snake(0) = 0.
       const int c = 16 * group + 4 * g;
       const float4 alpha4 = *reinterpret_cast<const float4*>(&taps[8 * k + c]);
+      const float4 inverse4 = *reinterpret_cast<const float4*>(&taps[9 * k + c]);
       float4 xv[MT];
 #pragma unroll
       for (int m = 0; m < MT; ++m) {
         xv[m] = *reinterpret_cast<const float4*>(&rows[(16 * m + r) * stride + c]);
         if (dw.alpha != nullptr)
-          xv[m] = float4{Snake(xv[m].x, alpha4.x), Snake(xv[m].y, alpha4.y),
-                         Snake(xv[m].z, alpha4.z), Snake(xv[m].w, alpha4.w)};
+          xv[m] = float4{Snake(xv[m].x, alpha4.x, inverse4.x),
+                         Snake(xv[m].y, alpha4.y, inverse4.y),
+                         Snake(xv[m].z, alpha4.z, inverse4.z),
+                         Snake(xv[m].w, alpha4.w, inverse4.w)};
       }
       multiply(wv[a], xv);
     }
