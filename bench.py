@@ -938,6 +938,8 @@ def main() -> int:
     parser.add_argument("--lm-step-workload", action="store_true",
                         help="only run the stacks' decode steps and the AudioVAE "
                              "(for kernel traces)")
+    parser.add_argument("--vae-workload", action="store_true",
+                        help="only run the AudioVAE's patch decodes (for counter runs)")
     args = parser.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
@@ -970,6 +972,9 @@ def main() -> int:
         return 0
     if args.lm_step_workload:
         gpu_lm_step(args, torch, ops, synth, device, stream)
+        gpu_vae(args, torch, ops, synth, device, stream)
+        return 0
+    if args.vae_workload:
         gpu_vae(args, torch, ops, synth, device, stream)
         return 0
 
