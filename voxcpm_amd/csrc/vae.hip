@@ -49,13 +49,14 @@ dim3 Blocks(std::size_t count) {
   return dim3(static_cast<unsigned>((count + kThreads - 1) / kThreads));
 }
 
-/// Snake(y) = y + sin^2(a y) / (a + 1e-9). The sine is the hardware's
-/// (v_sin_f32 takes turns: sin(2 pi r)) of a y in turns reduced to
-/// [-1/2, 1/2]: the decoder evaluates Snake on every element of every unit
-/// and block input, and the library sine's range reduction and polynomial
-/// made the units' products bound by their vector instructions.
+/// A channel's 1 / (a + 1e-9) in Snake.
 __device__ inline float SnakeScale(float a) { return 1.0F / (a + 1e-9F); }
-/// Snake with the channel's 1 / (a + 1e-9) given (the same value).
+/// Snake(y) = y + sin^2(a y) / (a + 1e-9), `inverse` the channel's
+/// SnakeScale(a). The sine is the hardware's (v_sin_f32 takes turns:
+/// sin(2 pi r)) of a y in turns reduced to [-1/2, 1/2]: the decoder
+/// evaluates Snake on every element of every unit and block input, and the
+/// library sine's range reduction and polynomial made the units' products
+/// bound by their vector instructions.
 __device__ inline float Snake(float y, float a, float inverse) {
   const float turns = a * y * 0.159154943091895336F;  // 1 / (2 pi)
   const float s = __builtin_amdgcn_sinf(turns - rintf(turns));
@@ -257,7 +258,7 @@ __global__ __launch_bounds__(W * kWave) void F32SkinnyKernel(
     UnitWindow unit, DwOperand dw) {
   // The waves' partial sums; with kDw they meet in the operand rows' LDS.
   __shared__ float reduce_static[kDw ? 1 : W][MT][4][kWave];
-  extern __shared__ float staged[];  // kDw: tap table [9][k], operand rows [16 MT][k + 4]
+  extern __shared__ float staged[];  // kDw: tap table [10][k], operand rows [16 MT][k + 4]
   const int lane = static_cast<int>(threadIdx.x) % kWave;
   const int wave = static_cast<int>(threadIdx.x) / kWave;
   const int r = lane % 16;
@@ -283,7 +284,7 @@ __global__ __launch_bounds__(W * kWave) void F32SkinnyKernel(
       head[e] = unit.state[e];
   }
   const float* x_all = x;  // before this workgroup's row offset
-  const int t_all_rows_outer = t;
+  const int all_rows = t;
   if constexpr (kDw) {
     // The window's last 6 d rows: window element t k + e.
     const int last = t * k;
@@ -402,11 +403,10 @@ __global__ __launch_bounds__(W * kWave) void F32SkinnyKernel(
     const int quads = k / 4;
     const int runs = (16 * MT + 4 * d - 1) / (4 * d);
     const int items = quads * d * runs;
-    const int t_all_rows = t_all_rows_outer;
     const __amdgpu_buffer_rsrc_t head_buffer = vx::q8::BufferOf(
         dw.head, dw.head != nullptr ? 4U * static_cast<std::uint32_t>(halo * k) : 0U);
     const __amdgpu_buffer_rsrc_t x_all_buffer = vx::q8::BufferOf(
-        x_all, dw.head != nullptr ? 4U * static_cast<std::uint32_t>(t_all_rows * k) : 0U);
+        x_all, dw.head != nullptr ? 4U * static_cast<std::uint32_t>(all_rows * k) : 0U);
     float4 win[10];
     int item_q = 0;
     int item_row = 0;  // rho + 4 it d
@@ -439,7 +439,7 @@ __global__ __launch_bounds__(W * kWave) void F32SkinnyKernel(
               float4,
               vx::q8::BufferLoad16(
                   x_all_buffer, 4U * static_cast<std::uint32_t>((w - halo) * k + 4 * item_q),
-                  live && w >= halo && w - halo < t_all_rows));
+                  live && w >= halo && w - halo < all_rows));
           win[l] = float4{from_head.x + from_x.x, from_head.y + from_x.y,
                           from_head.z + from_x.z, from_head.w + from_x.w};
         }
@@ -971,6 +971,8 @@ struct vx_vae {
       const std::size_t lds = dw != nullptr ? DwLdsFloats(k, mt) * sizeof(float) : 0;
       const dim3 grid(static_cast<unsigned>((n + 15) / 16),
                       static_cast<unsigned>((t + 16 * mt - 1) / (16 * mt)));
+      if ((t + 16 * mt - 1) / (16 * mt) > 65535)
+        return vx::Fail(VX_UNSUPPORTED, "vx_vae_decode: more row blocks than grid rows");
       const DwOperand none;
       const SkinnyLaunch launch{grid,
                                 lds,
