@@ -20,7 +20,12 @@ BOUND = 2e-3
 # "small" and "odd" take channel counts that are not multiples of 16 (8;
 # 24 and 12): their products go to the LDS-tiled float32 kernel
 # (F32TileKernel), whose epilogue makes the next inputs (unit windows, a
-# block's input, the output window) as the 16-column kernel's does.
+# block's input, the output window) as the 16-column kernel's does. Units
+# of at most 256 channels (and the latents' input convolutions) make their
+# depthwise convolution in the pointwise product's operand loads; chunks
+# of 1, 5 and 2 frames at the VoxCPM2 shape take one- and two-tile row
+# blocks and latents' histories that mix the previous chunk's rows with
+# this chunk's (fewer than 6 frames).
 CONFIGS = {
     "small": synth.VaeConfig(latent=16, decoder_dim=64, rates=(3, 2, 2)),
     "odd": synth.VaeConfig(latent=16, decoder_dim=48, rates=(2, 2)),
@@ -29,7 +34,8 @@ CONFIGS = {
 
 
 @pytest.mark.parametrize("name,chunks", [("small", (4, 4, 1)), ("small", (9,)),
-                                         ("odd", (3, 2, 5)), ("voxcpm2", (4, 4))])
+                                         ("odd", (3, 2, 5)), ("voxcpm2", (4, 4)),
+                                         ("voxcpm2", (1, 5, 2))])
 def test_vae_streaming_decode_against_oracle(vx, oracle, cuda, stream, name, chunks):
     config = CONFIGS[name]
     weights = synth.vae_weights(config, 91)
