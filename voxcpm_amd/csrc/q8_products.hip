@@ -346,6 +346,10 @@ EngineLauncher EnginePw(int pw, int m) {
     if (pw == 2)
       return EngineJr<MT, RG, 2, WK>(m);
   }
+  if constexpr (MT == 3 && WK == q8::Weights::kQ8) {
+    if (pw == 2)
+      return EngineJr<MT, RG, 2, WK>(m);
+  }
   return pw == 1 ? EngineJr<MT, RG, 1, WK>(m) : nullptr;
 }
 
@@ -565,6 +569,13 @@ ProductPlan PlanEngine(std::size_t m, std::size_t k, std::size_t n, q8::Weights 
   } else if (plan.mt == 2 && plan.rg == 1 && pairs >= 2 * plan.waves && kind == q8::Weights::kQ8) {
     // One row group, two or more pairs per 16-wave workgroup's wave: two in
     // flight ((2048, 2048) with two row blocks: 4.79 -> 4.69 us).
+    plan.pw = 2;
+  }
+  if (plan.mt == 3 && kind == q8::Weights::kQ8 && pairs >= 2 * plan.waves) {
+    // 33-48 rows over more than 256 row groups (one block of three tiles):
+    // two pairs in flight per wave (measured on MI355X at 44 rows:
+    // (1024, 8192) 6.81 -> 6.44 us, (2048, 16384) 14.36 -> 14.02 us; the
+    // same at 64 rows in blocks of four tiles measured slower).
     plan.pw = 2;
   }
   plan.splits = 1;
