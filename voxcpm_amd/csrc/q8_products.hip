@@ -516,7 +516,17 @@ ProductPlan PlanEngine(std::size_t m, std::size_t k, std::size_t n, q8::Weights 
     // (1024, 8192) 21.1 -> 10.6 us, (2048, 2048) 14.0 -> 7.6 us against the
     // engine on all 128 rows; (2048, 16384) 29.2 -> 28.8 us against the
     // LDS-tiled kernel.
-    return PlanRowBlocks(m, k, n);
+    ProductPlan blocks = PlanRowBlocks(m, k, n);
+    if (kind == q8::Weights::kQ8 && q8::Groups(n) > 256) {
+      // Exact arithmetic over more than 256 row groups: four per workgroup
+      // (measured on MI355X at 128 rows: (1024, 8192) 10.95 -> 10.65 us,
+      // (2048, 16384) 29.9 -> 29.0 us against two).
+      blocks.rg = 4;
+      blocks.tiles = static_cast<int>((q8::Groups(n) + 3) / 4);
+      blocks.waves = q8::EngineThreads(blocks.mt, blocks.rg) / kWave;
+      blocks.pairs_per_wave = (blocks.pairs_per_split + blocks.waves - 1) / blocks.waves;
+    }
+    return blocks;
   }
   plan.engine = true;
   const int groups = static_cast<int>(q8::Groups(n));
