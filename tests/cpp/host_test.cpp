@@ -202,14 +202,14 @@ void TestLinear(std::size_t in, std::size_t out, Random& rng,
   Report(threw, "unsupported weight format throws GpuError");
 }
 
-/// Bf16Gemm::Linear of 320 x 4096 x 2048 takes the expanded path's plan
+/// Bf16Gemm::Linear of 320 x 6144 x 2048 takes the expanded path's plan
 /// that splits k (its grid has few tiles): the operator's scratch holds the
 /// split's partial sums, as the reference's State owns its partials
 /// (gemm.cpp:95-98). The result is bit for bit vx_q8_linear's with a
 /// scratch that size, whose plan splits (and without one would not), and
 /// within 1e-4 of the expanded arithmetic (products_test.cpp:301-309).
 void TestPrefillSplit(Random& rng, hipStream_t stream) {
-  const std::size_t rows = 320, in = 4096, out = 2048;
+  const std::size_t rows = 320, in = 6144, out = 2048;
   const auto blocks = Weights(out, in, rng);
   const auto packed = Pack(blocks, out, in);
   const auto x = Activations(rows, in, rng, 2.0);
@@ -222,7 +222,7 @@ void TestPrefillSplit(Random& rng, hipStream_t stream) {
   vc::CheckVx(vx_q8_prefill_plan(rows, in, out, scratch, plan), "plan");
   vc::CheckVx(vx_q8_prefill_plan(rows, in, out, nullptr, bare), "plan");
   Report(plan[3] > 1 && bare[3] == 1,
-         "prefill 320 x 4096 x 2048 plan: " + std::to_string(plan[3]) +
+         "prefill 320 x 6144 x 2048 plan: " + std::to_string(plan[3]) +
              " splits with the scratch, " + std::to_string(bare[3]) + " without");
   vc::DeviceBuffer<float> y(rows * out);
   vc::DeviceBuffer<float> reference(rows * out);
@@ -237,9 +237,9 @@ void TestPrefillSplit(Random& rng, hipStream_t stream) {
   const auto result = Download(y.get(), y.size());
   const auto expected = Download(reference.get(), reference.size());
   Report(std::memcmp(result.data(), expected.data(), result.size() * sizeof(float)) == 0,
-         "Bf16Gemm::Linear 320 x 4096 x 2048 equals the split plan's product bit for bit");
+         "Bf16Gemm::Linear 320 x 6144 x 2048 equals the split plan's product bit for bit");
   const double worst = ExpandedError(result, x, blocks, nullptr, rows, in, out);
-  Report(worst <= 1e-4, "Bf16Gemm::Linear 320 x 4096 x 2048 (split k): worst " +
+  Report(worst <= 1e-4, "Bf16Gemm::Linear 320 x 6144 x 2048 (split k): worst " +
                             Scientific(worst));
 }
 

@@ -19,7 +19,7 @@ from voxcpm_amd import _lib, ops, synth  # noqa: E402
 
 def main() -> int:
     device = torch.device("cuda:0")
-    m, k, n = 320, 4096, 2048  # the tiled plan splits k four ways here
+    m, k, n = 320, 6144, 2048  # the tiled plan splits k four ways here
     rng = synth.Rng(202, m + n)
     blocks = synth.q8_blocks(rng, n, k)
     packed = ops.q8_pack(torch.from_numpy(blocks).to(device), n, k)

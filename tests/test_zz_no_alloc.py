@@ -37,7 +37,7 @@ def test_noalloc_product_matches_scratch_product(vx, oracle, cuda, stream):
     scratch = vx.Scratch(128, 16384)
     stream_handle = torch.cuda.current_stream().cuda_stream
     # Both tiled calls split k (4 splits of 80 tiles of 64 x 128).
-    for m, k, n in [(320, 4096, 2048), (300, 4096, 2048), (22, 1024, 4096)]:
+    for m, k, n in [(320, 6144, 2048), (300, 6144, 2048), (22, 1024, 4096)]:
         print(f"noalloc product m={m} k={k} n={n}", flush=True)
         if m > 128:
             plan = (ctypes.c_int32 * 4)()

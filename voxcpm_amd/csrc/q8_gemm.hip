@@ -485,10 +485,11 @@ GemmPlan PlanGemm(std::size_t m, std::size_t k, std::size_t n, std::size_t parti
     return plan;
   }
   // Measured on MI355X over m 129..1024, k 2048, n 2048..16384: 256 x 256
-  // tiles (two steps prefetched) once they fill the compute units, else
-  // 256 x 128 tiles, k split while the grid has fewer than 192
-  // workgroups and the partial sums fit the scratch.
-  if (tiles(256, 256) >= 256) {
+  // tiles (two steps prefetched) once they fill three quarters of the
+  // compute units (768 x 2048 x 16384: 70.5 -> 58.8 us against 256 x 128
+  // tiles), else 256 x 128 tiles, k split while the grid has fewer than
+  // 192 workgroups and the partial sums fit the scratch.
+  if (tiles(256, 256) >= 192) {
     plan.shape = 4;
   } else {
     plan.shape = 3;
@@ -505,7 +506,11 @@ GemmPlan PlanGemm(std::size_t m, std::size_t k, std::size_t n, std::size_t parti
   return plan;
 }
 
-bool UseGemm(std::size_t m, std::size_t n) { return m >= 512 && n >= 6144; }
+// From 512 rows over 6144 or more columns, and from 384 rows over 16384 or
+// more (384 x 2048 x 16384: 44.5 -> 39.1 us against the tiled kernel).
+bool UseGemm(std::size_t m, std::size_t n) {
+  return (m >= 512 && n >= 6144) || (m >= 384 && n >= 16384);
+}
 
 int RunGemm(const Bf16* x, const void* w, float* y, Bf16* y_bf16, std::size_t m, std::size_t k,
             std::size_t n, bool accumulate, bool bf16_weights, float* partials,

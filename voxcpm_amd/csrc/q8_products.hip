@@ -723,12 +723,15 @@ bool UseRowBlocks(std::size_t m, std::size_t k, std::size_t n, bool q8) {
   // where each 64-row block re-reads the weights. Q8_0 panels of up to
   // 2048 x 6144 values also up to 256 rows (129 x 2048 x 6144 24.2 -> 16.1
   // us, 256 x 6144 x 2048 25.8 -> 23.6 us; 256 x 2048 x 4096 and
-  // 256 x 1024 x 8192 on a par); bf16 panels lost there.
+  // 256 x 1024 x 8192 on a par), and up to 512 rows while k is at most
+  // 4096 (384 / 512 x 2048 x 6144 32.3 / 33.3 -> 25.4 / 30.6 us, 320 x
+  // 4096 x 2048 25.4 -> 20.7 us; 512 x 6144 x 2048 36.8 -> 40.0 us, so not
+  // there); bf16 panels lost there.
   if (m <= kExactRows)
     return false;
   const double work = static_cast<double>(m) * static_cast<double>(k) * static_cast<double>(n);
   return work <= 1.2e9 || (m <= 512 && k >= 2048 && k * n <= 2048 * 2048) ||
-         (q8 && m <= 256 && k * n <= 2048 * 6144);
+         (q8 && k * n <= 2048 * 6144 && (m <= 256 || (m <= 512 && k <= 4096)));
 }
 
 int RunRowBlocks(const Bf16* x, const void* w, float* y, Bf16* y_bf16, std::size_t m,
