@@ -911,11 +911,13 @@ struct vx_vae {
       (void)hipFree(p);
   }
 
-  /// y[t][n] (+)= x[t][k] W[n][k]^T. F32SkinnyKernel where k is whole
-  /// groups of 16 and its workgroups re-read at most 32 MiB of x between
-  /// them (one x read per 16 columns): every product of VoxCPM2's decoder
-  /// but block 2's transposed convolution (192 rows x 2048 over 1280
-  /// columns), which F32TileKernel tiles in both dimensions.
+  /// y[t][n] (+)= x[t][k] W[n][k]^T. F32SkinnyKernel can take it where k
+  /// is whole groups of 16 and its workgroups re-read at most 32 MiB of x
+  /// between them (one x read per 16 columns): every product of VoxCPM2's
+  /// decoder but block 2's transposed convolution (192 rows x 2048 over
+  /// 1280 columns), which F32TileKernel tiles in both dimensions (Gemm
+  /// also gives the tile kernel the unfused products it fills the compute
+  /// units with).
   static bool Skinny(std::size_t t, std::size_t k, std::size_t n) {
     const std::size_t x_reads = t * k * sizeof(float) * ((n + 15) / 16);
     return k % 16 == 0 && n * k * sizeof(float) < (std::size_t{1} << 32) &&
@@ -944,7 +946,14 @@ struct vx_vae {
            const DwOperand* dw = nullptr) {
     if (dw != nullptr && !Fusable(t, k, n))
       return vx::Fail(VX_UNSUPPORTED, "vx_vae_decode: fused operand shape");
-    if (Skinny(t, k, n)) {
+    // Over 32 rows an unfused product whose 32 x 32 tiles fill three
+    // quarters of the 256 compute units takes F32TileKernel, which reads x
+    // once per 32 columns instead of once per 16: blocks 3-5's transposed
+    // convolutions (240 tiles) 9.16 / 6.68 / 5.92 -> 7.68 / 6.34 / 5.60 us,
+    // where block 1's units (96 tiles) measured 5.6-5.8 -> 6.2-6.4 us.
+    const std::size_t tiles = ((n + kTileRows - 1) / kTileRows) * ((t + kTileRows - 1) / kTileRows);
+    const bool tiled = dw == nullptr && t > 32 && tiles >= 192;
+    if (Skinny(t, k, n) && !tiled) {
       // One 16-row tile per workgroup up to 16 rows, and up to 32 while
       // the tiles still take one workgroup per compute unit (twice the
       // workgroups of 32-row tiles, each with half the operand loads:
