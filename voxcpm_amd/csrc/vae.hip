@@ -963,21 +963,33 @@ struct vx_vae {
       // beyond.
       const std::size_t column_tiles = (n + 15) / 16;
       int mt = t <= 16 || (t <= 32 && 2 * column_tiles <= 256) ? 1 : 2;
-      if (dw != nullptr && DwLdsFloats(k, mt) * sizeof(float) > kDwLdsBytes)
+      // A fused operand of at most 32 channels takes 16-row tiles too:
+      // block 5's units (32 channels, 7680 rows) 7.1-7.6 -> 6.6-6.8 us, where
+      // block 4's (64 channels) measured 6.6-7.8 -> 7.2-8.2 us.
+      if (dw != nullptr && (k <= 32 || DwLdsFloats(k, mt) * sizeof(float) > kDwLdsBytes))
         mt = 1;
       const std::size_t groups = k / 16;
       // At least two groups of k per wave; with a fused operand one group
-      // per wave up to 8 waves, whose threads then make it in about one
-      // round and whose workgroups fit two to a compute unit.
+      // per wave from 4 up to 8 waves, whose threads then make it in about
+      // one round and whose workgroups fit two to a compute unit (waves
+      // past the groups make operand rows and outputs only: block 5's
+      // units, two groups of k, 7.8-8.3 -> 7.1-7.6 us with four waves
+      // instead of two; eight measured slower).
       const std::size_t per_wave = dw != nullptr ? 1 : 2;
       int waves = dw != nullptr ? kF32Waves / 2 : kF32Waves;
-      while (waves > 1 && groups < per_wave * static_cast<std::size_t>(waves))
+      const int fewest_waves = dw != nullptr ? 4 : 1;
+      while (waves > fewest_waves && groups < per_wave * static_cast<std::size_t>(waves))
         waves /= 2;
       // Groups per wave pass: two where that covers k in one pass.
       const int ka = groups <= 2 * static_cast<std::size_t>(waves) ? 2 : 4;
       if (dw != nullptr && groups > static_cast<std::size_t>(waves) * ka)
         return vx::Fail(VX_UNSUPPORTED, "vx_vae_decode: fused operand over one pass of k");
-      const std::size_t lds = dw != nullptr ? DwLdsFloats(k, mt) * sizeof(float) : 0;
+      // The waves' partial sums reuse the fused operand's LDS.
+      const std::size_t lds =
+          dw != nullptr ? std::max(DwLdsFloats(k, mt),
+                                   static_cast<std::size_t>(waves * mt * 4 * kWave)) *
+                              sizeof(float)
+                        : 0;
       const dim3 grid(static_cast<unsigned>((n + 15) / 16),
                       static_cast<unsigned>((t + 16 * mt - 1) / (16 * mt)));
       if ((t + 16 * mt - 1) / (16 * mt) > 65535)
