@@ -149,35 +149,56 @@ __global__ void DepthwiseKernel(const float* work, const float* w, const float* 
   copies.Store();
 }
 
-/// samples[f] = tanh(b + sum_c sum_j w[c][j] work[f + j][c]), one
-/// workgroup per 4 frames, lanes over channels; also state = work's last
+/// samples[f] = tanh(b + sum_c sum_j w[c][j] work[f + j][c]) with `lanes`
+/// lanes per frame (a power of two up to 64, at least c / 4 where it can
+/// be): lane q takes channel quads q, q + lanes, .., each with one 16-byte
+/// load per tap and its four channels' 28 taps as seven 16-byte loads, and
+/// the frame's lanes add their sums by butterfly. Also state = work's last
 /// 6 rows (this kernel never reads the state) and copy_to = copy_from
 /// (copy_count floats: the latents' history, which the first product of
-/// the chunk read).
+/// the chunk read). c a multiple of 4.
 __global__ void ToMonoKernel(const float* work, const float* w, float b, float* samples,
-                             float* state, std::size_t t, std::size_t c,
+                             float* state, std::size_t t, std::size_t c, int lanes,
                              const float* copy_from, float* copy_to, int copy_count) {
-  __shared__ float partial[kThreads / kWave];
-  const std::size_t first = static_cast<std::size_t>(blockIdx.x) * 4;
-  const int lane = static_cast<int>(threadIdx.x) % kWave;
-  const int wave = static_cast<int>(threadIdx.x) / kWave;  // frame first + wave
+  const std::size_t i = static_cast<std::size_t>(blockIdx.x) * blockDim.x + threadIdx.x;
   SideCopies<2> copies;  // the state refreshes, loaded beside the window
   copies.Add(0, state, work + t * c, static_cast<int>((kTaps - 1) * c));
   copies.Add(1, copy_to, copy_from, copy_count);
   copies.Load();
-  const std::size_t f = first + wave;
+  const std::size_t f = i / static_cast<std::size_t>(lanes);
+  const int q = static_cast<int>(i % static_cast<std::size_t>(lanes));
+  const int quads = static_cast<int>(c / 4);
   float sum = 0.0F;
   if (f < t)
-    for (std::size_t ch = lane; ch < c; ch += kWave)
+    for (int quad = q; quad < quads; quad += lanes) {
+      // Channel 4 quad + s's taps are taps[7 s .. 7 s + 6].
+      const float4* packed =
+          reinterpret_cast<const float4*>(w + static_cast<std::size_t>(quad) * 4 * kTaps);
+      float taps[4 * kTaps];
+#pragma unroll
+      for (int e = 0; e < kTaps; ++e) {
+        const float4 v = packed[e];
+        taps[4 * e] = v.x;
+        taps[4 * e + 1] = v.y;
+        taps[4 * e + 2] = v.z;
+        taps[4 * e + 3] = v.w;
+      }
+      float4 rows[kTaps];
 #pragma unroll
       for (int j = 0; j < kTaps; ++j)
-        sum += w[ch * kTaps + j] * work[(f + j) * c + ch];
-  sum = vx::WaveSum(sum);
-  if (lane == 0)
-    partial[wave] = sum;
-  __syncthreads();
-  if (threadIdx.x < 4 && first + threadIdx.x < t)
-    samples[first + threadIdx.x] = tanhf(partial[threadIdx.x] + b);
+        rows[j] = *reinterpret_cast<const float4*>(work + (f + j) * c + 4 * quad);
+#pragma unroll
+      for (int j = 0; j < kTaps; ++j) {
+        sum += taps[j] * rows[j].x;
+        sum += taps[kTaps + j] * rows[j].y;
+        sum += taps[2 * kTaps + j] * rows[j].z;
+        sum += taps[3 * kTaps + j] * rows[j].w;
+      }
+    }
+  for (int offset = lanes / 2; offset > 0; offset /= 2)
+    sum += __shfl_xor(sum, offset, kWave);
+  if (q == 0 && f < t)
+    samples[f] = tanhf(sum + b);
   copies.Store();
 }
 
@@ -1121,7 +1142,7 @@ struct vx_vae {
         return Gemm(window, w, y, t, k, n, accumulate, stream, next, &op);
       }
       const std::size_t rows = static_cast<std::size_t>(kTaps - 1) * d;
-      DepthwiseKernel<<<Blocks(std::max({t, rows, copy_count}) * k), kThreads, 0, stream>>>(
+      DepthwiseKernel<<<Blocks(std::max({t * k, rows * k, copy_count})), kThreads, 0, stream>>>(
           window, dw_w, dw_b, dw_alpha, next_rows, state, t, k, d, copy_from, copy_to,
           copy_count);
       return Gemm(next_rows, w, y, t, k, n, accumulate, stream, next);
@@ -1183,10 +1204,14 @@ struct vx_vae {
     }
     const std::size_t c = out_channels;
     float* out_window = windows[1];  // the last unit's (u = 2) next window
-    ToMonoKernel<<<static_cast<unsigned>((t + 3) / 4), kThreads, 0, stream>>>(
-        out_window, weights.out_conv, weights.out_bias, samples, out_state, t, c,
-        input_fused ? in_state_next : nullptr, input_fused ? in_state : nullptr,
-        input_fused ? static_cast<int>((kTaps - 1) * latent) : 0);
+    int lanes = 1;
+    while (lanes < kWave && 4 * static_cast<std::size_t>(lanes) < c)
+      lanes *= 2;
+    const std::size_t copy_floats = input_fused ? (kTaps - 1) * latent : 0;
+    ToMonoKernel<<<Blocks(std::max({t * lanes, (kTaps - 1) * c, copy_floats})), kThreads, 0,
+                   stream>>>(out_window, weights.out_conv, weights.out_bias, samples, out_state,
+                             t, c, lanes, input_fused ? in_state_next : nullptr,
+                             input_fused ? in_state : nullptr, static_cast<int>(copy_floats));
     return vx::LaunchStatus("vx_vae_decode");
   }
 };
