@@ -632,12 +632,19 @@ __global__ __launch_bounds__(W * kWave) void F32SkinnyKernel(
 // and step s of four multiplies slot 16 j + 4 g + s. Rows are 68 floats
 // apart in LDS: the 16 rows of a read fall on two passes of the 32 banks.
 // The epilogue is F32SkinnyKernel's (bias, unit window or block input).
+//
+// With a grid of S > 1 along z, workgroup z takes the z-th of S runs of
+// k (whole stages) and stores its sums into y + z t n, with no epilogue;
+// SplitSumKernel adds the S partial products in split order and applies
+// the epilogue.
 
 constexpr int kTileRows = 32;
 constexpr int kTileK = 128;
 constexpr int kTileStride = kTileK + 4;
 constexpr int kTileThreads = 512;
 constexpr int kTileDepth = 2;
+constexpr std::size_t kMaxSplits = 4;     // k splits of a few-row tile product
+constexpr std::size_t kSplitK = 2048;     // least k that splits
 
 __global__ __launch_bounds__(kTileThreads) void F32TileKernel(const float* x, const float* w, float* y,
                                                      int t, int k, int n, int accumulate,
@@ -655,6 +662,12 @@ __global__ __launch_bounds__(kTileThreads) void F32TileKernel(const float* x, co
   const int g = lane / 16;
   const int n0 = kTileRows * static_cast<int>(blockIdx.x);
   const int row0 = kTileRows * static_cast<int>(blockIdx.y);
+  // This workgroup's run of k: all of it, or split z of gridDim.z.
+  const int splits = static_cast<int>(gridDim.z);
+  const int run = ((k + splits - 1) / splits + kTileK - 1) / kTileK * kTileK;
+  const int k_begin = static_cast<int>(blockIdx.z) * run;
+  const int k_end = min(k, k_begin + run);
+  y += static_cast<std::size_t>(blockIdx.z) * t * n;
   const bool block_input = unit.scale != nullptr;
   if (unit.window != nullptr) {  // spread over every workgroup of the grid
     float* head = unit.window + (block_input ? unit.channels : 0);
@@ -677,8 +690,8 @@ __global__ __launch_bounds__(kTileThreads) void F32TileKernel(const float* x, co
     for (int h = 0; h < 2; ++h) {
       const int q = tid + kTileThreads * h;
       const int row = q / 32;
-      const int column = k0 + 4 * (q % 32);
-      const bool k_ok = column < k;
+      const int column = k_begin + k0 + 4 * (q % 32);
+      const bool k_ok = column < k_end;
       v.x[h] = __builtin_bit_cast(
           float4, vx::q8::BufferLoad16(
                       x_buffer, 4U * static_cast<std::uint32_t>((row0 + row) * k + column),
@@ -735,7 +748,7 @@ __global__ __launch_bounds__(kTileThreads) void F32TileKernel(const float* x, co
   }
 
   F32x4 acc = F32x4{0.0F, 0.0F, 0.0F, 0.0F};
-  const int stages = (k + kTileK - 1) / kTileK;
+  const int stages = k_end > k_begin ? (k_end - k_begin + kTileK - 1) / kTileK : 0;
   // kTileDepth stages' loads in flight: a stage's products take far less
   // time than a load's round trip.
   StageRegs regs[kTileDepth];
@@ -829,6 +842,47 @@ __global__ void RepackUpKernel(const float* up, float* w2, std::size_t in, std::
   w2[i] = up[(channel * out + o) * 2 * s + tap];
 }
 
+/// y[i] (+)= sum over s < splits of partials[s][i], s in order, for the t x
+/// n output, then the epilogue of the products (bias, unit window or block
+/// input; UnitWindow), a thread per element.
+__global__ void SplitSumKernel(const float* partials, int splits, float* y, int t, int n,
+                               int accumulate, UnitWindow unit) {
+  const int i = static_cast<int>(blockIdx.x * blockDim.x + threadIdx.x);
+  const bool block_input = unit.scale != nullptr;
+  const bool windowed = unit.window != nullptr;
+  if (windowed) {  // the next window's history, spread over the grid
+    float* head = unit.window + (block_input ? unit.channels : 0);
+    for (int e = i; e < unit.head; e += static_cast<int>(gridDim.x * blockDim.x))
+      head[e] = unit.state[e];
+  }
+  if (i >= t * n)
+    return;
+  const std::size_t count = static_cast<std::size_t>(t) * n;
+  float v = partials[i];
+  for (int s = 1; s < splits; ++s)
+    v += partials[s * count + i];
+  if (accumulate != 0)
+    v = y[i] + v;
+  if (windowed) {
+    const int row = i / n;
+    const int column = i % n;
+    const int channel = column % unit.channels;
+    if (unit.bias != nullptr)
+      v += unit.bias[channel];
+    if (block_input) {
+      // The output is [frames][channels]: frame row, channel column.
+      const float u = Snake(v * unit.scale[channel] + unit.shift[channel], unit.alpha[channel]);
+      const std::size_t c = static_cast<std::size_t>(unit.channels);
+      unit.window[static_cast<std::size_t>(row) * 2 * c + column] = u;
+      if (row + 1 < unit.frames)
+        unit.window[static_cast<std::size_t>(row + 1) * 2 * c + c + column] = u;
+    } else {
+      unit.window[unit.head + i] = Snake(v, unit.alpha[channel]);
+    }
+  }
+  y[i] = v;
+}
+
 /// One F32SkinnyKernel launch's grid and arguments.
 struct SkinnyLaunch {
   dim3 grid;
@@ -910,6 +964,7 @@ struct vx_vae {
   float* work = nullptr;
   float* scratch = nullptr;
   float* scratch2 = nullptr;
+  float* partials = nullptr;  // [kMaxSplits][t][n] of split products
   std::size_t capacity_frames = 0;
   GraphKey graph_key;
   hipGraphExec_t graph = nullptr;
@@ -928,7 +983,7 @@ struct vx_vae {
                     static_cast<void*>(out_state),
                     static_cast<void*>(hidden), static_cast<void*>(next),
                     static_cast<void*>(work), static_cast<void*>(scratch),
-                    static_cast<void*>(scratch2)})
+                    static_cast<void*>(scratch2), static_cast<void*>(partials)})
       (void)hipFree(p);
   }
 
@@ -974,7 +1029,17 @@ struct vx_vae {
     // where block 1's units (96 tiles) measured 5.6-5.8 -> 6.2-6.4 us.
     const std::size_t tiles = ((n + kTileRows - 1) / kTileRows) * ((t + kTileRows - 1) / kTileRows);
     const bool tiled = dw == nullptr && t > 32 && tiles >= 192;
-    if (Skinny(t, k, n) && !tiled) {
+    // A product of at most 32 rows whose 16-column workgroups would not
+    // fill the compute units, over k of at least kSplitK, splits k over
+    // the tile kernel's 32 x 32 tiles instead (each split reading x once
+    // per 32 columns), up to kMaxSplits and 384 workgroups, and a second
+    // launch adds the splits.
+    const std::size_t column_tiles16 = (n + 15) / 16;
+    std::size_t splits = 1;
+    if (dw == nullptr && t <= 32 && column_tiles16 < 256 && k >= kSplitK)
+      while (splits < kMaxSplits && tiles * 2 * splits <= 384 && k / (2 * splits) >= 256)
+        splits *= 2;
+    if (Skinny(t, k, n) && !tiled && splits == 1) {
       // One 16-row tile per workgroup up to 16 rows, and up to 32 while
       // the tiles still take one workgroup per compute unit (twice the
       // workgroups of 32-row tiles, each with half the operand loads:
@@ -1046,10 +1111,20 @@ struct vx_vae {
         t * n * sizeof(float) >= (std::size_t{1} << 32))
       return vx::Fail(VX_UNSUPPORTED, "vx_vae_decode: product shape");
     const dim3 grid(static_cast<unsigned>((n + kTileRows - 1) / kTileRows),
-                    static_cast<unsigned>((t + kTileRows - 1) / kTileRows));
-    F32TileKernel<<<grid, kTileThreads, 0, stream>>>(x, w, y, static_cast<int>(t),
-                                                     static_cast<int>(k), static_cast<int>(n),
-                                                     accumulate ? 1 : 0, unit);
+                    static_cast<unsigned>((t + kTileRows - 1) / kTileRows),
+                    static_cast<unsigned>(splits));
+    if (splits == 1) {
+      F32TileKernel<<<grid, kTileThreads, 0, stream>>>(x, w, y, static_cast<int>(t),
+                                                       static_cast<int>(k), static_cast<int>(n),
+                                                       accumulate ? 1 : 0, unit);
+      return VX_OK;
+    }
+    F32TileKernel<<<grid, kTileThreads, 0, stream>>>(x, w, partials, static_cast<int>(t),
+                                                     static_cast<int>(k), static_cast<int>(n), 0,
+                                                     UnitWindow{});
+    SplitSumKernel<<<Blocks(std::max(t * n, static_cast<std::size_t>(unit.head))), kThreads, 0,
+                     stream>>>(partials, static_cast<int>(splits), y, static_cast<int>(t),
+                               static_cast<int>(n), accumulate ? 1 : 0, unit);
     return VX_OK;
   }
 
@@ -1065,11 +1140,13 @@ struct vx_vae {
       widest = std::max(widest, t * b.out + 54 * b.out);
     }
     widest = std::max(widest, (t + kTaps) * out_channels);
-    for (float** p : {&hidden, &next, &work, &scratch, &scratch2}) {
+    for (float** p : {&hidden, &next, &work, &scratch, &scratch2, &partials}) {
       if (*p != nullptr)
         (void)hipFree(*p);
       *p = nullptr;
-      VX_TRY(Allocate(p, widest + (kTaps - 1) * shape.latent_dim, "vx_vae: hipMalloc"));
+      const std::size_t copies = p == &partials ? kMaxSplits : 1;
+      VX_TRY(Allocate(p, copies * (widest + (kTaps - 1) * shape.latent_dim),
+                      "vx_vae: hipMalloc"));
     }
     capacity_frames = frames;
     if (graph != nullptr) {
