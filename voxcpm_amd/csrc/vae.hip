@@ -49,6 +49,14 @@ dim3 Blocks(std::size_t count) {
   return dim3(static_cast<unsigned>((count + kThreads - 1) / kThreads));
 }
 
+// One-wave workgroups for the per-element launches between the products:
+// spread over more compute units they end sooner (a patch's six depthwise
+// launches 1.0 us faster than with 256 threads, 2.1 us slower with 1024).
+constexpr int kWaveThreads = kWave;
+dim3 WaveBlocks(std::size_t count) {
+  return dim3(static_cast<unsigned>((count + kWaveThreads - 1) / kWaveThreads));
+}
+
 /// A channel's 1 / (a + 1e-9) in Snake.
 __device__ inline float SnakeScale(float a) { return 1.0F / (a + 1e-9F); }
 /// Snake(y) = y + sin^2(a y) / (a + 1e-9), `inverse` the channel's
@@ -1219,7 +1227,8 @@ struct vx_vae {
         return Gemm(window, w, y, t, k, n, accumulate, stream, next, &op);
       }
       const std::size_t rows = static_cast<std::size_t>(kTaps - 1) * d;
-      DepthwiseKernel<<<Blocks(std::max({t * k, rows * k, copy_count})), kThreads, 0, stream>>>(
+      DepthwiseKernel<<<WaveBlocks(std::max({t * k, rows * k, copy_count})), kWaveThreads, 0,
+                        stream>>>(
           window, dw_w, dw_b, dw_alpha, next_rows, state, t, k, d, copy_from, copy_to,
           copy_count);
       return Gemm(next_rows, w, y, t, k, n, accumulate, stream, next);
