@@ -91,6 +91,31 @@ def test_vae_chunk_limit(vx, cuda):
     assert info.value.status == _lib.VX_BAD_ARG
 
 
+def test_vae_longest_chunk(vx, cuda):
+    """A chunk of vx_vae_max_frames frames at the VoxCPM2 shape (1092: its
+    32-row blocks fill the grid's 65535 rows at the output rate) decodes,
+    and equals the same latents decoded in chunks of 16 frames (vae.cpp
+    streams chunk by chunk; the two take different tilings, so the bound is
+    the oracle tolerance)."""
+    config = CONFIGS["voxcpm2"]
+    weights = synth.vae_weights(config, 97)
+    whole = vx.Vae(weights)
+    frames = whole.max_frames
+    assert frames == 65535 * 32 // config.hop
+    rng = synth.Rng(98, frames)
+    latents = torch.from_numpy(
+        rng.normal(frames * config.latent).astype(np.float32).reshape(frames, config.latent)
+    ).to(cuda)
+    print(f"longest chunk: {frames} frames", flush=True)
+    at_once = whole.decode(latents).cpu().numpy()
+    chunked = vx.Vae(weights)
+    pieces = [chunked.decode(latents[at:at + 16]).cpu().numpy() for at in range(0, frames, 16)]
+    error = float(np.max(np.abs(at_once - np.concatenate(pieces))))
+    print(f"longest chunk against 16-frame chunks: max |d| {error:.2e}", flush=True)
+    assert np.all(np.isfinite(at_once))
+    assert error <= BOUND
+
+
 def test_vae_decode_argument_checks(vx, cuda):
     """The C ABI takes bare pointers: Vae.decode refuses tensors whose bytes
     are not float32 [frames][latent] rows (bf16, strided, wrong width) and

@@ -1057,10 +1057,12 @@ struct vx_vae {
       // beyond.
       const std::size_t column_tiles = (n + 15) / 16;
       int mt = t <= 16 || (t <= 32 && 2 * column_tiles <= 256) ? 1 : 2;
-      // A fused operand of at most 32 channels takes 16-row tiles too:
-      // block 5's units (32 channels, 7680 rows) 7.1-7.6 -> 6.6-6.8 us, where
-      // block 4's (64 channels) measured 6.6-7.8 -> 7.2-8.2 us.
-      if (dw != nullptr && (k <= 32 || DwLdsFloats(k, mt) * sizeof(float) > kDwLdsBytes))
+      // A fused operand of at most 32 channels takes 16-row tiles too, while
+      // their row blocks fit the grid's rows: block 5's units (32 channels,
+      // 7680 rows) 7.1-7.6 -> 6.6-6.8 us, where block 4's (64 channels)
+      // measured 6.6-7.8 -> 7.2-8.2 us.
+      if (dw != nullptr && ((k <= 32 && (t + 15) / 16 <= 65535) ||
+                            DwLdsFloats(k, mt) * sizeof(float) > kDwLdsBytes))
         mt = 1;
       const std::size_t groups = k / 16;
       // At least two groups of k per wave; with a fused operand one group
