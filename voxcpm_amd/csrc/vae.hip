@@ -850,44 +850,25 @@ __global__ void RepackUpKernel(const float* up, float* w2, std::size_t in, std::
   w2[i] = up[(channel * out + o) * 2 * s + tap];
 }
 
-/// y[i] (+)= sum over s < splits of partials[s][i], s in order, for the t x
-/// n output, then the epilogue of the products (bias, unit window or block
-/// input; UnitWindow), a thread per element.
+/// y[i] = sum over s < splits of partials[s][i], s in order, for the t x n
+/// output of a product into a residual unit's window, then that epilogue
+/// (UnitWindow: bias, y, and Snake into the window after its history,
+/// which is copied here too), a thread per element.
 __global__ void SplitSumKernel(const float* partials, int splits, float* y, int t, int n,
-                               int accumulate, UnitWindow unit) {
+                               UnitWindow unit) {
   const int i = static_cast<int>(blockIdx.x * blockDim.x + threadIdx.x);
-  const bool block_input = unit.scale != nullptr;
-  const bool windowed = unit.window != nullptr;
-  if (windowed) {  // the next window's history, spread over the grid
-    float* head = unit.window + (block_input ? unit.channels : 0);
-    for (int e = i; e < unit.head; e += static_cast<int>(gridDim.x * blockDim.x))
-      head[e] = unit.state[e];
-  }
+  for (int e = i; e < unit.head; e += static_cast<int>(gridDim.x * blockDim.x))
+    unit.window[e] = unit.state[e];
   if (i >= t * n)
     return;
   const std::size_t count = static_cast<std::size_t>(t) * n;
   float v = partials[i];
   for (int s = 1; s < splits; ++s)
     v += partials[s * count + i];
-  if (accumulate != 0)
-    v = y[i] + v;
-  if (windowed) {
-    const int row = i / n;
-    const int column = i % n;
-    const int channel = column % unit.channels;
-    if (unit.bias != nullptr)
-      v += unit.bias[channel];
-    if (block_input) {
-      // The output is [frames][channels]: frame row, channel column.
-      const float u = Snake(v * unit.scale[channel] + unit.shift[channel], unit.alpha[channel]);
-      const std::size_t c = static_cast<std::size_t>(unit.channels);
-      unit.window[static_cast<std::size_t>(row) * 2 * c + column] = u;
-      if (row + 1 < unit.frames)
-        unit.window[static_cast<std::size_t>(row + 1) * 2 * c + c + column] = u;
-    } else {
-      unit.window[unit.head + i] = Snake(v, unit.alpha[channel]);
-    }
-  }
+  const int channel = (i % n) % unit.channels;
+  if (unit.bias != nullptr)
+    v += unit.bias[channel];
+  unit.window[unit.head + i] = Snake(v, unit.alpha[channel]);
   y[i] = v;
 }
 
@@ -1037,14 +1018,16 @@ struct vx_vae {
     // where block 1's units (96 tiles) measured 5.6-5.8 -> 6.2-6.4 us.
     const std::size_t tiles = ((n + kTileRows - 1) / kTileRows) * ((t + kTileRows - 1) / kTileRows);
     const bool tiled = dw == nullptr && t > 32 && tiles >= 192;
-    // A product of at most 32 rows whose 16-column workgroups would not
-    // fill the compute units, over k of at least kSplitK, splits k over
-    // the tile kernel's 32 x 32 tiles instead (each split reading x once
-    // per 32 columns), up to kMaxSplits and 384 workgroups, and a second
-    // launch adds the splits.
+    // A product of at most 32 rows into a residual unit's window (no
+    // accumulation) whose 16-column workgroups would not fill the compute
+    // units, over k of at least kSplitK, splits k over the tile kernel's
+    // 32 x 32 tiles instead (each split reading x once per 32 columns), up
+    // to kMaxSplits and 384 workgroups, and a second launch adds the
+    // splits and applies the epilogue.
     const std::size_t column_tiles16 = (n + 15) / 16;
     std::size_t splits = 1;
-    if (dw == nullptr && t <= 32 && column_tiles16 < 256 && k >= kSplitK)
+    const bool window_only = unit.window != nullptr && unit.scale == nullptr && !accumulate;
+    if (dw == nullptr && window_only && t <= 32 && column_tiles16 < 256 && k >= kSplitK)
       while (splits < kMaxSplits && tiles * 2 * splits <= 384 && k / (2 * splits) >= 256)
         splits *= 2;
     if (Skinny(t, k, n) && !tiled && splits == 1) {
@@ -1134,7 +1117,7 @@ struct vx_vae {
                                                      UnitWindow{});
     SplitSumKernel<<<Blocks(std::max(t * n, static_cast<std::size_t>(unit.head))), kThreads, 0,
                      stream>>>(partials, static_cast<int>(splits), y, static_cast<int>(t),
-                               static_cast<int>(n), accumulate ? 1 : 0, unit);
+                               static_cast<int>(n), unit);
     return VX_OK;
   }
 
