@@ -654,7 +654,7 @@ constexpr int kTileDepth = 2;
 // k splits of a few-row tile product: two (four measured 0.6 us slower per
 // patch, eight 3 us).
 constexpr std::size_t kMaxSplits = 2;
-constexpr std::size_t kSplitK = 2048;     // least k that splits
+constexpr std::size_t kSplitK = 2048;  // least k that splits
 
 __global__ __launch_bounds__(kTileThreads) void F32TileKernel(const float* x, const float* w, float* y,
                                                      int t, int k, int n, int accumulate,
