@@ -26,16 +26,21 @@ BOUND = 2e-3
 # of 1, 5 and 2 frames at the VoxCPM2 shape take one- and two-tile row
 # blocks and latents' histories that mix the previous chunk's rows with
 # this chunk's (fewer than 6 frames).
+# "split": a transposed convolution of k = 2080 over 1560 columns at a
+# few rows splits k over 32 x 32 tiles (the last column tile partial) and a
+# second launch adds the splits; its 520-channel units take depthwise
+# launches and the LDS-tiled kernel (520 is not a multiple of 16).
 CONFIGS = {
     "small": synth.VaeConfig(latent=16, decoder_dim=64, rates=(3, 2, 2)),
     "odd": synth.VaeConfig(latent=16, decoder_dim=48, rates=(2, 2)),
+    "split": synth.VaeConfig(latent=16, decoder_dim=1040, rates=(3,)),
     "voxcpm2": synth.VOXCPM2_VAE,
 }
 
 
 @pytest.mark.parametrize("name,chunks", [("small", (4, 4, 1)), ("small", (9,)),
-                                         ("odd", (3, 2, 5)), ("voxcpm2", (4, 4)),
-                                         ("voxcpm2", (1, 5, 2))])
+                                         ("odd", (3, 2, 5)), ("split", (4, 3, 1)),
+                                         ("voxcpm2", (4, 4)), ("voxcpm2", (1, 5, 2))])
 def test_vae_streaming_decode_against_oracle(vx, oracle, cuda, stream, name, chunks):
     config = CONFIGS[name]
     weights = synth.vae_weights(config, 91)
